@@ -1,0 +1,190 @@
+"""Benchmark: StrasGPT transformer forward pass on one MI355X.
+
+Workload (one "step" = one full greedy generation, KV cache reset first):
+the Qwen3-4B-shaped decoder (d 2560, FFN 9728, 36 layers, 32/8 heads of
+128, QK RMSNorm, vocab 151936, tied; random-init bf16 N(0, 0.02) weights,
+norm weights 1.0), a 512-token uniform-random prompt, then 128 greedy decode
+tokens. Weights are read from a seeded synthetic safetensors directory and
+are HBM-resident before the timed region.
+
+value = decode tokens/s (decode_count / sum of decode time over the timed
+steps); prefill tokens/s is reported beside it (prompt tokens / prefill
+time). The roofline object describes the dominant decode kernel (largest
+share of event-measured decode time), timed with HIP events on the
+library's stream in an eager profiling pass of the same workload; the
+cpu_baseline is the oracle (C + OpenMP restatement of the reference
+forward pass) timed on a bounded sample of the same model on the host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_path(name, seed):
+    base = "/dev/shm" if os.access("/dev/shm", os.W_OK) else "/tmp"
+    return os.path.join(base, f"strasgpt_bench_{name}_{seed}")
+
+
+def ensure_model(shp, seed):
+    from strasgpt_amd import synth
+    d = model_path(shp.name, seed)
+    if not os.path.exists(os.path.join(d, "config.json")):
+        t0 = time.time()
+        synth.write_model(shp, d, seed=seed)
+        log(f"wrote {shp.name} ({shp.weight_bytes() / 1e9:.2f} GB) in {time.time() - t0:.1f}s")
+    return d
+
+
+def cpu_baseline(d, shp, prompt, threads, decode_tokens):
+    """Oracle on the host cores: a short prefill then `decode_tokens` steps."""
+    from oracle import oracle as orc
+    t0 = time.time()
+    om = orc.OracleModel(d, threads=threads)
+    log(f"cpu baseline: oracle loaded in {time.time() - t0:.1f}s ({threads} threads)")
+    sample_prompt = prompt[:16]
+    t0 = time.time()
+    logits = om.predict(sample_prompt)
+    t_prefill = time.time() - t0
+    nxt = int(logits[0].argmax())
+    t0 = time.time()
+    for _ in range(decode_tokens):
+        nxt = int(om.predict([nxt])[0].argmax())
+    t_decode = time.time() - t0
+    om.close()
+    return {
+        "value": decode_tokens / t_decode, "unit": "tok/s", "cores": threads, "kind": "port",
+        "prefill_tok_s": len(sample_prompt) / t_prefill,
+        "sample": (f"{shp.name}: {len(sample_prompt)}-token prefill then {decode_tokens} "
+                   f"greedy decode steps, oracle/oracle.c (OpenMP, {threads} threads)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="qwen3-4b")
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-decode-tokens", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--precision", type=int, default=0, help="prefill GEMM: 0 bf16x2, 1 bf16")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU runs are "
+                                   "not part of it (run with --gpus 1)"}))
+        sys.exit(2)
+
+    from strasgpt_amd import runtime, synth
+    shp = synth.shape(args.config)
+    d = ensure_model(shp, args.seed)
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, 42)
+    steps_per_gen = shp.decode_len + 1
+
+    t0 = time.time()
+    t = runtime.Transformer(d)
+    t.set_prefill_precision(args.precision)
+    log(f"loaded into HBM in {time.time() - t0:.1f}s; {runtime.version()}")
+
+    for i in range(args.warmup):
+        t.reset()
+        t.generate(prompt, steps_per_gen)
+        log(f"warmup {i + 1}/{args.warmup} done")
+
+    prefill_s = decode_s = 0.0
+    decode_n = 0
+    tokens = None
+    t_start = time.perf_counter()
+    for i in range(args.steps):
+        t.reset()
+        tokens, tm = t.generate(prompt, steps_per_gen)  # synchronous
+        prefill_s += tm.prefill_s
+        decode_s += tm.decode_s
+        decode_n += tm.decode_count
+        log(f"step {i + 1}/{args.steps}: prefill {tm.prefill_s * 1e3:.1f} ms, "
+            f"decode {tm.decode_count} tok in {tm.decode_s * 1e3:.1f} ms")
+    wall = time.perf_counter() - t_start
+
+    # Eager profiling pass of the same workload: per-kernel event timing.
+    t.reset()
+    t.profile(True)
+    t.generate(prompt, steps_per_gen)
+    stats = t.profile_read()
+    t.profile(False)
+    t.close()
+
+    decode_kernels = ["qkv_gemv", "attention_decode", "o_gemv", "gate_up_gemv", "down_gemv",
+                      "logits_gemv", "argmax", "moe_route", "moe_gate_up", "moe_down"]
+    prefill_kernels = ["qkv_gemm", "o_gemm", "gate_up_gemm", "down_gemm"]
+    kernels = {}
+    for k, v in stats.items():
+        avg_ms = v["total_ms"] / v["launches"]
+        e = {"launches": v["launches"], "avg_us": avg_ms * 1e3,
+             "bytes_per_launch": v["bytes"] / v["launches"],
+             "flop_per_launch": v["flops"] / v["launches"]}
+        e["gbs"] = v["bytes"] / (v["total_ms"] * 1e-3) / 1e9 if v["total_ms"] else 0.0
+        e["tflops"] = v["flops"] / (v["total_ms"] * 1e-3) / 1e12 if v["total_ms"] else 0.0
+        kernels[k] = e
+    dec = {k: stats[k] for k in decode_kernels if k in stats}
+    dom = max(dec, key=lambda k: dec[k]["total_ms"])
+    kd = kernels[dom]
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(kd["gbs"], 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kd["gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": None, "avg_us": round(kd["avg_us"], 2),
+                "bytes_per_launch": kd["bytes_per_launch"]}
+    pre = {k: stats[k] for k in prefill_kernels if k in stats}
+    roofline_prefill = None
+    if pre:
+        flops = sum(v["flops"] for v in pre.values())
+        ms = sum(v["total_ms"] for v in pre.values())
+        tf = flops / (ms * 1e-3) / 1e12
+        roofline_prefill = {"kernels": sorted(pre), "bound": "mfma", "achieved": round(tf, 1),
+                            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                            "precision": "bf16x2" if args.precision == 0 else "bf16"}
+    decode_tok_s = decode_n / decode_s
+    prefill_tok_s = args.steps * len(prompt) / prefill_s
+    decode_bytes = sum(v["bytes"] for k, v in stats.items() if k in decode_kernels)
+    decode_ms = sum(v["total_ms"] for k, v in stats.items() if k in decode_kernels)
+    ntok = steps_per_gen - 1
+    out = {
+        "metric": "decode tok/s @batch1 + prefill tok/s; % of HBM BW / MFMA peak",
+        "value": round(decode_tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 weights, fp32 activations",
+        "data": "synthetic (seeded random-init weights, uniform-random prompt ids)",
+        "config": {"workload": f"{shp.name}-shaped decoder: {shp.prompt_len}-token prefill + "
+                               f"{shp.decode_len} greedy decode tokens, batch 1",
+                   "global_batch": 1, "seq_len": shp.prompt_len + shp.decode_len,
+                   "parallelism": "single GPU"},
+        "prefill_tok_s": round(prefill_tok_s, 1),
+        "decode_ms_per_token": round(decode_s / decode_n * 1e3, 4),
+        "decode_effective_gbs": round(decode_bytes / ntok / (decode_s / decode_n) / 1e9, 1),
+        "decode_kernel_busy_frac": round(decode_ms / 1e3 / (decode_s / args.steps), 3),
+        "roofline": roofline,
+        "roofline_prefill": roofline_prefill,
+        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
+                        for kk, vv in v.items()} for k, v in kernels.items()},
+        "tokens_head": tokens[:8],
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(d, shp, prompt, args.cpu_threads, args.cpu_decode_tokens)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

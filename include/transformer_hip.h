@@ -1,0 +1,105 @@
+/*
+ * Extensions of the StrasGPT C API that have no single reference entry
+ * point. Each one names the reference code it stands in for.
+ */
+#ifndef TRANSFORMER_HIP_H
+# define TRANSFORMER_HIP_H
+
+#include "transformer.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Greedy next-token selection on the device: transformer_predict with
+ * logits_count = 1 followed by the reference's sample_argmax (first index
+ * of the maximum, reference source/sampler.c:92-102) without copying the
+ * logits to the host. Returns the token id. */
+int transformer_predict_argmax(
+    transformer_t* transformer, size_t token_count, const int* token
+);
+
+typedef struct transformer_timing {
+  double prefill_s; /* first transformer_predict over the prompt */
+  double decode_s;  /* sum of the single-token steps */
+  size_t decode_count;
+} transformer_timing_t;
+
+/* The reference driver's greedy loop (source/strasgpt.c:206-252 with
+ * --temp 0): one prefill over the prompt, then step_count - 1 single-token
+ * steps, each feeding back the argmax. The loop stays on the device: the
+ * next token never leaves HBM between steps (decode steps are replayed
+ * from a captured HIP graph). Writes step_count token ids to out. Stops
+ * early (like the reference) when eos_token_id >= 0 is produced; returns
+ * the number of ids written. timing may be NULL. */
+size_t transformer_generate_greedy(
+    transformer_t* transformer,
+    size_t token_count,
+    const int* token,
+    size_t step_count,
+    int eos_token_id,
+    int* out,
+    transformer_timing_t* timing
+);
+
+/* Forget the KV cache (cached_count = 0) so that one loaded model can
+ * serve another sequence. The reference has no reset: it builds a new
+ * transformer_t per sequence. */
+void transformer_reset(transformer_t* transformer);
+
+/* Parity hook: when out is not NULL, the next transformer_predict copies
+ * the residual stream after every layer into out as
+ * [layer_count][token_count][embedding_dim] fp32 (the reference's
+ * embedding[t][e] after source/transformer.c:1498-1504), and the
+ * final-RMSNorm output into out_final as [token_count][embedding_dim]
+ * (source/transformer.c:1580-1590). The hook covers one call of at most
+ * TRANSFORMER_CHUNK_MAX_LEN tokens and is then cleared. */
+void transformer_capture_hidden(
+    transformer_t* transformer, float* out, float* out_final
+);
+
+/* GEMM arithmetic for prefill chunks longer than the GEMV threshold.
+ * 0: bf16x2 (fp32 activations split into two bf16 terms; products exact,
+ *    fp32 accumulate: matches the fp32 reference to fp32 rounding noise),
+ * 1: bf16 (activations rounded once to bf16: twice the MFMA rate, logits
+ *    move by about 1e-3 so greedy tokens can differ from the reference).
+ * Returns the previous mode. */
+int transformer_set_prefill_precision(transformer_t* transformer, int mode);
+
+/* Measurement hooks (no reference counterpart; the reference only times
+ * whole predict calls, source/strasgpt.c:206-274). While enabled, every
+ * kernel launch of the forward pass is bracketed by HIP events on the
+ * library's stream and the decode loop of transformer_generate_greedy runs
+ * eagerly instead of replaying its graph. Statistics accumulate per kernel
+ * class until profiling is enabled again (which clears them). Algorithmic
+ * bytes and FLOP are the work the kernel's inputs define, not counters. */
+enum transformer_kernel_class {
+  TRANSFORMER_K_QKV_GEMV, TRANSFORMER_K_ATTENTION_DECODE, TRANSFORMER_K_O_GEMV,
+  TRANSFORMER_K_GATE_UP_GEMV, TRANSFORMER_K_DOWN_GEMV, TRANSFORMER_K_LOGITS_GEMV,
+  TRANSFORMER_K_ARGMAX, TRANSFORMER_K_MOE_ROUTE, TRANSFORMER_K_MOE_GATE_UP,
+  TRANSFORMER_K_MOE_DOWN, TRANSFORMER_K_QKV_GEMM, TRANSFORMER_K_ATTENTION_PREFILL,
+  TRANSFORMER_K_O_GEMM, TRANSFORMER_K_GATE_UP_GEMM, TRANSFORMER_K_DOWN_GEMM,
+  TRANSFORMER_K_ELEMENTWISE, TRANSFORMER_K_CLASS_COUNT
+};
+
+typedef struct transformer_kernel_stat {
+  size_t launches;
+  double total_ms; /* sum of event-measured launch durations */
+  double bytes;    /* algorithmic HBM bytes, summed over launches */
+  double flops;    /* algorithmic FLOP, summed over launches */
+} transformer_kernel_stat_t;
+
+void transformer_profile(transformer_t* transformer, int enable);
+/* Returns 0, or -1 for an unknown kernel class. */
+int transformer_profile_read(
+    transformer_t* transformer, int kernel_class, transformer_kernel_stat_t* out
+);
+
+/* Library build identification (gfx target, kernel variants). */
+const char* transformer_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRANSFORMER_HIP_H */

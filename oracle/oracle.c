@@ -1,0 +1,511 @@
+/*
+ * ORACLE — test infrastructure, not part of the product. See oracle.h.
+ *
+ * CPU restatement of the StrasGPT reference forward pass
+ * (source/transformer.c), threaded with OpenMP. Compiled without
+ * -ffast-math and with -ffp-contract=off, so the arithmetic is exactly what
+ * is written here: fmaf() where the reference's AVX2 dot product issues
+ * FMAs, plain sequential fp32 sums elsewhere.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <omp.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+struct oracle_model {
+  oracle_config_t c;
+  size_t per_layer[ORACLE_CLASS_COUNT]; /* elements (bf16) or bytes (u8) */
+  void* w[ORACLE_CLASS_COUNT];
+  unsigned char* loaded[ORACLE_CLASS_COUNT];
+  /* chunk activations */
+  float *x, *xn, *q, *att, *g, *u, *tmp;
+  /* KV cache [L][kvh][ctx][hd] and RoPE table [ctx][hd] */
+  float *kc, *vc, *rope;
+  size_t cached;
+  float *cap, *cap_final;
+};
+
+/* ------------------------------------------------------------------------ */
+/* Primitives                                                                */
+
+/* Reference include/util.h:33-39: the bf16 bits are the top half of the
+ * fp32 bits. */
+static inline float bf16f(uint16_t w) {
+  uint32_t u = (uint32_t)w << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+float oracle_bf16_to_f32(uint16_t w) { return bf16f(w); }
+
+/* OCP Microscaling v1.0: E2M1 element (sign, 2-bit exponent, 1-bit
+ * mantissa) times an E8M0 scale 2^(s-127); s = 255 encodes NaN. No
+ * reference counterpart. */
+float oracle_mxfp4_value(uint8_t code, uint8_t scale) {
+  static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  if (scale == 255) return NAN;
+  float v = ldexpf(mag[code & 7], (int)scale - 127);
+  return (code & 8) ? -v : v;
+}
+
+void oracle_mxfp4_dequant(const uint8_t* blocks, const uint8_t* scales,
+                          size_t value_count, float* out) {
+  for (size_t i = 0; i < value_count; i++) {
+    uint8_t byte = blocks[i / 2];
+    uint8_t code = (i & 1) ? (byte >> 4) : (byte & 15);
+    out[i] = oracle_mxfp4_value(code, scales[i / 32]);
+  }
+}
+
+/* Reference dot() AVX2 variant (source/transformer.c:1095-1167): element i
+ * feeds accumulator lane i%8 of accumulator (i/8)%4 with an FMA; the four
+ * 8-lane accumulators are summed as (a0+a1)+(a2+a3), then lanes l and l+4,
+ * then ((s0+s1)+(s2+s3)). len is a multiple of 32. */
+static inline float reduce_4x8(float acc[4][8]) {
+  float v[8];
+  for (int l = 0; l < 8; l++) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+  float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+  return (s0 + s1) + (s2 + s3);
+}
+
+float oracle_dot_bf16(size_t len, const float* a, const uint16_t* w) {
+  float acc[4][8] = {{0}};
+  for (size_t i = 0; i < len; i += 32) {
+    for (int j = 0; j < 4; j++) {
+      for (int l = 0; l < 8; l++) {
+        size_t k = i + 8 * (size_t)j + (size_t)l;
+        acc[j][l] = fmaf(a[k], bf16f(w[k]), acc[j][l]);
+      }
+    }
+  }
+  return reduce_4x8(acc);
+}
+
+/* Same accumulation order with fp32 weights (dequantised MXFP4 rows). */
+static float dot_f32(size_t len, const float* a, const float* w) {
+  float acc[4][8] = {{0}};
+  for (size_t i = 0; i < len; i += 32) {
+    for (int j = 0; j < 4; j++) {
+      for (int l = 0; l < 8; l++) {
+        size_t k = i + 8 * (size_t)j + (size_t)l;
+        acc[j][l] = fmaf(a[k], w[k], acc[j][l]);
+      }
+    }
+  }
+  return reduce_4x8(acc);
+}
+
+/* Reference rmsnorm (source/transformer.c:978-999): ss = sum x^2 (fp32,
+ * in index order), ss /= n, s = (float)(1.0 / sqrtf(ss + eps)),
+ * y = (x * s) * w. y may alias x. */
+void oracle_rmsnorm(size_t n, float* y, const float* x, const uint16_t* w, float eps) {
+  float ss = 0.0f;
+  for (size_t j = 0; j < n; j++) ss = fmaf(x[j], x[j], ss);
+  ss /= (float)n;
+  ss = (float)(1.0 / (double)sqrtf(ss + eps));
+  for (size_t j = 0; j < n; j++) y[j] = (x[j] * ss) * bf16f(w[j]);
+}
+
+/* Reference state_from_safetensors RoPE table (source/transformer.c:126-146):
+ * freq = 1 / theta^((coef*j)/hd), angle = pos * freq, cos at j, sin at
+ * j + offset. Half-split: j < hd/2 step 1, offset hd/2, coef 2.
+ * Interleaved: j < hd step 2, offset 1, coef 1. */
+void oracle_rope_table(size_t ctx, size_t hd, float theta, int interleaved, float* out) {
+  size_t bound = interleaved ? hd : hd / 2;
+  size_t offset = interleaved ? 1 : hd / 2;
+  size_t stride = interleaved ? 2 : 1;
+  float coef = interleaved ? 1.0f : 2.0f;
+  for (size_t i = 0; i < ctx; i++) {
+    for (size_t j = 0; j < bound; j += stride) {
+      float freq = 1.0f / powf(theta, (coef * (float)j) / (float)hd);
+      float val = (float)i * freq;
+      out[i * hd + j] = cosf(val);
+      out[i * hd + j + offset] = sinf(val);
+    }
+  }
+}
+
+static void rope_apply(size_t hd, int interleaved, float* v, const float* cs) {
+  size_t bound = interleaved ? hd : hd / 2;
+  size_t offset = interleaved ? 1 : hd / 2;
+  size_t stride = interleaved ? 2 : 1;
+  for (size_t h = 0; h < bound; h += stride) {
+    float fr = cs[h], fi = cs[h + offset];
+    float v0 = v[h], v1 = v[h + offset];
+    v[h] = v0 * fr - v1 * fi;
+    v[h + offset] = v0 * fi + v1 * fr;
+  }
+}
+
+/* Reference attention for one (head, token) (source/transformer.c:1383-1419):
+ * scores q.k / sqrtf(hd) with the dot summed over h in order, softmax with
+ * max subtraction, expf, sequential sum and division, then
+ * out[h] = sum over s (in order) of p[s] * v[s][h]. */
+void oracle_attention_row(size_t hd, size_t count, const float* q, const float* k,
+                          const float* v, float* out) {
+  float* p = malloc(count * sizeof(float));
+  float scale = sqrtf((float)hd);
+  for (size_t s = 0; s < count; s++) {
+    float acc = 0.0f;
+    for (size_t h = 0; h < hd; h++) acc = fmaf(q[h], k[s * hd + h], acc);
+    p[s] = acc / scale;
+  }
+  float mx = p[0];
+  for (size_t s = 1; s < count; s++) mx = p[s] > mx ? p[s] : mx;
+  float sum = 0.0f;
+  for (size_t s = 0; s < count; s++) {
+    p[s] = expf(p[s] - mx);
+    sum += p[s];
+  }
+  for (size_t s = 0; s < count; s++) p[s] /= sum;
+  for (size_t h = 0; h < hd; h++) out[h] = 0.0f;
+  for (size_t s = 0; s < count; s++) {
+    for (size_t h = 0; h < hd; h++) out[h] = fmaf(p[s], v[s * hd + h], out[h]);
+  }
+  free(p);
+}
+
+/* Reference sample_argmax (source/sampler.c:92-102): first index holding
+ * the strict maximum. */
+size_t oracle_argmax(const float* x, size_t n) {
+  size_t best = 0;
+  float bv = x[0];
+  for (size_t i = 1; i < n; i++) {
+    if (x[i] > bv) {
+      best = i;
+      bv = x[i];
+    }
+  }
+  return best;
+}
+
+/* MoE router (no reference counterpart): the k largest logits in
+ * descending order, ties to the lowest index, then softmax over those k
+ * with max subtraction, expf and a sequential sum. */
+void oracle_topk_softmax(size_t n, const float* logits, size_t k, int* index, float* weight) {
+  unsigned char taken[1024] = {0};
+  for (size_t j = 0; j < k; j++) {
+    int best = -1;
+    for (size_t e = 0; e < n; e++) {
+      if (taken[e]) continue;
+      if (best < 0 || logits[e] > logits[best]) best = (int)e;
+    }
+    taken[best] = 1;
+    index[j] = best;
+  }
+  float mx = logits[index[0]], sum = 0.0f;
+  for (size_t j = 0; j < k; j++) {
+    weight[j] = expf(logits[index[j]] - mx);
+    sum += weight[j];
+  }
+  for (size_t j = 0; j < k; j++) weight[j] /= sum;
+}
+
+static inline float silu_mul(float g, float u) {
+  /* Reference source/transformer.c:1477-1486. */
+  g *= 1.0f / (1.0f + expf(-g));
+  return g * u;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Model                                                                     */
+
+static int is_u8(int cls) {
+  return cls >= ORACLE_GATE_BLOCKS && cls <= ORACLE_DOWN_SCALES;
+}
+
+oracle_model_t* oracle_create(const oracle_config_t* cfg) {
+  oracle_model_t* m = calloc(1, sizeof(*m));
+  m->c = *cfg;
+  const oracle_config_t* c = &m->c;
+  size_t d = c->embedding_dim, hd = c->head_dim, H = c->hidden_dim, E = c->expert_count;
+  size_t* p = m->per_layer;
+  p[ORACLE_EMBEDDING] = c->vocabulary_len * d;
+  p[ORACLE_MHA_NORM] = d;
+  p[ORACLE_Q] = c->q_head_count * hd * d;
+  p[ORACLE_Q_NORM] = c->qk_norm ? hd : 0;
+  p[ORACLE_K] = c->kv_head_count * hd * d;
+  p[ORACLE_K_NORM] = c->qk_norm ? hd : 0;
+  p[ORACLE_V] = c->kv_head_count * hd * d;
+  p[ORACLE_O] = d * c->q_head_count * hd;
+  p[ORACLE_FFN_NORM] = d;
+  p[ORACLE_GATE] = E ? 0 : H * d;
+  p[ORACLE_UP] = E ? 0 : H * d;
+  p[ORACLE_DOWN] = E ? 0 : d * H;
+  p[ORACLE_OUT_NORM] = d;
+  p[ORACLE_OUT] = c->tied ? 0 : c->vocabulary_len * d;
+  p[ORACLE_ROUTER] = E * d;
+  p[ORACLE_GATE_BLOCKS] = E * H * d / 2;
+  p[ORACLE_GATE_SCALES] = E * H * d / 32;
+  p[ORACLE_UP_BLOCKS] = E * H * d / 2;
+  p[ORACLE_UP_SCALES] = E * H * d / 32;
+  p[ORACLE_DOWN_BLOCKS] = E * d * H / 2;
+  p[ORACLE_DOWN_SCALES] = E * d * H / 32;
+  for (int k = 0; k < ORACLE_CLASS_COUNT; k++) {
+    if (!p[k]) continue;
+    size_t layers = (k == ORACLE_EMBEDDING || k == ORACLE_OUT_NORM || k == ORACLE_OUT)
+                        ? 1 : c->layer_count;
+    size_t bytes = p[k] * layers * (is_u8(k) ? 1 : 2);
+    m->w[k] = malloc(bytes);
+    m->loaded[k] = calloc(layers, 1);
+    if (!m->w[k] || !m->loaded[k]) {
+      oracle_free(m);
+      return NULL;
+    }
+  }
+  size_t T = ORACLE_CHUNK_MAX_LEN, qd = c->q_head_count * hd;
+  size_t hid = H > d ? H : d;
+  m->x = malloc(T * d * sizeof(float));
+  m->xn = malloc(T * d * sizeof(float));
+  m->q = malloc(T * qd * sizeof(float));
+  m->att = malloc(T * qd * sizeof(float));
+  m->g = malloc(T * hid * sizeof(float));
+  m->u = malloc(T * hid * sizeof(float));
+  m->tmp = malloc(T * d * sizeof(float));
+  size_t cache = c->layer_count * c->kv_head_count * c->context_len * hd;
+  m->kc = calloc(cache, sizeof(float));
+  m->vc = calloc(cache, sizeof(float));
+  m->rope = malloc(c->context_len * hd * sizeof(float));
+  if (!m->x || !m->xn || !m->q || !m->att || !m->g || !m->u || !m->tmp ||
+      !m->kc || !m->vc || !m->rope) {
+    oracle_free(m);
+    return NULL;
+  }
+  oracle_rope_table(c->context_len, hd, c->rope_theta, c->rope_interleaved, m->rope);
+  return m;
+}
+
+int oracle_load_tensor(oracle_model_t* m, int cls, size_t layer, const char* file,
+                       size_t offset, size_t size) {
+  if (cls < 0 || cls >= ORACLE_CLASS_COUNT || !m->w[cls]) return -1;
+  size_t esz = is_u8(cls) ? 1 : 2;
+  if (size != m->per_layer[cls] * esz) return -1;
+  size_t layers = (cls == ORACLE_EMBEDDING || cls == ORACLE_OUT_NORM || cls == ORACLE_OUT)
+                      ? 1 : m->c.layer_count;
+  if (layer >= layers) return -1;
+  FILE* f = fopen(file, "rb");
+  if (!f) return -1;
+  int rc = 0;
+  if (fseek(f, (long)offset, SEEK_SET) != 0 ||
+      fread((char*)m->w[cls] + layer * size, 1, size, f) != size)
+    rc = -1;
+  fclose(f);
+  if (rc == 0) m->loaded[cls][layer] = 1;
+  return rc;
+}
+
+int oracle_finalize(oracle_model_t* m) {
+  int missing = 0;
+  for (int k = 0; k < ORACLE_CLASS_COUNT; k++) {
+    if (!m->w[k]) continue;
+    size_t layers = (k == ORACLE_EMBEDDING || k == ORACLE_OUT_NORM || k == ORACLE_OUT)
+                        ? 1 : m->c.layer_count;
+    for (size_t l = 0; l < layers; l++) missing += !m->loaded[k][l];
+  }
+  return missing;
+}
+
+void oracle_free(oracle_model_t* m) {
+  if (!m) return;
+  for (int k = 0; k < ORACLE_CLASS_COUNT; k++) {
+    free(m->w[k]);
+    free(m->loaded[k]);
+  }
+  free(m->x); free(m->xn); free(m->q); free(m->att); free(m->g); free(m->u);
+  free(m->tmp); free(m->kc); free(m->vc); free(m->rope);
+  free(m);
+}
+
+void oracle_reset(oracle_model_t* m) { m->cached = 0; }
+size_t oracle_cached_count(const oracle_model_t* m) { return m->cached; }
+void oracle_set_threads(int n) { if (n > 0) omp_set_num_threads(n); }
+
+void oracle_capture_hidden(oracle_model_t* m, float* out, float* out_final) {
+  m->cap = out;
+  m->cap_final = out_final;
+}
+
+static const uint16_t* W(const oracle_model_t* m, int cls, size_t layer) {
+  return (const uint16_t*)m->w[cls] + layer * m->per_layer[cls];
+}
+
+/* Expert FFN of one token: reference SwiGLU FFN (source/transformer.c:
+ * 1461-1504) with MXFP4 weights, per selected expert, accumulated as
+ * acc = fmaf(weight_j, expert_j(x), acc) in top-k order. */
+static void moe_token(const oracle_model_t* m, size_t l, const float* xn, float* out) {
+  const oracle_config_t* c = &m->c;
+  size_t d = c->embedding_dim, H = c->hidden_dim, E = c->expert_count, K = c->expert_used_count;
+  float logits[1024];
+  int sel[64];
+  float wsel[64];
+  for (size_t e = 0; e < E; e++) logits[e] = oracle_dot_bf16(d, xn, W(m, ORACLE_ROUTER, l) + e * d);
+  oracle_topk_softmax(E, logits, K, sel, wsel);
+  float* a = malloc(H * sizeof(float));
+  float* row = malloc((H > d ? H : d) * sizeof(float));
+  for (size_t e = 0; e < d; e++) out[e] = 0.0f;
+  const uint8_t* gb = (const uint8_t*)m->w[ORACLE_GATE_BLOCKS] + l * m->per_layer[ORACLE_GATE_BLOCKS];
+  const uint8_t* gs = (const uint8_t*)m->w[ORACLE_GATE_SCALES] + l * m->per_layer[ORACLE_GATE_SCALES];
+  const uint8_t* ub = (const uint8_t*)m->w[ORACLE_UP_BLOCKS] + l * m->per_layer[ORACLE_UP_BLOCKS];
+  const uint8_t* us = (const uint8_t*)m->w[ORACLE_UP_SCALES] + l * m->per_layer[ORACLE_UP_SCALES];
+  const uint8_t* db = (const uint8_t*)m->w[ORACLE_DOWN_BLOCKS] + l * m->per_layer[ORACLE_DOWN_BLOCKS];
+  const uint8_t* ds = (const uint8_t*)m->w[ORACLE_DOWN_SCALES] + l * m->per_layer[ORACLE_DOWN_SCALES];
+  for (size_t j = 0; j < K; j++) {
+    size_t e = (size_t)sel[j];
+    for (size_t h = 0; h < H; h++) {
+      size_t r = e * H + h;
+      oracle_mxfp4_dequant(gb + r * d / 2, gs + r * d / 32, d, row);
+      float g = dot_f32(d, xn, row);
+      oracle_mxfp4_dequant(ub + r * d / 2, us + r * d / 32, d, row);
+      float u = dot_f32(d, xn, row);
+      a[h] = silu_mul(g, u);
+    }
+    for (size_t o = 0; o < d; o++) {
+      size_t r = e * d + o;
+      oracle_mxfp4_dequant(db + r * H / 2, ds + r * H / 32, H, row);
+      out[o] = fmaf(wsel[j], dot_f32(H, a, row), out[o]);
+    }
+  }
+  free(a);
+  free(row);
+}
+
+/* Reference transformer_predict_chunk (source/transformer.c:1186-1602). */
+static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc, float* logits,
+                          size_t cap_row, size_t cap_rows) {
+  const oracle_config_t* c = &m->c;
+  size_t d = c->embedding_dim, hd = c->head_dim, H = c->hidden_dim, L = c->layer_count;
+  size_t qh = c->q_head_count, kvh = c->kv_head_count, G = qh / kvh, ctx = c->context_len;
+  size_t qd = qh * hd, P = m->cached, V = c->vocabulary_len;
+  float eps = c->epsilon;
+  float *x = m->x, *xn = m->xn, *q = m->q, *att = m->att, *g = m->g, *u = m->u, *tmp = m->tmp;
+
+  for (size_t t = 0; t < T; t++)
+    for (size_t e = 0; e < d; e++)
+      x[t * d + e] = bf16f(W(m, ORACLE_EMBEDDING, 0)[(size_t)tok[t] * d + e]);
+
+  for (size_t l = 0; l < L; l++) {
+    float* kc = m->kc + l * kvh * ctx * hd;
+    float* vc = m->vc + l * kvh * ctx * hd;
+    #pragma omp parallel for schedule(static)
+    for (size_t t = 0; t < T; t++) oracle_rmsnorm(d, xn + t * d, x + t * d, W(m, ORACLE_MHA_NORM, l), eps);
+
+    /* K and V projections into the cache (source/transformer.c:1271-1291) */
+    #pragma omp parallel for schedule(static)
+    for (size_t r = 0; r < kvh * hd; r++) {
+      size_t head = r / hd, h = r % hd;
+      const uint16_t* wk = W(m, ORACLE_K, l) + r * d;
+      const uint16_t* wv = W(m, ORACLE_V, l) + r * d;
+      for (size_t t = 0; t < T; t++) {
+        kc[(head * ctx + P + t) * hd + h] = oracle_dot_bf16(d, xn + t * d, wk);
+        vc[(head * ctx + P + t) * hd + h] = oracle_dot_bf16(d, xn + t * d, wv);
+      }
+    }
+    /* K-norm and RoPE on the new keys (source/transformer.c:1293-1323) */
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (size_t head = 0; head < kvh; head++) {
+      for (size_t t = 0; t < T; t++) {
+        float* kr = kc + (head * ctx + P + t) * hd;
+        if (c->qk_norm) oracle_rmsnorm(hd, kr, kr, W(m, ORACLE_K_NORM, l), eps);
+        rope_apply(hd, c->rope_interleaved, kr, m->rope + (P + t) * hd);
+      }
+    }
+    /* Q projection, Q-norm, RoPE (source/transformer.c:1327-1373) */
+    #pragma omp parallel for schedule(static)
+    for (size_t r = 0; r < qd; r++) {
+      const uint16_t* wq = W(m, ORACLE_Q, l) + r * d;
+      for (size_t t = 0; t < T; t++) q[t * qd + r] = oracle_dot_bf16(d, xn + t * d, wq);
+    }
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (size_t head = 0; head < qh; head++) {
+      for (size_t t = 0; t < T; t++) {
+        float* qr = q + t * qd + head * hd;
+        if (c->qk_norm) oracle_rmsnorm(hd, qr, qr, W(m, ORACLE_Q_NORM, l), eps);
+        rope_apply(hd, c->rope_interleaved, qr, m->rope + (P + t) * hd);
+      }
+    }
+    /* Causal GQA attention (source/transformer.c:1375-1422) */
+    #pragma omp parallel for collapse(2) schedule(dynamic, 4)
+    for (size_t head = 0; head < qh; head++) {
+      for (size_t t = 0; t < T; t++) {
+        size_t kvhead = head / G;
+        oracle_attention_row(hd, P + t + 1, q + t * qd + head * hd, kc + kvhead * ctx * hd,
+                             vc + kvhead * ctx * hd, att + t * qd + head * hd);
+      }
+    }
+    /* Output projection + residual (source/transformer.c:1426-1445) */
+    #pragma omp parallel for schedule(static)
+    for (size_t e = 0; e < d; e++) {
+      const uint16_t* wo = W(m, ORACLE_O, l) + e * qd;
+      for (size_t t = 0; t < T; t++) tmp[t * d + e] = oracle_dot_bf16(qd, att + t * qd, wo);
+    }
+    for (size_t i = 0; i < T * d; i++) x[i] += tmp[i];
+
+    #pragma omp parallel for schedule(static)
+    for (size_t t = 0; t < T; t++) oracle_rmsnorm(d, xn + t * d, x + t * d, W(m, ORACLE_FFN_NORM, l), eps);
+
+    if (c->expert_count == 0) {
+      /* Gate, up, SwiGLU, down + residual (source/transformer.c:1461-1504) */
+      #pragma omp parallel for schedule(static)
+      for (size_t h = 0; h < H; h++) {
+        const uint16_t* wg = W(m, ORACLE_GATE, l) + h * d;
+        const uint16_t* wu = W(m, ORACLE_UP, l) + h * d;
+        for (size_t t = 0; t < T; t++) {
+          float gv = oracle_dot_bf16(d, xn + t * d, wg);
+          float uv = oracle_dot_bf16(d, xn + t * d, wu);
+          g[t * H + h] = silu_mul(gv, uv);
+        }
+      }
+      #pragma omp parallel for schedule(static)
+      for (size_t e = 0; e < d; e++) {
+        const uint16_t* wd = W(m, ORACLE_DOWN, l) + e * H;
+        for (size_t t = 0; t < T; t++) tmp[t * d + e] = oracle_dot_bf16(H, g + t * H, wd);
+      }
+    } else {
+      #pragma omp parallel for schedule(dynamic, 1)
+      for (size_t t = 0; t < T; t++) moe_token(m, l, xn + t * d, tmp + t * d);
+    }
+    for (size_t i = 0; i < T * d; i++) x[i] += tmp[i];
+    if (m->cap) memcpy(m->cap + (l * cap_rows + cap_row) * d, x, T * d * sizeof(float));
+  }
+  (void)u;
+
+  /* Final RMSNorm in place, classifier for the last lc rows
+   * (source/transformer.c:1580-1601) */
+  for (size_t t = 0; t < T; t++) oracle_rmsnorm(d, x + t * d, x + t * d, W(m, ORACLE_OUT_NORM, 0), eps);
+  if (m->cap_final) memcpy(m->cap_final + cap_row * d, x, T * d * sizeof(float));
+  const uint16_t* wout = c->tied ? W(m, ORACLE_EMBEDDING, 0) : W(m, ORACLE_OUT, 0);
+  #pragma omp parallel for schedule(static)
+  for (size_t v = 0; v < V; v++) {
+    for (size_t r = 0; r < lc; r++) {
+      logits[r * V + v] = oracle_dot_bf16(d, x + (T - lc + r) * d, wout + v * d);
+    }
+  }
+}
+
+/* Reference transformer_predict (source/transformer.c:1607-1727): chunks
+ * of at most 512 tokens, logits for the last min(lc, T) positions. */
+int oracle_predict(oracle_model_t* m, size_t T, const int* tok, size_t lc, float* logits) {
+  if (!m || !logits || T == 0 || lc == 0) return 0;
+  if (T + m->cached > m->c.context_len) return -1;
+  if (lc > T) lc = T;
+  size_t V = m->c.vocabulary_len, start = T - lc;
+  for (size_t t = 0; t < T; t += ORACLE_CHUNK_MAX_LEN) {
+    size_t n = T - t < ORACLE_CHUNK_MAX_LEN ? T - t : ORACLE_CHUNK_MAX_LEN;
+    size_t lo = t > start ? t : start, hi = t + n;
+    size_t clc = lo < hi ? hi - lo : 0;
+    float* out = logits + (lo - start) * V;
+    if (clc == 0) {
+      /* The chunk still runs its classifier loop over zero rows. */
+      out = logits;
+    }
+    predict_chunk(m, n, tok + t, clc, out, t, T);
+    m->cached += n;
+  }
+  m->cap = NULL;
+  m->cap_final = NULL;
+  return 0;
+}

@@ -1,0 +1,100 @@
+// Device helpers shared by the gfx950 kernels: bf16 / MXFP4 decoding,
+// wavefront (64-lane) reductions, vector types for 128-bit memory access.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define WAVE 64
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// bf16 bits are the upper half of the fp32 bits (reference
+// include/util.h:33-39): exact.
+__device__ __forceinline__ float bf16_lo(uint32_t packed) {
+  return __uint_as_float(packed << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t packed) {
+  return __uint_as_float(packed & 0xFFFF0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t w) {
+  return __uint_as_float((uint32_t)w << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (finite inputs).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// MXFP4 (OCP MX v1.0) E2M1 element: sign bit 3, exponent bits 2..1,
+// mantissa bit 0. Magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6 built directly as
+// fp32 bit patterns: exponent e >= 1 gives 2^(e-1) * (1 + m/2).
+__device__ __forceinline__ float e2m1_value(uint32_t code) {
+  const uint32_t e = (code >> 1) & 3u, m = code & 1u;
+  float v = e ? __uint_as_float(((126u + e) << 23) | (m << 22)) : (m ? 0.5f : 0.0f);
+  return (code & 8u) ? -v : v;
+}
+__device__ __forceinline__ float e8m0_scale(uint32_t s) {
+  // 2^(s-127) as an fp32 bit pattern; s = 0 gives 2^-127 (subnormal) and
+  // s = 255 is NaN.
+  if (s == 255u) return __uint_as_float(0x7FC00000u);
+  return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+}
+
+// 16-byte streaming load of weights that are read once per step.
+__device__ __forceinline__ uint4 load_nt_u4(const void* p) {
+  const uint4* q = (const uint4*)p;
+  uint4 r;
+  r.x = __builtin_nontemporal_load(&q->x);
+  r.y = __builtin_nontemporal_load(&q->y);
+  r.z = __builtin_nontemporal_load(&q->z);
+  r.w = __builtin_nontemporal_load(&q->w);
+  return r;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
+  return v;
+}
+
+// Sum over a power-of-two group of `width` lanes (aligned groups).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+// Block-wide sum for blockDim.x == NT (multiple of 64); `red` holds
+// NT/64 floats of shared memory. Every thread gets the result.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NT / WAVE; i++) s += red[i];
+  __syncthreads();
+  return s;
+}
+
+// RMSNorm scale exactly as the reference computes it from the sum of
+// squares (source/transformer.c:990-992): ss/n, then
+// (float)(1.0 / sqrtf(ss + eps)).
+__device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
+  ss /= (float)n;
+  return (float)(1.0 / (double)sqrtf(ss + eps));
+}

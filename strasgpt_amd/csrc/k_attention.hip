@@ -1,0 +1,329 @@
+// Causal GQA attention over the device fp32 KV cache
+// ([kv_heads][ctx][head_dim] per layer), reference
+// source/transformer.c:1375-1422: score = (q . k) / sqrtf(hd), softmax
+// with max subtraction and expf, out = sum_s p[s] v[s].
+//
+// Prefill: one block per (64-query tile, q head); key tiles of 64 staged in
+// LDS; 4x4 register-blocked fp32 scores, online softmax (running max and
+// sum per query row), P kept in LDS for the P.V product.
+//
+// Decode: split-K over the cached positions ("flash decoding"): one block
+// per (64-key chunk, q head) writes (max, sum, partial output); the last
+// block of a head to finish (device-scope counter) combines the chunks.
+// The block also applies this step's QK RMSNorm + RoPE to q and to the new
+// key (read raw from the QKV projection), and one block per KV head writes
+// the processed key into the cache.
+#include "device_common.h"
+#include "hip_check.h"
+#include "kernels.h"
+
+namespace sg {
+
+namespace {
+
+constexpr int BQ = 64, BKV = 64;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
+  constexpr int LD = HD + 4;
+  constexpr int DU = HD / 16;  // output dims per thread
+  __shared__ __attribute__((aligned(16))) float qs[BQ * LD];
+  __shared__ __attribute__((aligned(16))) float ks[BKV * LD];
+  __shared__ __attribute__((aligned(16))) float vs[BKV * LD];
+  __shared__ float ps[BQ * (BKV + 4)];
+
+  const int tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+  const int head = blockIdx.y, q0 = blockIdx.x * BQ;
+  const int G = p.q_heads / p.kv_heads, kvh = head / G;
+  const int P = *p.pos, T = p.T;
+  const int qd = p.q_heads * HD;
+  const float* kbase = p.kcache + (size_t)kvh * p.ctx * HD;
+  const float* vbase = p.vcache + (size_t)kvh * p.ctx * HD;
+  const float scale = sqrtf((float)HD);
+
+  for (int i = tid; i < BQ * HD / 4; i += 256) {
+    const int r = i / (HD / 4), c = (i % (HD / 4)) * 4;
+    const int t = q0 + r;
+    float4 v = t < T ? *(const float4*)(p.q + (size_t)t * qd + head * HD + c)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    *(float4*)&qs[r * LD + c] = v;
+  }
+
+  float m[4], l[4], o[4][DU];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    m[i] = -INFINITY;
+    l[i] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < DU; u++) o[i][u] = 0.0f;
+  }
+
+  const int kv_end = min(P + q0 + BQ, P + T);  // keys visible to this tile
+  for (int kv0 = 0; kv0 < kv_end; kv0 += BKV) {
+    __syncthreads();
+    for (int i = tid; i < BKV * HD / 4; i += 256) {
+      const int r = i / (HD / 4), c = (i % (HD / 4)) * 4;
+      const int s = kv0 + r;
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+      if (s < kv_end) {
+        kv = *(const float4*)(kbase + (size_t)s * HD + c);
+        vv = *(const float4*)(vbase + (size_t)s * HD + c);
+      }
+      *(float4*)&ks[r * LD + c] = kv;
+      *(float4*)&vs[r * LD + c] = vv;
+    }
+    __syncthreads();
+
+    float sc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) sc[i][j] = 0.0f;
+    for (int h = 0; h < HD; h += 4) {
+      float4 qv[4], kv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) qv[i] = *(const float4*)&qs[(ty * 4 + i) * LD + h];
+#pragma unroll
+      for (int j = 0; j < 4; j++) kv[j] = *(const float4*)&ks[(tx + 16 * j) * LD + h];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          float a = sc[i][j];
+          a = fmaf(qv[i].x, kv[j].x, a);
+          a = fmaf(qv[i].y, kv[j].y, a);
+          a = fmaf(qv[i].z, kv[j].z, a);
+          a = fmaf(qv[i].w, kv[j].w, a);
+          sc[i][j] = a;
+        }
+    }
+    float corr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int t = q0 + ty * 4 + i;
+      float rmax = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int s = kv0 + tx + 16 * j;
+        sc[i][j] = (s <= P + t && s < kv_end) ? sc[i][j] / scale : -INFINITY;
+        rmax = fmaxf(rmax, sc[i][j]);
+      }
+      rmax = fmaxf(rmax, __shfl_xor(rmax, 8, WAVE));
+      rmax = fmaxf(rmax, __shfl_xor(rmax, 4, WAVE));
+      rmax = fmaxf(rmax, __shfl_xor(rmax, 2, WAVE));
+      rmax = fmaxf(rmax, __shfl_xor(rmax, 1, WAVE));
+      const float mnew = fmaxf(m[i], rmax);
+      corr[i] = mnew == -INFINITY ? 1.0f : expf(m[i] - mnew);
+      float rsum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float pv = mnew == -INFINITY ? 0.0f : expf(sc[i][j] - mnew);
+        ps[(ty * 4 + i) * (BKV + 4) + tx + 16 * j] = pv;
+        rsum += pv;
+      }
+      rsum += __shfl_xor(rsum, 8, WAVE);
+      rsum += __shfl_xor(rsum, 4, WAVE);
+      rsum += __shfl_xor(rsum, 2, WAVE);
+      rsum += __shfl_xor(rsum, 1, WAVE);
+      l[i] = l[i] * corr[i] + rsum;
+      m[i] = mnew;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int u = 0; u < DU; u++) o[i][u] *= corr[i];
+    const int nk = min(BKV, kv_end - kv0);
+    for (int c = 0; c < nk; c++) {
+      float pv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) pv[i] = ps[(ty * 4 + i) * (BKV + 4) + c];
+#pragma unroll
+      for (int u = 0; u < DU; u++) {
+        const float vv = vs[c * LD + tx + 16 * u];
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i][u] = fmaf(pv[i], vv, o[i][u]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int t = q0 + ty * 4 + i;
+    if (t >= T) continue;
+#pragma unroll
+    for (int u = 0; u < DU; u++)
+      p.out[(size_t)t * qd + head * HD + tx + 16 * u] = o[i][u] / l[i];
+  }
+}
+
+// RMSNorm (optional) + RoPE of one head vector by one wavefront, result in
+// LDS `dst`. Same arithmetic as the reference (source/transformer.c:
+// 1293-1323).
+template <int HD>
+__device__ void norm_rope_wave(const float* src, const uint16_t* nw, float eps,
+                               const float* cs, int pb, int po, int pst, float* dst) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x % WAVE;
+  float ss = 0.0f;
+  for (int e = lane; e < HD; e += WAVE) {
+    const float x = src[e];
+    dst[e] = x;
+    ss = fmaf(x, x, ss);
+  }
+  ss = wave_sum(ss);
+  if (nw) {
+    const float s = rms_scale(ss, HD, eps);
+    for (int e = lane; e < HD; e += WAVE) dst[e] = (dst[e] * s) * bf16_to_f32(nw[e]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  float r0[4], r1[4];
+  int hh[4];
+  int cnt = 0;
+  for (int i = lane; i * pst < pb; i += WAVE) {
+    const int h = i * pst;
+    const float fr = cs[h], fi = cs[h + po];
+    const float v0 = dst[h], v1 = dst[h + po];
+    r0[cnt] = v0 * fr - v1 * fi;
+    r1[cnt] = v0 * fi + v1 * fr;
+    hh[cnt] = h;
+    cnt++;
+  }
+  __builtin_amdgcn_wave_barrier();
+  for (int c = 0; c < cnt; c++) {
+    dst[hh[c]] = r0[c];
+    dst[hh[c] + po] = r1[c];
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
+  constexpr int CH = 64;
+  __shared__ float qs[HD], kn[HD], sc[CH];
+  __shared__ float red[256 / HD > 0 ? 256 / HD : 1][HD];
+  __shared__ float stat[2];
+  __shared__ bool last;
+
+  const int split = blockIdx.x, head = blockIdx.y;
+  const int G = p.q_heads / p.kv_heads, kvh = head / G;
+  const int P = *p.pos, total = P + 1;
+  const int nsplit = (total + CH - 1) / CH;
+  if (split >= nsplit) return;
+  const int s0 = split * CH, s1 = min(s0 + CH, total);
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const float* cs = p.rope + (size_t)P * HD;
+  const bool has_new = s1 == total;
+
+  if (wave == 0)
+    norm_rope_wave<HD>(p.q + (size_t)head * HD, p.qn, p.eps, cs, p.pair_bound, p.pair_offset,
+                       p.pair_stride, qs);
+  if (wave == 1 && has_new)
+    norm_rope_wave<HD>(p.kraw + (size_t)kvh * HD, p.kn, p.eps, cs, p.pair_bound,
+                       p.pair_offset, p.pair_stride, kn);
+  __syncthreads();
+  const float* kbase = p.kcache + (size_t)kvh * p.ctx * HD;
+  const float* vbase = p.vcache + (size_t)kvh * p.ctx * HD;
+  if (has_new && head % G == 0) {
+    for (int e = threadIdx.x; e < HD; e += 256) p.kcache_w[((size_t)kvh * p.ctx + P) * HD + e] = kn[e];
+  }
+
+  // Scores: 16 lanes per key.
+  const int g = threadIdx.x / 16, l16 = threadIdx.x % 16;
+  constexpr int PER = HD / 16;
+  const float scale = sqrtf((float)HD);
+  for (int s = s0 + g; s < s1; s += 16) {
+    const float* kr = s == P ? kn : kbase + (size_t)s * HD;
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; e++) a = fmaf(qs[l16 * PER + e], kr[l16 * PER + e], a);
+    a = group_sum<16>(a);
+    if (l16 == 0) sc[s - s0] = a / scale;
+  }
+  __syncthreads();
+  const int n = s1 - s0;
+  if (wave == 0) {
+    const float v = lane < n ? sc[lane] : -INFINITY;
+    const float mx = wave_max(v);
+    const float e = lane < n ? expf(v - mx) : 0.0f;
+    if (lane < n) sc[lane] = e;
+    const float sum = wave_sum(e);
+    if (lane == 0) {
+      stat[0] = mx;
+      stat[1] = sum;
+    }
+  }
+  __syncthreads();
+  constexpr int KG = 256 / HD > 0 ? 256 / HD : 1;
+  const int d = threadIdx.x % HD, kg = threadIdx.x / HD;
+  if (kg < KG) {
+    float a = 0.0f;
+    for (int s = s0 + kg; s < s1; s += KG) a = fmaf(sc[s - s0], vbase[(size_t)s * HD + d], a);
+    red[kg][d] = a;
+  }
+  __syncthreads();
+  float* part = p.partial + ((size_t)head * p.splits + split) * (HD + 2);
+  if (threadIdx.x < HD) {
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KG; k++) a += red[k][threadIdx.x];
+    part[2 + threadIdx.x] = a;
+  }
+  if (threadIdx.x == 0) {
+    part[0] = stat[0];
+    part[1] = stat[1];
+  }
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) last = atomicAdd(&p.counter[head], 1u) == (unsigned)nsplit - 1;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  const float* pb = p.partial + (size_t)head * p.splits * (HD + 2);
+  float M = -INFINITY;
+  for (int i = 0; i < nsplit; i++) M = fmaxf(M, __builtin_nontemporal_load(&pb[(size_t)i * (HD + 2)]));
+  if (threadIdx.x < HD) {
+    float L = 0.0f, o = 0.0f;
+    for (int i = 0; i < nsplit; i++) {
+      const float* q = pb + (size_t)i * (HD + 2);
+      const float w = expf(__builtin_nontemporal_load(&q[0]) - M);
+      L = fmaf(__builtin_nontemporal_load(&q[1]), w, L);
+      o = fmaf(__builtin_nontemporal_load(&q[2 + threadIdx.x]), w, o);
+    }
+    p.out[(size_t)head * HD + threadIdx.x] = o / L;
+  }
+  if (threadIdx.x == 0) p.counter[head] = 0u;
+}
+
+}  // namespace
+
+int attention_decode_splits(int ctx, int chunk) { return (ctx + chunk - 1) / chunk; }
+
+void attention_prefill(const AttnParams& p, hipStream_t s) {
+  if (p.T <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
+  dim3 grid((p.T + BQ - 1) / BQ, p.q_heads);
+  switch (p.hd) {
+    case 16: hipLaunchKernelGGL(attn_prefill_kernel<16>, grid, dim3(256), 0, s, p); break;
+    case 32: hipLaunchKernelGGL(attn_prefill_kernel<32>, grid, dim3(256), 0, s, p); break;
+    case 64: hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, s, p); break;
+    case 128: hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, s, p); break;
+    default: ST_DIE("attention supports head_dim 16, 32, 64 or 128");
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+void attention_decode(const AttnParams& p, hipStream_t s) {
+  if (p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
+  if (p.chunk != 64) ST_DIE("decode attention chunk must be 64");
+  if (p.splits != attention_decode_splits(p.ctx, p.chunk)) ST_DIE("decode split count mismatch");
+  dim3 grid(p.splits, p.q_heads);
+  switch (p.hd) {
+    case 16: hipLaunchKernelGGL(attn_decode_kernel<16>, grid, dim3(256), 0, s, p); break;
+    case 32: hipLaunchKernelGGL(attn_decode_kernel<32>, grid, dim3(256), 0, s, p); break;
+    case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, s, p); break;
+    case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, s, p); break;
+    default: ST_DIE("attention supports head_dim 16, 32, 64 or 128");
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace sg

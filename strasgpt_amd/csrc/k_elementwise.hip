@@ -1,0 +1,191 @@
+// Small fused kernels of the forward pass: embedding gather, row RMSNorm,
+// per-head QK RMSNorm + RoPE, and the greedy argmax over the vocabulary.
+#include "device_common.h"
+#include "hip_check.h"
+#include "kernels.h"
+
+namespace sg {
+
+namespace {
+
+// Reference source/transformer.c:1247-1255: x[t][e] = bf16 -> f32 of the
+// token's embedding row (exact).
+__global__ __launch_bounds__(256) void embed_kernel(const int* tok, const uint16_t* table,
+                                                    int d, float* x) {
+  const int t = blockIdx.x;
+  const uint16_t* row = table + (size_t)tok[t] * d;
+  for (int e = threadIdx.x; e < d; e += blockDim.x) x[(size_t)t * d + e] = bf16_to_f32(row[e]);
+}
+
+// Reference rmsnorm (source/transformer.c:978-999) on one row per block.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const uint16_t* w,
+                                                      float* y, int d, float eps) {
+  __shared__ float red[4];
+  const float* xr = x + (size_t)blockIdx.x * d;
+  float* yr = y + (size_t)blockIdx.x * d;
+  float ss = 0.0f;
+  for (int e = threadIdx.x; e < d; e += 256) ss = fmaf(xr[e], xr[e], ss);
+  const float s = rms_scale(block_sum<256>(ss, red), d, eps);
+  for (int e = threadIdx.x; e < d; e += 256) yr[e] = (xr[e] * s) * bf16_to_f32(w[e]);
+}
+
+// One wavefront per (token, head): optional per-head RMSNorm with the
+// layer's q/k norm weight (source/transformer.c:1293-1307, 1340-1356), then
+// the pair rotation v0' = v0 cos - v1 sin, v1' = v0 sin + v1 cos with the
+// host-built table (source/transformer.c:1309-1323, 1358-1373).
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(
+    float* q, int q_heads, float* kcache, int ctx, int hd, const int* pos,
+    const uint16_t* qn, const uint16_t* kn, float eps, const float* rope,
+    int pair_bound, int pair_offset, int pair_stride) {
+#pragma clang fp contract(off)
+  __shared__ float v[512];
+  const int t = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+  const int P = *pos + t;
+  float* row;
+  const uint16_t* nw;
+  if (head < q_heads) {
+    row = q + ((size_t)t * q_heads + head) * hd;
+    nw = qn;
+  } else {
+    row = kcache + ((size_t)(head - q_heads) * ctx + P) * hd;
+    nw = kn;
+  }
+  float ss = 0.0f;
+  for (int e = lane; e < hd; e += WAVE) {
+    const float x = row[e];
+    v[e] = x;
+    ss = fmaf(x, x, ss);
+  }
+  ss = wave_sum(ss);
+  if (nw) {
+    const float s = rms_scale(ss, hd, eps);
+    for (int e = lane; e < hd; e += WAVE) v[e] = (v[e] * s) * bf16_to_f32(nw[e]);
+  }
+  __syncthreads();
+  const float* cs = rope + (size_t)P * hd;
+  for (int i = lane; i * pair_stride < pair_bound; i += WAVE) {
+    const int h = i * pair_stride;
+    const float fr = cs[h], fi = cs[h + pair_offset];
+    const float v0 = v[h], v1 = v[h + pair_offset];
+    row[h] = v0 * fr - v1 * fi;
+    row[h + pair_offset] = v0 * fi + v1 * fr;
+  }
+}
+
+// ------------------------------------------------------------- argmax --
+constexpr int kArgmaxBlocks = 512;
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  // Larger value wins; equal values keep the lower index. NaN never wins.
+  return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(ArgmaxParams p) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  __shared__ bool last;
+  const int n = p.n;
+  const int per = (n + gridDim.x - 1) / gridDim.x;
+  const int lo = blockIdx.x * per, hi = min(n, lo + per);
+  float bv = -INFINITY;
+  int bi = n;
+  for (int i = lo + (int)threadIdx.x; i < hi; i += 256) {
+    const float v = p.x[i];
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (threadIdx.x < st && better(sv[threadIdx.x + st], si[threadIdx.x + st], sv[threadIdx.x], si[threadIdx.x])) {
+      sv[threadIdx.x] = sv[threadIdx.x + st];
+      si[threadIdx.x] = si[threadIdx.x + st];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    p.part_v[blockIdx.x] = sv[0];
+    p.part_i[blockIdx.x] = si[0];
+    __threadfence();
+    last = atomicAdd(p.counter, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  bv = -INFINITY;
+  bi = n;
+  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) {
+    const float v = __builtin_nontemporal_load(&p.part_v[b]);
+    const int i = __builtin_nontemporal_load(&p.part_i[b]);
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (threadIdx.x < st && better(sv[threadIdx.x + st], si[threadIdx.x + st], sv[threadIdx.x], si[threadIdx.x])) {
+      sv[threadIdx.x] = sv[threadIdx.x + st];
+      si[threadIdx.x] = si[threadIdx.x + st];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    int best = si[0];
+    // Sequential-scan semantics: a NaN at index 0 is never replaced, and
+    // when nothing compares greater than element 0 the answer is 0.
+    if (best >= n || p.x[0] != p.x[0]) best = 0;
+    *p.out = best;
+    if (p.seq) {
+      const int k = *p.seq_len;
+      p.seq[k] = best;
+      *p.seq_len = k + 1;
+    }
+    if (p.pos_inc) *p.pos_inc += 1;
+    *p.counter = 0u;
+  }
+}
+
+}  // namespace
+
+void embed(const int* tok, int T, const uint16_t* table, int d, float* x, hipStream_t s) {
+  if (T <= 0) ST_DIE("embed needs T > 0");
+  hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, s, tok, table, d, x);
+  HIP_CHECK(hipGetLastError());
+}
+
+void rmsnorm_rows(const float* x, const uint16_t* w, float* y, int rows, int d, float eps,
+                  hipStream_t s) {
+  if (rows <= 0) ST_DIE("rmsnorm needs rows > 0");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, w, y, d, eps);
+  HIP_CHECK(hipGetLastError());
+}
+
+void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T, const int* pos,
+                  int ctx, int hd, const uint16_t* qn, const uint16_t* kn, float eps,
+                  const float* rope, int pair_bound, int pair_offset, int pair_stride,
+                  hipStream_t s) {
+  if (hd > 512 || hd % 2) ST_DIE("head_dim must be even and at most 512");
+  if (pair_stride < 1 || pair_bound - pair_stride + pair_offset >= hd)
+    ST_DIE("inconsistent RoPE pair geometry");
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(T, q_heads + kv_heads), dim3(64), 0, s, q,
+                     q_heads, kcache, ctx, hd, pos, qn, kn, eps, rope, pair_bound,
+                     pair_offset, pair_stride);
+  HIP_CHECK(hipGetLastError());
+}
+
+int argmax_blocks() { return kArgmaxBlocks; }
+
+void argmax(const ArgmaxParams& p, hipStream_t s) {
+  if (p.n <= 0) ST_DIE("argmax needs n > 0");
+  const int blocks = p.n < kArgmaxBlocks * 256 ? (p.n + 255) / 256 : kArgmaxBlocks;
+  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, p);
+  HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace sg

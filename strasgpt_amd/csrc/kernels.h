@@ -1,0 +1,140 @@
+// Host-side launch interface of the gfx950 kernels. Every launcher checks
+// on the host that the shapes fit what its kernel assumes (alignment,
+// multiples, shared-memory limits) and dies with a message otherwise, so
+// no kernel is launched on operands it would index out of bounds.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace sg {
+
+// ---------------------------------------------------------------- GEMV --
+// One activation row (decode step) against a bf16 [N][K] weight matrix,
+// fp32 accumulation. Optional RMSNorm of the input row (the reference's
+// rmsnorm, source/transformer.c:978-999) is computed by every block.
+enum GemvEpilogue {
+  GEMV_STORE = 0,    // y[n] = acc
+  GEMV_RESIDUAL = 1, // y[n] += acc                 (O-proj, down-proj)
+  GEMV_QKV = 2,      // rows -> q | raw k | v-cache (fused QKV projection)
+  GEMV_SWIGLU = 3,   // y[n] = silu(gate_n . x) * (up_n . x)
+};
+
+struct GemvParams {
+  const uint16_t* w;      // [N][K] bf16
+  const uint16_t* w2;     // up matrix for GEMV_SWIGLU, else null
+  const float* x;         // [K]
+  const uint16_t* norm_w; // RMSNorm weight [K] or null (no norm)
+  float eps;
+  int N, K;
+  float* y;
+  // GEMV_QKV destinations
+  float* q;        // [q_dim]
+  float* kraw;     // [kv_dim]  (pre-norm, pre-RoPE keys of this step)
+  float* vcache;   // this layer's [kv_heads][ctx][head_dim]
+  const int* pos;  // device: cache position of this step
+  int q_dim, kv_dim, head_dim, ctx;
+};
+void gemv(const GemvParams& p, int epilogue, hipStream_t s);
+
+// MXFP4 expert GEMV rows (decode MoE). Rows of expert e are
+// [N][K/32][16] code bytes and [N][K/32] E8M0 exponents.
+struct MoeGemvParams {
+  const uint8_t* blocks;   // [E][N][K/2]
+  const uint8_t* scales;   // [E][N][K/32]
+  const uint8_t* blocks2;  // up (SWIGLU) or null
+  const uint8_t* scales2;
+  const float* x;          // SWIGLU: [tokens][K]; DOWN: [tokens][topk][K]
+  const int* expert;       // [tokens][topk] selected expert ids
+  const float* weight;     // [tokens][topk] routing weights (down-proj only)
+  int tokens, topk, N, K;
+  float* y;                // SWIGLU: [tokens*topk][N]; DOWN: y[t][n] += routed sum
+};
+void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s);
+void moe_gemv_down(const MoeGemvParams& p, hipStream_t s);
+
+// ---------------------------------------------------------------- GEMM --
+// C[M][N] = A[M][K] (fp32) x W[N][K]^T (bf16) on MFMA; A is split into
+// bf16 hi + lo terms (SPLIT2) or rounded once (BF16).
+enum GemmPrecision { GEMM_SPLIT2 = 0, GEMM_BF16 = 1 };
+enum GemmEpilogue {
+  GEMM_STORE = 0,    // C[m][n] = acc
+  GEMM_RESIDUAL = 1, // C[m][n] += acc
+  GEMM_QKV = 2,      // q[m][n] | k-cache | v-cache rows at position P+m
+  GEMM_SWIGLU = 3,   // C[m][n] = silu(A.Wg_n) * (A.Wu_n)
+};
+struct GemmParams {
+  const float* a;  // [M][lda]
+  int lda;
+  const uint16_t* w;   // [N][K]
+  const uint16_t* w2;  // up matrix for GEMM_SWIGLU
+  int M, N, K;
+  float* c;            // [M][ldc]
+  int ldc;
+  // GEMM_QKV
+  float* q; float* kcache; float* vcache; const int* pos;
+  int q_dim, kv_dim, head_dim, ctx;
+};
+void gemm(const GemmParams& p, int epilogue, int precision, hipStream_t s);
+
+// -------------------------------------------------------- elementwise --
+void embed(const int* tok, int T, const uint16_t* table, int d, float* x, hipStream_t s);
+void rmsnorm_rows(const float* x, const uint16_t* w, float* y, int rows, int d,
+                  float eps, hipStream_t s);
+// Per-head RMSNorm (if norm weights given) and RoPE, in place, on T rows of
+// q ([T][heads*hd]) and on the T new key rows of one layer's k-cache.
+void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T,
+                  const int* pos, int ctx, int hd, const uint16_t* qn,
+                  const uint16_t* kn, float eps, const float* rope,
+                  int pair_bound, int pair_offset, int pair_stride, hipStream_t s);
+
+// ---------------------------------------------------------- attention --
+struct AttnParams {
+  const float* q;        // [T][q_heads*hd]
+  const float* kcache;   // layer base [kv_heads][ctx][hd]
+  const float* vcache;
+  float* out;            // [T][q_heads*hd]
+  const int* pos;        // device: position of the first query (cached count)
+  int T, q_heads, kv_heads, hd, ctx;
+  // decode only: raw key of this step and QK-norm/RoPE inputs
+  const float* kraw;     // [kv_heads*hd] or null
+  float* kcache_w;       // k-cache (writable) for the processed key
+  const uint16_t* qn;
+  const uint16_t* kn;
+  float eps;
+  const float* rope;
+  int pair_bound, pair_offset, pair_stride;
+  float* partial;        // [q_heads][splits][hd + 2]
+  unsigned* counter;     // [q_heads], zero on entry, left zero on exit
+  int chunk, splits;
+};
+void attention_prefill(const AttnParams& p, hipStream_t s);
+void attention_decode(const AttnParams& p, hipStream_t s);
+int attention_decode_splits(int ctx, int chunk);
+
+// ------------------------------------------------------------- argmax --
+// First index of the maximum (reference source/sampler.c:92-102). The last
+// block to finish writes out[0], appends to seq[*seq_len] (if seq) and
+// bumps *pos_inc (if given) so that a replayed decode step advances.
+struct ArgmaxParams {
+  const float* x;
+  int n;
+  float* part_v;   // [blocks]
+  int* part_i;     // [blocks]
+  unsigned* counter;
+  int* out;        // next token
+  int* seq;        // token log or null
+  int* seq_len;    // device counter or null
+  int* pos_inc;    // device position to increment or null
+};
+void argmax(const ArgmaxParams& p, hipStream_t s);
+int argmax_blocks();
+
+// ---------------------------------------------------------------- MoE --
+// Router logits (bf16 GEMV), top-k with lowest-index ties, softmax over
+// the k selected logits.
+void moe_route(const float* xn, int T, const uint16_t* router, int E, int d, int k,
+               int* sel, float* sel_w, hipStream_t s);
+
+}  // namespace sg

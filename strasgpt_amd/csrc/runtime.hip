@@ -1,0 +1,1144 @@
+// Host runtime of the StrasGPT forward pass on one MI355X.
+//
+// Load: every tensor of the safetensors description is read once (pread
+// into pinned staging buffers, two in flight) and copied to HBM; names are
+// matched like the reference loader (source/transformer.c:513-625: the
+// Hugging Face names and the Qwen3-VL "model.language_model." aliases),
+// sizes are checked exactly, and missing tensors are an error. Q, K and V
+// of a layer land in one fused [(qh + 2 kvh) hd][d] matrix.
+//
+// Predict: the reference's chunk loop (source/transformer.c:1607-1727)
+// over at most 512 tokens. A single-token chunk runs the decode kernels
+// (GEMV with fused RMSNorm and epilogues, split-K attention); longer
+// chunks run the MFMA GEMMs and the tiled prefill attention. The cache
+// position lives in device memory, so the single-token step can be
+// captured once as a HIP graph and replayed by the greedy generation loop,
+// whose argmax kernel feeds the next token and advances the position on
+// the device.
+#include <fcntl.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/stat.h>
+#include <time.h>
+#include <unistd.h>
+
+#include <vector>
+
+#include "hip_check.h"
+#include "kernels.h"
+#include "runtime.h"
+#include "safetensors.h"
+
+namespace {
+
+enum WClass {
+  W_EMB, W_MHA_NORM, W_Q, W_Q_NORM, W_K, W_K_NORM, W_V, W_O, W_FFN_NORM, W_GATE,
+  W_UP, W_DOWN, W_OUT_NORM, W_OUT, W_ROUTER, W_GB, W_GS, W_UB, W_US, W_DB, W_DS,
+  W_COUNT
+};
+
+const char* kClassName[W_COUNT] = {
+    "embedding", "mha_norm", "mha_q", "mha_q_norm", "mha_k", "mha_k_norm", "mha_v",
+    "mha_out", "ffn_norm", "ffn_fc", "ffn_up", "ffn_out", "out_norm", "out",
+    "moe_router", "moe_gate_blocks", "moe_gate_scales", "moe_up_blocks",
+    "moe_up_scales", "moe_down_blocks", "moe_down_scales"};
+
+struct LayerName {
+  const char* suffix;
+  WClass cls;
+};
+const LayerName kLayerNames[] = {
+    {"input_layernorm.weight", W_MHA_NORM},
+    {"self_attn.q_proj.weight", W_Q},
+    {"self_attn.q_norm.weight", W_Q_NORM},
+    {"self_attn.k_proj.weight", W_K},
+    {"self_attn.k_norm.weight", W_K_NORM},
+    {"self_attn.v_proj.weight", W_V},
+    {"self_attn.o_proj.weight", W_O},
+    {"post_attention_layernorm.weight", W_FFN_NORM},
+    {"mlp.gate_proj.weight", W_GATE},
+    {"mlp.up_proj.weight", W_UP},
+    {"mlp.down_proj.weight", W_DOWN},
+    {"mlp.router.weight", W_ROUTER},
+    {"mlp.experts.gate_proj_blocks", W_GB},
+    {"mlp.experts.gate_proj_scales", W_GS},
+    {"mlp.experts.up_proj_blocks", W_UB},
+    {"mlp.experts.up_proj_scales", W_US},
+    {"mlp.experts.down_proj_blocks", W_DB},
+    {"mlp.experts.down_proj_scales", W_DS},
+};
+
+// Name -> (class, layer). Accepts the base names and the
+// "model.language_model." aliases (reference source/transformer.c:520-574).
+bool classify(const char* name, WClass* cls, long* layer) {
+  char buf[SAFETENSORS_MAX_STRING];
+  const char* alias = "model.language_model.";
+  if (strncmp(name, alias, strlen(alias)) == 0) {
+    snprintf(buf, sizeof(buf), "model.%s", name + strlen(alias));
+    name = buf;
+  }
+  *layer = 0;
+  if (strcmp(name, SAFETENSORS_PATTERN_EMBEDDING_WEIGHT) == 0) { *cls = W_EMB; return true; }
+  if (strcmp(name, SAFETENSORS_PATTERN_OUT_NORM_WEIGHT) == 0) { *cls = W_OUT_NORM; return true; }
+  if (strcmp(name, SAFETENSORS_PATTERN_OUT_WEIGHT) == 0) { *cls = W_OUT; return true; }
+  const char* pre = "model.layers.";
+  if (strncmp(name, pre, strlen(pre)) != 0) return false;
+  const char* p = name + strlen(pre);
+  if (*p < '0' || *p > '9') return false;
+  long idx = 0;
+  while (*p >= '0' && *p <= '9') idx = idx * 10 + (*p++ - '0');
+  if (*p++ != '.') return false;
+  for (const LayerName& ln : kLayerNames) {
+    if (strcmp(p, ln.suffix) == 0) {
+      *cls = ln.cls;
+      *layer = idx;
+      return true;
+    }
+  }
+  return false;
+}
+
+bool is_global(int c) { return c == W_EMB || c == W_OUT_NORM || c == W_OUT; }
+
+struct Summary {
+  size_t bytes = 0;
+  float first[3] = {0, 0, 0}, last[3] = {0, 0, 0};
+  bool present = false;
+};
+
+double now_s() {
+  timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+}  // namespace
+
+struct transformer_device {
+  hipStream_t stream = nullptr;
+  int d = 0, hd = 0, H = 0, L = 0, qh = 0, kvh = 0, V = 0, ctx = 0, qd = 0, kvd = 0;
+  int qkv_rows = 0, E = 0, topk = 0;
+  float eps = 0.f;
+  bool qk_norm = false, moe = false, tied = false;
+  int pb = 0, po = 0, pst = 0;
+  size_t per_layer[W_COUNT] = {0};  // bytes per layer (or total for globals)
+  void* w[W_COUNT] = {nullptr};
+  // activations [512][...]
+  float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *act = nullptr;
+  float *kraw = nullptr, *logits = nullptr;
+  int logits_rows = 0;
+  size_t host_pos = 0;  // host mirror of *pos (profiling byte counts)
+  float *kc = nullptr, *vc = nullptr, *rope = nullptr;
+  int *tok = nullptr, *pos = nullptr, *next = nullptr, *seq = nullptr, *seq_len = nullptr;
+  int seq_cap = 0;
+  float* attn_part = nullptr;
+  unsigned* attn_cnt = nullptr;
+  int attn_splits = 0;
+  float* am_v = nullptr;
+  int* am_i = nullptr;
+  unsigned* am_cnt = nullptr;
+  int* h_tok = nullptr;
+  int* h_pos = nullptr;
+  int* h_next = nullptr;
+  hipGraphExec_t graph = nullptr;
+  int precision = sg::GEMM_SPLIT2;
+  float* cap_out = nullptr;
+  float* cap_final = nullptr;
+  float* cap_dev = nullptr;
+  float* cap_final_dev = nullptr;
+  // MoE scratch
+  int* moe_sel = nullptr;
+  float* moe_w = nullptr;
+  float* moe_act = nullptr;
+  Summary summary[W_COUNT];
+  // measurement hooks
+  bool prof = false;
+  struct Pending {
+    int cls;
+    hipEvent_t a, b;
+    double bytes, flops;
+  };
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> event_pool;
+  transformer_kernel_stat_t stat[TRANSFORMER_K_CLASS_COUNT];
+};
+
+namespace {
+
+typedef transformer_device Dev;
+
+template <typename T>
+T* dalloc(size_t count) {
+  void* p = nullptr;
+  if (count == 0) count = 1;
+  HIP_CHECK(hipMalloc(&p, count * sizeof(T)));
+  return (T*)p;
+}
+
+uint16_t* W16(Dev* D, int cls, int layer = 0) {
+  return (uint16_t*)((char*)D->w[cls] + (size_t)layer * D->per_layer[cls]);
+}
+uint8_t* W8(Dev* D, int cls, int layer = 0) {
+  return (uint8_t*)D->w[cls] + (size_t)layer * D->per_layer[cls];
+}
+
+// Brackets one launch with events when profiling is on.
+struct Prof {
+  Dev* D;
+  int cls;
+  double bytes, flops;
+  hipEvent_t a = nullptr, b = nullptr;
+  Prof(Dev* d, int c, double by, double fl) : D(d), cls(c), bytes(by), flops(fl) {
+    if (!D->prof) return;
+    a = take();
+    b = take();
+    HIP_CHECK(hipEventRecord(a, D->stream));
+  }
+  ~Prof() {
+    if (!D->prof) return;
+    HIP_CHECK(hipEventRecord(b, D->stream));
+    D->pending.push_back({cls, a, b, bytes, flops});
+  }
+  hipEvent_t take() {
+    if (D->event_pool.empty()) {
+      hipEvent_t e;
+      HIP_CHECK(hipEventCreate(&e));
+      return e;
+    }
+    hipEvent_t e = D->event_pool.back();
+    D->event_pool.pop_back();
+    return e;
+  }
+};
+
+// Called after a stream synchronisation: folds finished launches into the
+// per-class statistics.
+void harvest(Dev* D) {
+  for (auto& p : D->pending) {
+    float ms = 0.f;
+    HIP_CHECK(hipEventElapsedTime(&ms, p.a, p.b));
+    transformer_kernel_stat_t& st = D->stat[p.cls];
+    st.launches++;
+    st.total_ms += ms;
+    st.bytes += p.bytes;
+    st.flops += p.flops;
+    D->event_pool.push_back(p.a);
+    D->event_pool.push_back(p.b);
+  }
+  D->pending.clear();
+}
+
+// -------------------------------------------------------------- upload --
+
+struct Stager {
+  static constexpr size_t kChunk = 64u << 20;
+  void* buf[2] = {nullptr, nullptr};
+  hipEvent_t ev[2];
+  bool used[2] = {false, false};
+  int cur = 0;
+  hipStream_t s;
+  explicit Stager(hipStream_t st) : s(st) {
+    for (int i = 0; i < 2; i++) {
+      HIP_CHECK(hipHostMalloc(&buf[i], kChunk, hipHostMallocDefault));
+      HIP_CHECK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+    }
+  }
+  ~Stager() {
+    HIP_CHECK(hipStreamSynchronize(s));
+    for (int i = 0; i < 2; i++) {
+      HIP_CHECK(hipHostFree(buf[i]));
+      HIP_CHECK(hipEventDestroy(ev[i]));
+    }
+  }
+  void copy(int fd, size_t offset, size_t size, void* dst) {
+    size_t done = 0;
+    while (done < size) {
+      const size_t n = size - done < kChunk ? size - done : kChunk;
+      if (used[cur]) HIP_CHECK(hipEventSynchronize(ev[cur]));
+      size_t got = 0;
+      while (got < n) {
+        ssize_t r = pread(fd, (char*)buf[cur] + got, n - got, (off_t)(offset + done + got));
+        if (r <= 0) ST_DIE("failed to read from file");
+        got += (size_t)r;
+      }
+      HIP_CHECK(hipMemcpyAsync((char*)dst + done, buf[cur], n, hipMemcpyHostToDevice, s));
+      HIP_CHECK(hipEventRecord(ev[cur], s));
+      used[cur] = true;
+      cur ^= 1;
+      done += n;
+    }
+  }
+};
+
+void build_rope_table(const transformer_configuration_t* c, std::vector<float>& t) {
+  // Reference state_from_safetensors (source/transformer.c:126-146), same
+  // fp32 libm calls so the table is bit-identical to the CPU path's.
+  const size_t hd = c->head_dim;
+  const bool interleaved = c->rope_pair_stride == 2;
+  const float coef = interleaved ? 1.0f : 2.0f;
+  t.assign(c->context_len * hd, 0.0f);
+  for (size_t i = 0; i < c->context_len; i++) {
+    for (size_t j = 0; j < c->rope_pair_bound; j += c->rope_pair_stride) {
+      float freq = 1.0f / powf(c->rope_theta, (coef * (float)j) / (float)hd);
+      float val = (float)i * freq;
+      t[i * hd + j] = cosf(val);
+      t[i * hd + j + c->rope_pair_offset] = sinf(val);
+    }
+  }
+}
+
+bool has_tensor(const safetensors_t* s, WClass want) {
+  for (size_t i = 0; i < s->tensor_count; i++) {
+    WClass c;
+    long l;
+    if (classify(s->tensor[i].name, &c, &l) && c == want) return true;
+  }
+  return false;
+}
+
+// ------------------------------------------------------------- forward --
+
+enum {
+  K_QKV_GEMV = TRANSFORMER_K_QKV_GEMV, K_ATT_DEC = TRANSFORMER_K_ATTENTION_DECODE,
+  K_O_GEMV = TRANSFORMER_K_O_GEMV, K_GU_GEMV = TRANSFORMER_K_GATE_UP_GEMV,
+  K_DOWN_GEMV = TRANSFORMER_K_DOWN_GEMV, K_LOGITS = TRANSFORMER_K_LOGITS_GEMV,
+  K_ARGMAX = TRANSFORMER_K_ARGMAX, K_ROUTE = TRANSFORMER_K_MOE_ROUTE,
+  K_MOE_GU = TRANSFORMER_K_MOE_GATE_UP, K_MOE_DOWN = TRANSFORMER_K_MOE_DOWN,
+  K_QKV_GEMM = TRANSFORMER_K_QKV_GEMM, K_ATT_PRE = TRANSFORMER_K_ATTENTION_PREFILL,
+  K_O_GEMM = TRANSFORMER_K_O_GEMM, K_GU_GEMM = TRANSFORMER_K_GATE_UP_GEMM,
+  K_DOWN_GEMM = TRANSFORMER_K_DOWN_GEMM, K_ELEM = TRANSFORMER_K_ELEMENTWISE
+};
+
+double mxfp4_bytes(double values) { return values * (0.5 + 1.0 / 32.0); }
+
+// MoE FFN of T rows: RMSNorm, router top-k, MXFP4 SwiGLU experts, routed
+// down-projection accumulated into the residual stream.
+void ffn_moe(Dev* D, int l, int T) {
+  hipStream_t s = D->stream;
+  const double d = D->d, H = D->H, k = D->topk;
+  {
+    Prof pr(D, K_ELEM, 2.0 * T * d * 4, 0);
+    sg::rmsnorm_rows(D->x, W16(D, W_FFN_NORM, l), D->xn, T, D->d, D->eps, s);
+  }
+  {
+    Prof pr(D, K_ROUTE, (double)D->E * d * 2, 2.0 * T * D->E * d);
+    sg::moe_route(D->xn, T, W16(D, W_ROUTER, l), D->E, D->d, D->topk, D->moe_sel, D->moe_w, s);
+  }
+  sg::MoeGemvParams g{};
+  g.blocks = W8(D, W_GB, l);
+  g.scales = W8(D, W_GS, l);
+  g.blocks2 = W8(D, W_UB, l);
+  g.scales2 = W8(D, W_US, l);
+  g.x = D->xn;
+  g.expert = D->moe_sel;
+  g.tokens = T;
+  g.topk = D->topk;
+  g.N = D->H;
+  g.K = D->d;
+  g.y = D->moe_act;
+  {
+    Prof pr(D, K_MOE_GU, T * k * mxfp4_bytes(2 * H * d), 4.0 * T * k * H * d);
+    sg::moe_gemv_swiglu(g, s);
+  }
+  sg::MoeGemvParams dn{};
+  dn.blocks = W8(D, W_DB, l);
+  dn.scales = W8(D, W_DS, l);
+  dn.x = D->moe_act;
+  dn.expert = D->moe_sel;
+  dn.weight = D->moe_w;
+  dn.tokens = T;
+  dn.topk = D->topk;
+  dn.N = D->d;
+  dn.K = D->H;
+  dn.y = D->x;
+  {
+    Prof pr(D, K_MOE_DOWN, T * k * mxfp4_bytes(H * d), 2.0 * T * k * H * d);
+    sg::moe_gemv_down(dn, s);
+  }
+}
+
+void layer_decode(Dev* D, int l) {
+  hipStream_t s = D->stream;
+  const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
+  float* kc = D->kc + l * cache_layer;
+  float* vc = D->vc + l * cache_layer;
+  const double d = D->d;
+
+  sg::GemvParams g{};
+  g.w = W16(D, W_Q, l);  // fused QKV block of layer l
+  g.x = D->x;
+  g.norm_w = W16(D, W_MHA_NORM, l);
+  g.eps = D->eps;
+  g.N = D->qkv_rows;
+  g.K = D->d;
+  g.q = D->q;
+  g.kraw = D->kraw;
+  g.vcache = vc;
+  g.pos = D->pos;
+  g.q_dim = D->qd;
+  g.kv_dim = D->kvd;
+  g.head_dim = D->hd;
+  g.ctx = D->ctx;
+  {
+    Prof pr(D, K_QKV_GEMV, (double)D->qkv_rows * d * 2, 2.0 * D->qkv_rows * d);
+    sg::gemv(g, sg::GEMV_QKV, s);
+  }
+
+  sg::AttnParams a{};
+  a.q = D->q;
+  a.kcache = kc;
+  a.vcache = vc;
+  a.out = D->att;
+  a.pos = D->pos;
+  a.T = 1;
+  a.q_heads = D->qh;
+  a.kv_heads = D->kvh;
+  a.hd = D->hd;
+  a.ctx = D->ctx;
+  a.kraw = D->kraw;
+  a.kcache_w = kc;
+  a.qn = D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr;
+  a.kn = D->qk_norm ? W16(D, W_K_NORM, l) : nullptr;
+  a.eps = D->eps;
+  a.rope = D->rope;
+  a.pair_bound = D->pb;
+  a.pair_offset = D->po;
+  a.pair_stride = D->pst;
+  a.partial = D->attn_part;
+  a.counter = D->attn_cnt;
+  a.chunk = 64;
+  a.splits = D->attn_splits;
+  {
+    const double keys = (double)D->host_pos + 1;
+    Prof pr(D, K_ATT_DEC, 2.0 * D->kvh * keys * D->hd * 4, 4.0 * D->qh * keys * D->hd);
+    sg::attention_decode(a, s);
+  }
+
+  sg::GemvParams o{};
+  o.w = W16(D, W_O, l);
+  o.x = D->att;
+  o.N = D->d;
+  o.K = D->qd;
+  o.y = D->x;
+  {
+    Prof pr(D, K_O_GEMV, d * D->qd * 2, 2.0 * d * D->qd);
+    sg::gemv(o, sg::GEMV_RESIDUAL, s);
+  }
+
+  if (!D->moe) {
+    sg::GemvParams f{};
+    f.w = W16(D, W_GATE, l);
+    f.w2 = W16(D, W_UP, l);
+    f.x = D->x;
+    f.norm_w = W16(D, W_FFN_NORM, l);
+    f.eps = D->eps;
+    f.N = D->H;
+    f.K = D->d;
+    f.y = D->act;
+    {
+      Prof pr(D, K_GU_GEMV, 2.0 * D->H * d * 2, 4.0 * D->H * d);
+      sg::gemv(f, sg::GEMV_SWIGLU, s);
+    }
+    sg::GemvParams dn{};
+    dn.w = W16(D, W_DOWN, l);
+    dn.x = D->act;
+    dn.N = D->d;
+    dn.K = D->H;
+    dn.y = D->x;
+    {
+      Prof pr(D, K_DOWN_GEMV, d * D->H * 2, 2.0 * d * D->H);
+      sg::gemv(dn, sg::GEMV_RESIDUAL, s);
+    }
+  } else {
+    ffn_moe(D, l, 1);
+  }
+}
+
+void layer_prefill(Dev* D, int l, int T) {
+  hipStream_t s = D->stream;
+  const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
+  float* kc = D->kc + l * cache_layer;
+  float* vc = D->vc + l * cache_layer;
+  const double d = D->d, M = T;
+
+  {
+    Prof pr(D, K_ELEM, 2.0 * M * d * 4, 0);
+    sg::rmsnorm_rows(D->x, W16(D, W_MHA_NORM, l), D->xn, T, D->d, D->eps, s);
+  }
+  sg::GemmParams g{};
+  g.a = D->xn;
+  g.lda = D->d;
+  g.w = W16(D, W_Q, l);
+  g.M = T;
+  g.N = D->qkv_rows;
+  g.K = D->d;
+  g.q = D->q;
+  g.kcache = kc;
+  g.vcache = vc;
+  g.pos = D->pos;
+  g.q_dim = D->qd;
+  g.kv_dim = D->kvd;
+  g.head_dim = D->hd;
+  g.ctx = D->ctx;
+  {
+    Prof pr(D, K_QKV_GEMM, (double)D->qkv_rows * d * 2, 2.0 * M * D->qkv_rows * d);
+    sg::gemm(g, sg::GEMM_QKV, D->precision, s);
+  }
+  {
+    Prof pr(D, K_ELEM, 2.0 * M * (D->qd + D->kvd) * 4, 0);
+    sg::qk_norm_rope(D->q, D->qh, kc, D->kvh, T, D->pos, D->ctx, D->hd,
+                     D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr,
+                     D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
+                     D->po, D->pst, s);
+  }
+  sg::AttnParams a{};
+  a.q = D->q;
+  a.kcache = kc;
+  a.vcache = vc;
+  a.out = D->att;
+  a.pos = D->pos;
+  a.T = T;
+  a.q_heads = D->qh;
+  a.kv_heads = D->kvh;
+  a.hd = D->hd;
+  a.ctx = D->ctx;
+  {
+    // causal (query, key) pairs: sum over t of (P + t + 1)
+    const double pairs = M * (double)D->host_pos + M * (M + 1) / 2;
+    Prof pr(D, K_ATT_PRE, 2.0 * D->kvh * ((double)D->host_pos + M) * D->hd * 4,
+            4.0 * D->qh * D->hd * pairs);
+    sg::attention_prefill(a, s);
+  }
+  sg::GemmParams o{};
+  o.a = D->att;
+  o.lda = D->qd;
+  o.w = W16(D, W_O, l);
+  o.M = T;
+  o.N = D->d;
+  o.K = D->qd;
+  o.c = D->x;
+  o.ldc = D->d;
+  {
+    Prof pr(D, K_O_GEMM, d * D->qd * 2, 2.0 * M * d * D->qd);
+    sg::gemm(o, sg::GEMM_RESIDUAL, D->precision, s);
+  }
+  if (!D->moe) {
+    {
+      Prof pr(D, K_ELEM, 2.0 * M * d * 4, 0);
+      sg::rmsnorm_rows(D->x, W16(D, W_FFN_NORM, l), D->xn, T, D->d, D->eps, s);
+    }
+    sg::GemmParams f{};
+    f.a = D->xn;
+    f.lda = D->d;
+    f.w = W16(D, W_GATE, l);
+    f.w2 = W16(D, W_UP, l);
+    f.M = T;
+    f.N = D->H;
+    f.K = D->d;
+    f.c = D->act;
+    f.ldc = D->H;
+    {
+      Prof pr(D, K_GU_GEMM, 2.0 * D->H * d * 2, 4.0 * M * D->H * d);
+      sg::gemm(f, sg::GEMM_SWIGLU, D->precision, s);
+    }
+    sg::GemmParams dn{};
+    dn.a = D->act;
+    dn.lda = D->H;
+    dn.w = W16(D, W_DOWN, l);
+    dn.M = T;
+    dn.N = D->d;
+    dn.K = D->H;
+    dn.c = D->x;
+    dn.ldc = D->d;
+    {
+      Prof pr(D, K_DOWN_GEMM, d * D->H * 2, 2.0 * M * d * D->H);
+      sg::gemm(dn, sg::GEMM_RESIDUAL, D->precision, s);
+    }
+  } else {
+    ffn_moe(D, l, T);
+  }
+}
+
+// Logits of chunk rows [T - lc, T): final RMSNorm fused into the GEMV.
+void classifier(Dev* D, int T, int lc) {
+  for (int r = 0; r < lc; r++) {
+    sg::GemvParams g{};
+    g.w = D->tied ? W16(D, W_EMB) : W16(D, W_OUT);
+    g.x = D->x + (size_t)(T - lc + r) * D->d;
+    g.norm_w = W16(D, W_OUT_NORM);
+    g.eps = D->eps;
+    g.N = D->V;
+    g.K = D->d;
+    g.y = D->logits + (size_t)r * D->V;
+    Prof pr(D, K_LOGITS, (double)D->V * D->d * 2, 2.0 * D->V * D->d);
+    sg::gemv(g, sg::GEMV_STORE, D->stream);
+  }
+}
+
+// One chunk of T <= 512 tokens whose ids are in device memory at `tok`,
+// at the device position *D->pos (mirrored on the host in D->host_pos).
+void forward_chunk(Dev* D, const int* tok, int T, int lc) {
+  {
+    Prof pr(D, K_ELEM, (double)T * D->d * 6, 0);
+    sg::embed(tok, T, W16(D, W_EMB), D->d, D->x, D->stream);
+  }
+  const bool capture = D->cap_out != nullptr;
+  for (int l = 0; l < D->L; l++) {
+    if (T == 1) layer_decode(D, l);
+    else layer_prefill(D, l, T);
+    if (capture)
+      HIP_CHECK(hipMemcpyAsync(D->cap_dev + (size_t)l * T * D->d, D->x,
+                               (size_t)T * D->d * sizeof(float), hipMemcpyDeviceToDevice,
+                               D->stream));
+  }
+  if (capture) sg::rmsnorm_rows(D->x, W16(D, W_OUT_NORM), D->cap_final_dev, T, D->d, D->eps, D->stream);
+  if (lc > 0) classifier(D, T, lc);
+}
+
+void ensure_logits(Dev* D, int rows) {
+  if (rows <= D->logits_rows) return;
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  if (D->graph) {  // the captured decode step points at the old buffer
+    HIP_CHECK(hipGraphExecDestroy(D->graph));
+    D->graph = nullptr;
+  }
+  if (D->logits) HIP_CHECK(hipFree(D->logits));
+  D->logits = dalloc<float>((size_t)rows * D->V);
+  D->logits_rows = rows;
+}
+
+void set_pos(Dev* D, size_t pos) {
+  *D->h_pos = (int)pos;
+  D->host_pos = pos;
+  HIP_CHECK(hipMemcpyAsync(D->pos, D->h_pos, sizeof(int), hipMemcpyHostToDevice, D->stream));
+}
+
+void upload_tokens(Dev* D, const int* token, int T) {
+  for (int i = 0; i < T; i++) {
+    if (token[i] < 0 || token[i] >= D->V) ST_DIE("token id out of range");
+    D->h_tok[i] = token[i];
+  }
+  HIP_CHECK(hipMemcpyAsync(D->tok, D->h_tok, (size_t)T * sizeof(int), hipMemcpyHostToDevice,
+                           D->stream));
+}
+
+void argmax_to(Dev* D, const float* row, bool log_seq, bool bump_pos) {
+  sg::ArgmaxParams p{};
+  p.x = row;
+  p.n = D->V;
+  p.part_v = D->am_v;
+  p.part_i = D->am_i;
+  p.counter = D->am_cnt;
+  p.out = D->next;
+  p.seq = log_seq ? D->seq : nullptr;
+  p.seq_len = log_seq ? D->seq_len : nullptr;
+  p.pos_inc = bump_pos ? D->pos : nullptr;
+  Prof pr(D, K_ARGMAX, (double)D->V * 4, 0);
+  sg::argmax(p, D->stream);
+}
+
+// The reference chunk loop over `token` (source/transformer.c:1643-1726):
+// logits of the caller's window [T - lc, T) are copied to host_logits (if
+// given); the last chunk's rows stay on the device.
+void predict_device(transformer_t* t, size_t T, const int* token, size_t lc,
+                    float* host_logits) {
+  Dev* D = t->device;
+  if (T + t->state->cached_count > (size_t)D->ctx) ST_DIE("context length exhausted");
+  if (lc > T) lc = T;
+  const size_t start = T - lc;
+  const size_t chunk_max = TRANSFORMER_CHUNK_MAX_LEN;
+  if (D->cap_out && T > chunk_max) ST_DIE("hidden-state capture covers one chunk of at most 512 tokens");
+  for (size_t c0 = 0; c0 < T; c0 += chunk_max) {
+    const size_t n = T - c0 < chunk_max ? T - c0 : chunk_max;
+    const size_t lo = c0 > start ? c0 : start, hi = c0 + n;
+    const size_t clc = lo < hi ? hi - lo : 0;
+    ensure_logits(D, (int)(clc > 0 ? clc : 1));
+    upload_tokens(D, token + c0, (int)n);
+    set_pos(D, t->state->cached_count);
+    forward_chunk(D, D->tok, (int)n, (int)clc);
+    if (clc > 0 && host_logits) {
+      HIP_CHECK(hipMemcpyAsync(host_logits + (lo - start) * D->V, D->logits,
+                               clc * D->V * sizeof(float), hipMemcpyDeviceToHost, D->stream));
+    }
+    HIP_CHECK(hipStreamSynchronize(D->stream));
+    harvest(D);
+    t->state->cached_count += n;
+  }
+  if (D->cap_out) {
+    HIP_CHECK(hipMemcpy(D->cap_out, D->cap_dev, (size_t)D->L * T * D->d * sizeof(float),
+                        hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(D->cap_final, D->cap_final_dev, T * D->d * sizeof(float),
+                        hipMemcpyDeviceToHost));
+    D->cap_out = nullptr;
+    D->cap_final = nullptr;
+  }
+}
+
+void build_decode_graph(Dev* D) {
+  if (D->graph) return;
+  hipGraph_t g;
+  float* cap = D->cap_out;  // hidden-state capture is never part of the graph
+  D->cap_out = nullptr;
+  HIP_CHECK(hipStreamBeginCapture(D->stream, hipStreamCaptureModeThreadLocal));
+  forward_chunk(D, D->next, 1, 1);
+  argmax_to(D, D->logits, true, true);
+  HIP_CHECK(hipStreamEndCapture(D->stream, &g));
+  D->cap_out = cap;
+  HIP_CHECK(hipGraphInstantiate(&D->graph, g, nullptr, nullptr, 0));
+  HIP_CHECK(hipGraphDestroy(g));
+}
+
+}  // namespace
+
+// ================================================================= API ==
+
+extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
+  if (!st) ST_DIE("NULL safetensors");
+  transformer_t* t = (transformer_t*)calloc(1, sizeof(transformer_t));
+  transformer_configuration_t* c =
+      (transformer_configuration_t*)calloc(1, sizeof(transformer_configuration_t));
+  transformer_weights_t* w = (transformer_weights_t*)calloc(1, sizeof(transformer_weights_t));
+  transformer_state_t* ss = (transformer_state_t*)calloc(1, sizeof(transformer_state_t));
+  Dev* D = new Dev();
+  if (!t || !c || !w || !ss) ST_DIE("failed to malloc for transformer_t");
+  t->config = c;
+  t->weights = w;
+  t->state = ss;
+  t->device = D;
+
+  // Configuration (reference configuration_from_safetensors,
+  // source/transformer.c:17-58).
+  c->embedding_dim = st->embedding_dim;
+  c->head_dim = st->head_dim;
+  c->hidden_dim = st->hidden_dim;
+  c->layer_count = st->layer_count;
+  c->q_head_count = st->q_head_count;
+  c->kv_head_count = st->kv_head_count;
+  c->vocabulary_len = st->vocabulary_len;
+  c->context_len = st->context_len;
+  c->epsilon = st->epsilon;
+  c->rope_theta = st->rope_theta;
+  if (st->rope_interleaved) {
+    c->rope_pair_bound = st->head_dim;
+    c->rope_pair_offset = 1;
+    c->rope_pair_stride = 2;
+  } else {
+    c->rope_pair_bound = st->head_dim / 2;
+    c->rope_pair_offset = st->head_dim / 2;
+    c->rope_pair_stride = 1;
+  }
+  c->mrope_section_count = st->mrope_section_count;
+  if (c->mrope_section_count) {
+    c->mrope_section = (size_t*)calloc(c->mrope_section_count, sizeof(size_t));
+    for (size_t i = 0; i < c->mrope_section_count; i++) c->mrope_section[i] = st->mrope_section[i];
+  }
+  c->aliased_out_weight = safetensors_aliased_out_weight(st);
+  c->qk_norm = has_tensor(st, W_Q_NORM);
+  const bool moe = has_tensor(st, W_ROUTER);
+  c->expert_count = moe ? st->expert_count : 0;
+  c->expert_used_count = moe ? st->expert_used_count : 0;
+
+  D->d = (int)c->embedding_dim;
+  D->hd = (int)c->head_dim;
+  D->H = (int)c->hidden_dim;
+  D->L = (int)c->layer_count;
+  D->qh = (int)c->q_head_count;
+  D->kvh = (int)c->kv_head_count;
+  D->V = (int)c->vocabulary_len;
+  D->ctx = (int)c->context_len;
+  D->qd = D->qh * D->hd;
+  D->kvd = D->kvh * D->hd;
+  D->qkv_rows = D->qd + 2 * D->kvd;
+  D->eps = c->epsilon;
+  D->qk_norm = c->qk_norm;
+  D->moe = moe;
+  D->tied = c->aliased_out_weight;
+  D->E = (int)c->expert_count;
+  D->topk = (int)c->expert_used_count;
+  D->pb = (int)c->rope_pair_bound;
+  D->po = (int)c->rope_pair_offset;
+  D->pst = (int)c->rope_pair_stride;
+
+  if (!D->d || !D->hd || !D->H || !D->L || !D->qh || !D->kvh || !D->V || !D->ctx)
+    ST_DIE("incomplete model configuration");
+  if (D->qh % D->kvh) ST_DIE("q_head_count must be a multiple of kv_head_count");
+  if (D->d % 32 || D->H % 32 || D->qd % 32) ST_DIE("model dimensions must be multiples of 32");
+  if (D->hd != 16 && D->hd != 32 && D->hd != 64 && D->hd != 128)
+    ST_DIE("head_dim must be 16, 32, 64 or 128");
+  if (moe && (D->E <= 0 || D->topk <= 0 || D->topk > D->E || D->E > 1024))
+    ST_DIE("MoE model needs num_local_experts and num_experts_per_tok");
+
+  HIP_CHECK(hipStreamCreateWithFlags(&D->stream, hipStreamNonBlocking));
+
+  // Per-layer byte sizes of each weight class.
+  const size_t d = D->d, hd = D->hd, H = D->H, E = D->E, V = D->V;
+  size_t* pl = D->per_layer;
+  pl[W_EMB] = V * d * 2;
+  pl[W_MHA_NORM] = d * 2;
+  pl[W_Q] = (size_t)D->qkv_rows * d * 2;  // fused Q|K|V block
+  pl[W_Q_NORM] = c->qk_norm ? hd * 2 : 0;
+  pl[W_K_NORM] = c->qk_norm ? hd * 2 : 0;
+  pl[W_O] = d * D->qd * 2;
+  pl[W_FFN_NORM] = d * 2;
+  pl[W_GATE] = moe ? 0 : H * d * 2;
+  pl[W_UP] = moe ? 0 : H * d * 2;
+  pl[W_DOWN] = moe ? 0 : d * H * 2;
+  pl[W_OUT_NORM] = d * 2;
+  pl[W_OUT] = D->tied ? 0 : V * d * 2;
+  pl[W_ROUTER] = E * d * 2;
+  pl[W_GB] = pl[W_UB] = E * H * d / 2;
+  pl[W_GS] = pl[W_US] = E * H * d / 32;
+  pl[W_DB] = E * d * H / 2;
+  pl[W_DS] = E * d * H / 32;
+  for (int k = 0; k < W_COUNT; k++) {
+    if (!pl[k]) continue;
+    const size_t layers = is_global(k) ? 1 : (size_t)D->L;
+    D->w[k] = dalloc<uint8_t>(pl[k] * layers);
+  }
+  if (D->tied) D->w[W_OUT] = D->w[W_EMB];
+
+  // Expected tensor size for each class (K and V share the fused block).
+  auto expect = [&](int cls) -> size_t {
+    if (cls == W_Q) return (size_t)D->qd * d * 2;
+    if (cls == W_K || cls == W_V) return (size_t)D->kvd * d * 2;
+    return pl[cls];
+  };
+  auto dest = [&](int cls, long l) -> char* {
+    if (cls == W_Q) return (char*)D->w[W_Q] + l * pl[W_Q];
+    if (cls == W_K) return (char*)D->w[W_Q] + l * pl[W_Q] + (size_t)D->qd * d * 2;
+    if (cls == W_V) return (char*)D->w[W_Q] + l * pl[W_Q] + (size_t)(D->qd + D->kvd) * d * 2;
+    return (char*)D->w[cls] + l * pl[cls];
+  };
+
+  std::vector<std::vector<char>> seen(W_COUNT + 2);
+  for (int k = 0; k < W_COUNT + 2; k++) seen[k].assign(k < W_COUNT && is_global(k) ? 1 : D->L, 0);
+  std::vector<int> fds(st->file_count, -1);
+  {
+    Stager stage(D->stream);
+    for (size_t i = 0; i < st->tensor_count; i++) {
+      const safetensors_tensor_t* tn = &st->tensor[i];
+      WClass cls;
+      long layer;
+      if (!classify(tn->name, &cls, &layer) ||
+          (cls != W_K && cls != W_V && !pl[cls] && !(cls == W_OUT && !D->tied))) {
+        fprintf(stderr, "[StrasGPT] Warning: unknown tensor %s\n", tn->name);
+        continue;
+      }
+      if (layer < 0 || layer >= (is_global(cls) ? 1 : D->L)) ST_DIE("tensor layer index out of range");
+      const bool u8 = cls >= W_GB;
+      if (tn->type != (u8 ? SAFETENSORS_TYPE_U8 : SAFETENSORS_TYPE_BF16)) {
+        char m[SAFETENSORS_MAX_STRING];
+        snprintf(m, sizeof(m), "unexpected dtype for %s", tn->name);
+        ST_DIE(m);
+      }
+      if (tn->size != expect(cls)) {
+        char m[SAFETENSORS_MAX_STRING];
+        snprintf(m, sizeof(m), "unexpected size for %s: have %zu expected %zu", tn->name,
+                 tn->size, expect(cls));
+        ST_DIE(m);
+      }
+      if (tn->file >= st->file_count) ST_DIE("tensor file index out of range");
+      if (fds[tn->file] < 0) {
+        fds[tn->file] = open(st->file[tn->file], O_RDONLY);
+        if (fds[tn->file] < 0) ST_DIE("failed to open file");
+      }
+      stage.copy(fds[tn->file], tn->offset, tn->size, dest(cls, layer));
+      const int slot = (cls == W_K) ? W_COUNT : (cls == W_V) ? W_COUNT + 1 : cls;
+      seen[slot][layer] = 1;
+    }
+  }
+  for (int fd : fds)
+    if (fd >= 0) close(fd);
+  for (int k = 0; k < W_COUNT + 2; k++) {
+    const bool needed = k >= W_COUNT || (pl[k] && !(k == W_OUT && D->tied));
+    if (!needed) continue;
+    for (size_t l = 0; l < seen[k].size(); l++) {
+      if (!seen[k][l]) {
+        char m[256];
+        snprintf(m, sizeof(m), "missing tensor: %s of layer %zu",
+                 k == W_COUNT ? "mha_k" : k == W_COUNT + 1 ? "mha_v" : kClassName[k], l);
+        ST_DIE(m);
+      }
+    }
+  }
+
+  // Public weight pointers.
+  w->embedding_weight = W16(D, W_EMB);
+  w->mha_norm_weight = W16(D, W_MHA_NORM);
+  w->mha_qkv_weight = W16(D, W_Q);
+  w->mha_q_norm_weight = c->qk_norm ? W16(D, W_Q_NORM) : nullptr;
+  w->mha_k_norm_weight = c->qk_norm ? W16(D, W_K_NORM) : nullptr;
+  w->mha_out_weight = W16(D, W_O);
+  w->ffn_norm_weight = W16(D, W_FFN_NORM);
+  w->ffn_fc_weight = moe ? nullptr : W16(D, W_GATE);
+  w->ffn_up_weight = moe ? nullptr : W16(D, W_UP);
+  w->ffn_out_weight = moe ? nullptr : W16(D, W_DOWN);
+  w->out_norm_weight = W16(D, W_OUT_NORM);
+  w->out_weight = W16(D, W_OUT);
+  if (moe) {
+    w->moe_router_weight = W16(D, W_ROUTER);
+    w->moe_gate_blocks = W8(D, W_GB);
+    w->moe_gate_scales = W8(D, W_GS);
+    w->moe_up_blocks = W8(D, W_UB);
+    w->moe_up_scales = W8(D, W_US);
+    w->moe_down_blocks = W8(D, W_DB);
+    w->moe_down_scales = W8(D, W_DS);
+  }
+
+  // Host-side summaries for transformer_print (first/last values).
+  for (int k = 0; k < W_COUNT; k++) {
+    Summary& sm = D->summary[k];
+    if (!D->w[k] || (k == W_OUT && D->tied)) continue;
+    sm.present = true;
+    sm.bytes = pl[k] * (is_global(k) ? 1 : D->L);
+    if (k >= W_GB) continue;
+    uint16_t head[3], tail[3];
+    HIP_CHECK(hipMemcpy(head, D->w[k], sizeof(head), hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(tail, (char*)D->w[k] + sm.bytes - sizeof(tail), sizeof(tail),
+                        hipMemcpyDeviceToHost));
+    for (int i = 0; i < 3; i++) {
+      uint32_t a = (uint32_t)head[i] << 16, b = (uint32_t)tail[i] << 16;
+      memcpy(&sm.first[i], &a, 4);
+      memcpy(&sm.last[i], &b, 4);
+    }
+  }
+
+  // State.
+  const size_t T = TRANSFORMER_CHUNK_MAX_LEN;
+  const size_t wide = H > d ? H : d;
+  D->x = dalloc<float>(T * d);
+  D->xn = dalloc<float>(T * wide);
+  D->q = dalloc<float>(T * D->qd);
+  D->att = dalloc<float>(T * D->qd);
+  D->act = dalloc<float>(T * wide);
+  D->kraw = dalloc<float>(D->kvd);
+  const size_t cache = (size_t)D->L * D->kvh * D->ctx * hd;
+  D->kc = dalloc<float>(cache);
+  D->vc = dalloc<float>(cache);
+  HIP_CHECK(hipMemsetAsync(D->kc, 0, cache * sizeof(float), D->stream));
+  HIP_CHECK(hipMemsetAsync(D->vc, 0, cache * sizeof(float), D->stream));
+  std::vector<float> rope;
+  build_rope_table(c, rope);
+  D->rope = dalloc<float>(rope.size());
+  HIP_CHECK(hipMemcpy(D->rope, rope.data(), rope.size() * sizeof(float), hipMemcpyHostToDevice));
+  D->tok = dalloc<int>(T);
+  D->pos = dalloc<int>(1);
+  D->next = dalloc<int>(1);
+  D->seq_cap = D->ctx + 1;
+  D->seq = dalloc<int>(D->seq_cap);
+  D->seq_len = dalloc<int>(1);
+  D->attn_splits = sg::attention_decode_splits(D->ctx, 64);
+  D->attn_part = dalloc<float>((size_t)D->qh * D->attn_splits * (hd + 2));
+  D->attn_cnt = dalloc<unsigned>(D->qh);
+  HIP_CHECK(hipMemsetAsync(D->attn_cnt, 0, D->qh * sizeof(unsigned), D->stream));
+  D->am_v = dalloc<float>(sg::argmax_blocks());
+  D->am_i = dalloc<int>(sg::argmax_blocks());
+  D->am_cnt = dalloc<unsigned>(1);
+  HIP_CHECK(hipMemsetAsync(D->am_cnt, 0, sizeof(unsigned), D->stream));
+  if (moe) {
+    D->moe_sel = dalloc<int>(T * D->topk);
+    D->moe_w = dalloc<float>(T * D->topk);
+    D->moe_act = dalloc<float>(T * D->topk * H);
+  }
+  HIP_CHECK(hipHostMalloc((void**)&D->h_tok, T * sizeof(int), hipHostMallocDefault));
+  HIP_CHECK(hipHostMalloc((void**)&D->h_pos, sizeof(int), hipHostMallocDefault));
+  HIP_CHECK(hipHostMalloc((void**)&D->h_next, sizeof(int), hipHostMallocDefault));
+  ensure_logits(D, 1);
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+
+  ss->embedding = D->x;
+  ss->mha_q = D->q;
+  ss->mha_att = D->att;
+  ss->ffn_act = D->act;
+  ss->logits = D->logits;
+  ss->cached_count = 0;
+  ss->k_cache = D->kc;
+  ss->v_cache = D->vc;
+  ss->rope_cos_sin = D->rope;
+  return t;
+}
+
+extern "C" void sg_free(transformer_t* t) {
+  if (!t) return;
+  Dev* D = t->device;
+  if (D) {
+    if (D->stream) HIP_CHECK(hipStreamSynchronize(D->stream));
+    harvest(D);
+    for (hipEvent_t e : D->event_pool) HIP_CHECK(hipEventDestroy(e));
+    if (D->graph) HIP_CHECK(hipGraphExecDestroy(D->graph));
+    for (int k = 0; k < W_COUNT; k++) {
+      if (D->w[k] && !(k == W_OUT && D->tied)) HIP_CHECK(hipFree(D->w[k]));
+    }
+    void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
+                    D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part,
+                    D->attn_cnt, D->am_v, D->am_i, D->am_cnt, D->cap_dev, D->cap_final_dev,
+                    D->moe_sel, D->moe_w, D->moe_act};
+    for (void* b : bufs)
+      if (b) HIP_CHECK(hipFree(b));
+    if (D->h_tok) HIP_CHECK(hipHostFree(D->h_tok));
+    if (D->h_pos) HIP_CHECK(hipHostFree(D->h_pos));
+    if (D->h_next) HIP_CHECK(hipHostFree(D->h_next));
+    if (D->stream) HIP_CHECK(hipStreamDestroy(D->stream));
+    delete D;
+  }
+  free(t->config->mrope_section);
+  free(t->config);
+  free(t->weights);
+  free(t->state);
+  free(t);
+}
+
+extern "C" void sg_print(FILE* f, const transformer_t* t) {
+  if (!t) {
+    fprintf(f, "transformer: NULL\n");
+    return;
+  }
+  const transformer_configuration_t* c = t->config;
+  fprintf(f, "Transformer (MI355X, %s):\n- Configuration:\n", sg_version());
+  fprintf(f, "--- embedding_dim:      %zu\n", c->embedding_dim);
+  fprintf(f, "--- head_dim:           %zu\n", c->head_dim);
+  fprintf(f, "--- hidden_dim:         %zu\n", c->hidden_dim);
+  fprintf(f, "--- layer_count:        %zu\n", c->layer_count);
+  fprintf(f, "--- q_head_count:       %zu\n", c->q_head_count);
+  fprintf(f, "--- kv_head_count:      %zu\n", c->kv_head_count);
+  fprintf(f, "--- vocabulary_len:     %zu\n", c->vocabulary_len);
+  fprintf(f, "--- context_len:        %zu\n", c->context_len);
+  fprintf(f, "--- epsilon:            %g\n", c->epsilon);
+  fprintf(f, "--- rope_theta:         %.1f\n", c->rope_theta);
+  fprintf(f, "--- rope_pair_bound     %zu\n", c->rope_pair_bound);
+  fprintf(f, "--- rope_pair_offset    %zu\n", c->rope_pair_offset);
+  fprintf(f, "--- rope_pair_stride    %zu\n", c->rope_pair_stride);
+  fprintf(f, "--- qk_norm:            %s\n", c->qk_norm ? "true" : "false");
+  if (c->expert_count)
+    fprintf(f, "--- experts:            %zu (top-%zu)\n", c->expert_count, c->expert_used_count);
+  fprintf(f, "--- aliased_out_weight: %s\n", c->aliased_out_weight ? "true" : "false");
+  fprintf(f, "- Weights (HBM):\n");
+  const Dev* D = t->device;
+  double total = 0, gb = 1024.0 * 1024.0 * 1024.0;
+  for (int k = 0; k < W_COUNT; k++) {
+    const Summary& sm = D->summary[k];
+    if (!sm.present) continue;
+    total += (double)sm.bytes;
+    if (k >= W_GB) {
+      fprintf(f, "--- %15s (%7.4f GB)\n", kClassName[k], sm.bytes / gb);
+      continue;
+    }
+    fprintf(f, "--- %15s (%7.4f GB): [ %6.3f %6.3f %6.3f ... %6.3f %6.3f %6.3f ]\n",
+            k == W_Q ? "mha_qkv" : kClassName[k], sm.bytes / gb, sm.first[0], sm.first[1],
+            sm.first[2], sm.last[0], sm.last[1], sm.last[2]);
+  }
+  if (c->aliased_out_weight) fprintf(f, "--- %15s (%7.4f GB): alias to embedding\n", "out", 0.0);
+  fprintf(f, "---  total size:%7.4f GB\n", total / gb);
+}
+
+extern "C" void sg_predict(transformer_t* t, size_t T, const int* token, size_t lc,
+                           float* logits) {
+  predict_device(t, T, token, lc, logits);
+}
+
+extern "C" int sg_predict_argmax(transformer_t* t, size_t T, const int* token) {
+  Dev* D = t->device;
+  predict_device(t, T, token, 1, nullptr);
+  argmax_to(D, D->logits, false, false);
+  HIP_CHECK(hipMemcpyAsync(D->h_next, D->next, sizeof(int), hipMemcpyDeviceToHost, D->stream));
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  return *D->h_next;
+}
+
+extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* token,
+                                     size_t steps, int eos, int* out,
+                                     transformer_timing_t* timing) {
+  Dev* D = t->device;
+  if (t->state->cached_count + T + (steps - 1) > (size_t)D->ctx)
+    ST_DIE("context length exhausted");
+  HIP_CHECK(hipMemsetAsync(D->seq_len, 0, sizeof(int), D->stream));
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  const double t0 = now_s();
+  predict_device(t, T, token, 1, nullptr);
+  argmax_to(D, D->logits, true, false);
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  harvest(D);
+  const double t1 = now_s();
+  size_t produced = 1;
+  bool stop = false;
+  if (eos >= 0) {
+    HIP_CHECK(hipMemcpy(D->h_next, D->next, sizeof(int), hipMemcpyDeviceToHost));
+    stop = *D->h_next == eos;
+  }
+  if (steps > 1 && !stop) {
+    if (!D->prof) build_decode_graph(D);
+    set_pos(D, t->state->cached_count);
+    for (size_t i = 1; i < steps && !stop; i++) {
+      if (D->prof) {
+        // Eager step (events around every launch); same kernels as the graph.
+        D->host_pos = t->state->cached_count + produced - 1;
+        forward_chunk(D, D->next, 1, 1);
+        argmax_to(D, D->logits, true, true);
+        HIP_CHECK(hipStreamSynchronize(D->stream));
+        harvest(D);
+      } else {
+        HIP_CHECK(hipGraphLaunch(D->graph, D->stream));
+      }
+      produced++;
+      if (eos >= 0) {
+        HIP_CHECK(hipMemcpyAsync(D->h_next, D->next, sizeof(int), hipMemcpyDeviceToHost, D->stream));
+        HIP_CHECK(hipStreamSynchronize(D->stream));
+        stop = *D->h_next == eos;
+      }
+    }
+    HIP_CHECK(hipStreamSynchronize(D->stream));
+    t->state->cached_count += produced - 1;
+  }
+  const double t2 = now_s();
+  HIP_CHECK(hipMemcpy(out, D->seq, produced * sizeof(int), hipMemcpyDeviceToHost));
+  if (timing) {
+    timing->prefill_s = t1 - t0;
+    timing->decode_s = t2 - t1;
+    timing->decode_count = produced - 1;
+  }
+  return produced;
+}
+
+extern "C" void sg_reset(transformer_t* t) { t->state->cached_count = 0; }
+
+extern "C" void sg_capture_hidden(transformer_t* t, float* out, float* out_final) {
+  Dev* D = t->device;
+  if (!out || !out_final) {
+    D->cap_out = nullptr;
+    D->cap_final = nullptr;
+    return;
+  }
+  if (!D->cap_dev) {
+    D->cap_dev = dalloc<float>((size_t)D->L * TRANSFORMER_CHUNK_MAX_LEN * D->d);
+    D->cap_final_dev = dalloc<float>((size_t)TRANSFORMER_CHUNK_MAX_LEN * D->d);
+  }
+  D->cap_out = out;
+  D->cap_final = out_final;
+}
+
+extern "C" int sg_set_prefill_precision(transformer_t* t, int mode) {
+  if (mode != sg::GEMM_SPLIT2 && mode != sg::GEMM_BF16) ST_DIE("unknown prefill precision");
+  const int old = t->device->precision;
+  t->device->precision = mode;
+  return old;
+}
+
+extern "C" void sg_profile(transformer_t* t, int enable) {
+  Dev* D = t->device;
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  harvest(D);
+  if (enable) memset(D->stat, 0, sizeof(D->stat));
+  D->prof = enable != 0;
+}
+
+extern "C" int sg_profile_read(transformer_t* t, int cls, transformer_kernel_stat_t* out) {
+  if (cls < 0 || cls >= TRANSFORMER_K_CLASS_COUNT) return -1;
+  *out = t->device->stat[cls];
+  return 0;
+}
+
+extern "C" const char* sg_version(void) {
+  return "strasgpt-hip gfx950 (GEMV bf16/fp32, MFMA 16x16x32 bf16x2, split-K decode attention)";
+}

@@ -1,0 +1,324 @@
+"""Pins of the CPU oracle (oracle/): closed forms, float64 restatements,
+planted mistakes, and the golden fixtures written by the reference C
+sources (tests/golden/make_golden.py)."""
+import ctypes
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN_DIR, MODEL_SEED, PROMPT_SEED
+
+from oracle import oracle as orc
+from strasgpt_amd import synth
+
+pytestmark = pytest.mark.skipif(not orc.oracle_available(), reason="oracle not built")
+
+
+def lib():
+    return orc.load_lib()
+
+
+def bf16_to_f32_np(u16):
+    return (np.asarray(u16, np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_np(x):
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def test_bf16_exhaustive():
+    L = lib()
+    codes = np.arange(65536, dtype=np.uint32)
+    ref = (codes << 16).view(np.float32)
+    got = np.array([L.oracle_bf16_to_f32(int(c)) for c in codes[::257]], np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), ref[::257].view(np.uint32))
+
+
+def test_mxfp4_exhaustive():
+    """E2M1 x E8M0 against the OCP MX closed form, all 16 x 256 pairs."""
+    L = lib()
+    mag = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    for s in range(256):
+        for c in range(16):
+            got = L.oracle_mxfp4_value(c, s)
+            if s == 255:
+                assert np.isnan(got)
+                continue
+            want = (-1.0 if c & 8 else 1.0) * mag[c & 7] * 2.0 ** (s - 127)
+            assert np.float32(got) == np.float32(want), (c, s)
+
+
+def test_mxfp4_dequant_layout():
+    """Element 2i is the low nibble of byte i; one scale per 32 values."""
+    L = lib()
+    rng = np.random.default_rng(0)
+    blocks = rng.integers(0, 256, 64, dtype=np.uint8)
+    scales = np.array([120, 125, 119, 123], np.uint8)
+    out = np.zeros(128, np.float32)
+    L.oracle_mxfp4_dequant(blocks.ctypes.data, scales.ctypes.data, 128, orc.fptr(out))
+    mag = np.array([0, .5, 1, 1.5, 2, 3, 4, 6])
+    codes = np.empty(128, np.uint8)
+    codes[0::2] = blocks & 15
+    codes[1::2] = blocks >> 4
+    want = np.where(codes & 8, -1.0, 1.0) * mag[codes & 7] * 2.0 ** (scales.repeat(32).astype(np.float64) - 127)
+    np.testing.assert_array_equal(out, want.astype(np.float32))
+
+
+def dot_model(a, w):
+    """Reference AVX2 dot order (source/transformer.c:1095-1167) in float32."""
+    a = np.asarray(a, np.float32)
+    wf = bf16_to_f32_np(w)
+    acc = np.zeros((4, 8), np.float32)
+    for i in range(0, len(a), 32):
+        blk = (a[i:i + 32].astype(np.float64) * wf[i:i + 32]).reshape(4, 8)
+        # FMA: exact product, one rounding with the accumulator
+        acc = (acc.astype(np.float64) + blk).astype(np.float32)
+    v = (acc[0] + acc[1]) + (acc[2] + acc[3])
+    s = v[:4] + v[4:]
+    return (s[0] + s[1]) + (s[2] + s[3])
+
+
+def test_dot_matches_fma_model_and_float64():
+    L = lib()
+    rng = np.random.default_rng(1)
+    for n in (32, 64, 2048, 2880):
+        a = rng.standard_normal(n).astype(np.float32)
+        w = f32_to_bf16_np(rng.standard_normal(n) * 0.02)
+        got = L.oracle_dot_bf16(n, orc.fptr(a), w.ctypes.data)
+        exact = float(np.dot(a.astype(np.float64), bf16_to_f32_np(w).astype(np.float64)))
+        assert np.float32(got) == dot_model(a, w)
+        assert abs(got - exact) <= 1e-5 * (np.abs(a) @ np.abs(bf16_to_f32_np(w))) + 1e-30
+
+
+def test_dot_planted_transpose_fails():
+    """A transposed weight row (a plausible indexing mistake) is detected."""
+    L = lib()
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal(64).astype(np.float32)
+    w = f32_to_bf16_np(rng.standard_normal(64))
+    got = L.oracle_dot_bf16(64, orc.fptr(a), w.ctypes.data)
+    wrong = float(np.dot(a, bf16_to_f32_np(w[::-1])))
+    assert abs(got - wrong) > 1e-3
+
+
+def test_rmsnorm_float64():
+    L = lib()
+    rng = np.random.default_rng(3)
+    for n in (16, 128, 2560):
+        x = rng.standard_normal(n).astype(np.float32)
+        w = f32_to_bf16_np(1.0 + 0.1 * rng.standard_normal(n))
+        y = np.zeros(n, np.float32)
+        L.oracle_rmsnorm(n, orc.fptr(y), orc.fptr(x), w.ctypes.data, ctypes.c_float(1e-5))
+        xd = x.astype(np.float64)
+        want = xd / np.sqrt(np.mean(xd * xd) + 1e-5) * bf16_to_f32_np(w)
+        np.testing.assert_allclose(y, want, rtol=2e-6, atol=1e-7)
+        # planted mistake: forgetting the mean (sum instead) is far off
+        assert np.abs(y - xd / np.sqrt(np.sum(xd * xd)) * bf16_to_f32_np(w)).max() > 1e-2
+
+
+@pytest.mark.parametrize("interleaved", [0, 1])
+def test_rope_table_float64(interleaved):
+    L = lib()
+    ctx, hd, theta = 40, 16, 10000.0
+    out = np.zeros((ctx, hd), np.float32)
+    L.oracle_rope_table(ctx, hd, ctypes.c_float(theta), interleaved, orc.fptr(out))
+    pos = np.arange(ctx)[:, None].astype(np.float64)
+    if interleaved:
+        j = np.arange(0, hd, 2)
+        ang = pos / theta ** (j / hd)
+        np.testing.assert_allclose(out[:, 0::2], np.cos(ang), atol=2e-5)
+        np.testing.assert_allclose(out[:, 1::2], np.sin(ang), atol=2e-5)
+    else:
+        j = np.arange(hd // 2)
+        ang = pos / theta ** (2 * j / hd)
+        np.testing.assert_allclose(out[:, :hd // 2], np.cos(ang), atol=2e-5)
+        np.testing.assert_allclose(out[:, hd // 2:], np.sin(ang), atol=2e-5)
+
+
+def test_attention_row_float64():
+    L = lib()
+    rng = np.random.default_rng(4)
+    hd, n = 32, 17
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal((n, hd)).astype(np.float32)
+    v = rng.standard_normal((n, hd)).astype(np.float32)
+    out = np.zeros(hd, np.float32)
+    L.oracle_attention_row(hd, n, orc.fptr(q), orc.fptr(k), orc.fptr(v), orc.fptr(out))
+    s = k.astype(np.float64) @ q / np.sqrt(hd)
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    np.testing.assert_allclose(out, p @ v, rtol=1e-5, atol=1e-6)
+    # single key: output is that key's value exactly
+    L.oracle_attention_row(hd, 1, orc.fptr(q), orc.fptr(k), orc.fptr(v), orc.fptr(out))
+    np.testing.assert_allclose(out, v[0], rtol=0, atol=1e-7)
+
+
+def test_argmax_semantics():
+    L = lib()
+    x = np.array([1.0, 3.0, 2.0, 3.0], np.float32)
+    assert L.oracle_argmax(orc.fptr(x), 4) == 1  # first maximum
+    x = np.array([np.nan, 5.0, 1.0], np.float32)
+    assert L.oracle_argmax(orc.fptr(x), 3) == 0  # NaN at 0 is never replaced
+    x = np.array([1.0, np.nan, 5.0], np.float32)
+    assert L.oracle_argmax(orc.fptr(x), 3) == 2
+
+
+def test_topk_softmax():
+    L = lib()
+    lg = np.array([0.5, 2.0, -1.0, 2.0, 1.5], np.float32)
+    idx = (ctypes.c_int * 3)()
+    w = np.zeros(3, np.float32)
+    L.oracle_topk_softmax(5, orc.fptr(lg), 3, idx, orc.fptr(w))
+    assert list(idx) == [1, 3, 4]  # ties to the lowest index, descending order
+    e = np.exp(np.array([2.0, 2.0, 1.5]) - 2.0)
+    np.testing.assert_allclose(w, e / e.sum(), rtol=1e-6)
+
+
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk"])
+def test_oracle_matches_reference_golden(name, model_dir):
+    """The oracle reproduces the reference C run of tests/golden/<name>.npz."""
+    g = np.load(os.path.join(GOLDEN_DIR, f"{name}.npz"))
+    d = model_dir(name)
+    digest = hashlib.sha256(open(os.path.join(d, "model.safetensors"), "rb").read()).hexdigest()
+    assert digest == str(g["sha256"]), "synthetic model generator drifted"
+    prompt = [int(v) for v in g["prompt"]]
+    assert prompt == synth.prompt_tokens(synth.shape(name).vocab, len(prompt), PROMPT_SEED)
+    om = orc.OracleModel(d, threads=4)
+    logits, hid, fin = om.predict(prompt, capture=True)
+    np.testing.assert_allclose(logits[0], g["logits"], rtol=1e-4, atol=1e-4)
+    last = g["hidden"].shape[1]
+    np.testing.assert_allclose(fin[-last:], g["hidden"][-1], rtol=1e-4, atol=1e-4)
+    # per-layer normalised residual stream (norm weights are 1.0)
+    for l in range(om.layers - 1):
+        xl = hid[l][-last:].astype(np.float64)
+        xn = xl / np.sqrt(np.mean(xl * xl, axis=1, keepdims=True) + om.config.epsilon)
+        np.testing.assert_allclose(xn, g["hidden"][l], rtol=1e-4, atol=1e-4)
+    om.reset()
+    assert om.generate(prompt, len(g["generated"])) == [int(v) for v in g["generated"]]
+
+
+def test_oracle_chunk_invariance(model_dir):
+    """Prefill in one call == prefill split across calls (reference chunk
+    independence, source/transformer.c:1643-1726)."""
+    d = model_dir("tiny-llama")
+    om = orc.OracleModel(d, threads=2)
+    prompt = synth.prompt_tokens(256, 8, 11)
+    a = om.predict(prompt)
+    om.reset()
+    om.predict(prompt[:5])
+    b = om.predict(prompt[5:])
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_oracle_moe_float64(model_dir):
+    """MoE semantics (no reference counterpart) against a float64 numpy
+    restatement on the tiny MoE model."""
+    d = model_dir("tiny-moe")
+    om = orc.OracleModel(d, threads=2)
+    prompt = synth.prompt_tokens(256, 3, 5)
+    got = om.predict(prompt)[0]
+    want = numpy_forward(d, prompt)
+    np.testing.assert_allclose(got, want, rtol=2e-4, atol=2e-4)
+
+
+def numpy_forward(model_dir, prompt):
+    """float64 restatement of the forward pass (dense or MoE), last logits."""
+    cfg = orc.read_config(model_dir)
+    tab = {n: (p, o, s) for n, p, o, s in orc.tensor_table(model_dir)}
+    meta = {n: (t, shp) for n, t, shp, *_ in synth.tensor_table(model_dir)}
+
+    def get(name):
+        p, o, s = tab[name]
+        dt, shp = meta[name]
+        raw = np.fromfile(p, np.uint8, s, offset=o)
+        if dt == "BF16":
+            return bf16_to_f32_np(raw.view(np.uint16)).astype(np.float64).reshape(shp)
+        return raw.reshape(shp)
+
+    d = cfg["hidden_size"]; hd = cfg["head_dim"]; L = cfg["num_hidden_layers"]
+    qh = cfg["num_attention_heads"]; kvh = cfg["num_key_value_heads"]
+    eps = cfg["rms_norm_eps"]; theta = cfg["rope_theta"]
+    E = cfg.get("num_local_experts", 0); K = cfg.get("num_experts_per_tok", 0)
+    T = len(prompt)
+
+    def rms(x, w):
+        return x / np.sqrt(np.mean(x * x, -1, keepdims=True) + eps) * w
+
+    def rope(v, pos):
+        half = hd // 2
+        j = np.arange(half)
+        ang = pos[:, None] / theta ** (2 * j / hd)
+        c, s_ = np.cos(ang), np.sin(ang)
+        v0, v1 = v[..., :half].copy(), v[..., half:].copy()
+        out = v.copy()
+        out[..., :half] = v0 * c[:, None] - v1 * s_[:, None]
+        out[..., half:] = v0 * s_[:, None] + v1 * c[:, None]
+        return out
+
+    def mx(blocks, scales):
+        mag = np.array([0, .5, 1, 1.5, 2, 3, 4, 6])
+        codes = np.stack([blocks & 15, blocks >> 4], -1).reshape(*blocks.shape[:-1], 32)
+        val = np.where(codes & 8, -1.0, 1.0) * mag[codes & 7]
+        val = val * 2.0 ** (scales[..., None].astype(np.float64) - 127)
+        return val.reshape(*blocks.shape[:-2], -1)
+
+    emb = get("model.embed_tokens.weight")
+    x = emb[prompt]
+    pos = np.arange(T, dtype=np.float64)
+    for l in range(L):
+        pre = f"model.layers.{l}."
+        xn = rms(x, get(pre + "input_layernorm.weight"))
+        q = (xn @ get(pre + "self_attn.q_proj.weight").T).reshape(T, qh, hd)
+        k = (xn @ get(pre + "self_attn.k_proj.weight").T).reshape(T, kvh, hd)
+        v = (xn @ get(pre + "self_attn.v_proj.weight").T).reshape(T, kvh, hd)
+        q, k = rope(q, pos), rope(k, pos)
+        att = np.zeros((T, qh, hd))
+        for h in range(qh):
+            kv = h // (qh // kvh)
+            s = q[:, h] @ k[:, kv].T / np.sqrt(hd)
+            s = np.where(np.tril(np.ones((T, T))) > 0, s, -np.inf)
+            p = np.exp(s - s.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            att[:, h] = p @ v[:, kv]
+        x = x + att.reshape(T, -1) @ get(pre + "self_attn.o_proj.weight").T
+        xn = rms(x, get(pre + "post_attention_layernorm.weight"))
+        if E:
+            r = xn @ get(pre + "mlp.router.weight").T
+            G = mx(get(pre + "mlp.experts.gate_proj_blocks"), get(pre + "mlp.experts.gate_proj_scales"))
+            U = mx(get(pre + "mlp.experts.up_proj_blocks"), get(pre + "mlp.experts.up_proj_scales"))
+            D = mx(get(pre + "mlp.experts.down_proj_blocks"), get(pre + "mlp.experts.down_proj_scales"))
+            out = np.zeros_like(x)
+            for t in range(T):
+                sel = np.argsort(-r[t], kind="stable")[:K]
+                w = np.exp(r[t, sel] - r[t, sel].max())
+                w /= w.sum()
+                for j, e in enumerate(sel):
+                    g = G[e] @ xn[t]
+                    u = U[e] @ xn[t]
+                    a = g / (1 + np.exp(-g)) * u
+                    out[t] += w[j] * (D[e] @ a)
+            x = x + out
+        else:
+            g = xn @ get(pre + "mlp.gate_proj.weight").T
+            u = xn @ get(pre + "mlp.up_proj.weight").T
+            x = x + (g / (1 + np.exp(-g)) * u) @ get(pre + "mlp.down_proj.weight").T
+    xn = rms(x, get("model.norm.weight"))
+    out_w = get("lm_head.weight") if "lm_head.weight" in tab else emb
+    return xn[-1] @ out_w.T
+
+
+def test_oracle_dense_float64(model_dir):
+    d = model_dir("tiny-qwen")
+    om = orc.OracleModel(d, threads=2)
+    prompt = synth.prompt_tokens(300, 4, 9)
+    # tiny-qwen has QK-norm: the float64 restatement above has no QK-norm,
+    # so compare on tiny-llama instead and check tiny-qwen through golden.
+    d2 = model_dir("tiny-llama")
+    om2 = orc.OracleModel(d2, threads=2)
+    p2 = synth.prompt_tokens(256, 5, 9)
+    np.testing.assert_allclose(om2.predict(p2)[0], numpy_forward(d2, p2), rtol=2e-4, atol=2e-4)
+    assert om.predict(prompt).shape == (1, 300)
