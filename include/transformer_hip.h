@@ -31,7 +31,9 @@ typedef struct transformer_timing {
  * next token never leaves HBM between steps (decode steps are replayed
  * from a captured HIP graph). Writes step_count token ids to out. Stops
  * early (like the reference) when eos_token_id >= 0 is produced; returns
- * the number of ids written. timing may be NULL. */
+ * the number of ids written. timing may be NULL. With the environment
+ * variable STRASGPT_DECODE_GRAPH=0 the same kernels are launched eagerly
+ * per step instead (for tools that do not follow graph launches). */
 size_t transformer_generate_greedy(
     transformer_t* transformer,
     size_t token_count,

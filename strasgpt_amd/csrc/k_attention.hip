@@ -8,8 +8,9 @@
 // sum per query row), P kept in LDS for the P.V product.
 //
 // Decode: split-K over the cached positions ("flash decoding"): one block
-// per (64-key chunk, q head) writes (max, sum, partial output); the last
-// block of a head to finish (device-scope counter) combines the chunks.
+// per (64-key chunk, q head) writes (max, sum, partial output); a second
+// small kernel combines the chunks of each head (the kernel boundary is
+// the only synchronisation: no device-wide fences).
 // The block also applies this step's QK RMSNorm + RoPE to q and to the new
 // key (read raw from the QKV projection), and one block per KV head writes
 // the processed key into the cache.
@@ -199,18 +200,19 @@ __device__ void norm_rope_wave(const float* src, const uint16_t* nw, float eps,
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
   constexpr int CH = 64;
-  __shared__ float qs[HD], kn[HD], sc[CH];
-  __shared__ float red[256 / HD > 0 ? 256 / HD : 1][HD];
+  __shared__ __attribute__((aligned(16))) float qs[HD];
+  __shared__ __attribute__((aligned(16))) float kn[HD];
+  __shared__ float sc[CH];
+  __shared__ float red[256 / HD][HD];
   __shared__ float stat[2];
-  __shared__ bool last;
 
   const int split = blockIdx.x, head = blockIdx.y;
   const int G = p.q_heads / p.kv_heads, kvh = head / G;
   const int P = *p.pos, total = P + 1;
   const int nsplit = (total + CH - 1) / CH;
   if (split >= nsplit) return;
-  const int s0 = split * CH, s1 = min(s0 + CH, total);
-  const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const int s0 = split * CH, s1 = min(s0 + CH, total), n = s1 - s0;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const float* cs = p.rope + (size_t)P * HD;
   const bool has_new = s1 == total;
 
@@ -224,23 +226,32 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
   const float* kbase = p.kcache + (size_t)kvh * p.ctx * HD;
   const float* vbase = p.vcache + (size_t)kvh * p.ctx * HD;
   if (has_new && head % G == 0) {
-    for (int e = threadIdx.x; e < HD; e += 256) p.kcache_w[((size_t)kvh * p.ctx + P) * HD + e] = kn[e];
+    for (int e = tid; e < HD; e += 256) p.kcache_w[((size_t)kvh * p.ctx + P) * HD + e] = kn[e];
   }
 
-  // Scores: 16 lanes per key.
-  const int g = threadIdx.x / 16, l16 = threadIdx.x % 16;
-  constexpr int PER = HD / 16;
-  const float scale = sqrtf((float)HD);
-  for (int s = s0 + g; s < s1; s += 16) {
-    const float* kr = s == P ? kn : kbase + (size_t)s * HD;
+  // Scores: 4 lanes per key, each a contiguous quarter of the head
+  // (coalesced 128-bit loads of consecutive key rows).
+  {
+    const int key = tid / 4, sub = tid % 4;
+    constexpr int Q4 = HD / 4;
     float a = 0.0f;
+    const int s = s0 + key;
+    if (key < n) {
+      const float* kr = s == P ? kn : kbase + (size_t)s * HD;
 #pragma unroll
-    for (int e = 0; e < PER; e++) a = fmaf(qs[l16 * PER + e], kr[l16 * PER + e], a);
-    a = group_sum<16>(a);
-    if (l16 == 0) sc[s - s0] = a / scale;
+      for (int e = sub * Q4; e < (sub + 1) * Q4; e += 4) {
+        const float4 kv = *(const float4*)(kr + e);
+        const float4 qv = *(const float4*)(qs + e);
+        a = fmaf(qv.x, kv.x, a);
+        a = fmaf(qv.y, kv.y, a);
+        a = fmaf(qv.z, kv.z, a);
+        a = fmaf(qv.w, kv.w, a);
+      }
+    }
+    a = group_sum<4>(a);
+    if (sub == 0 && key < n) sc[key] = a / sqrtf((float)HD);
   }
   __syncthreads();
-  const int n = s1 - s0;
   if (wave == 0) {
     const float v = lane < n ? sc[lane] : -INFINITY;
     const float mx = wave_max(v);
@@ -253,45 +264,45 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-  constexpr int KG = 256 / HD > 0 ? 256 / HD : 1;
-  const int d = threadIdx.x % HD, kg = threadIdx.x / HD;
-  if (kg < KG) {
+  constexpr int KG = 256 / HD;
+  const int d = tid % HD, kg = tid / HD;
+  {
     float a = 0.0f;
-    for (int s = s0 + kg; s < s1; s += KG) a = fmaf(sc[s - s0], vbase[(size_t)s * HD + d], a);
+#pragma unroll 8
+    for (int s = kg; s < n; s += KG) a = fmaf(sc[s], vbase[(size_t)(s0 + s) * HD + d], a);
     red[kg][d] = a;
   }
   __syncthreads();
   float* part = p.partial + ((size_t)head * p.splits + split) * (HD + 2);
-  if (threadIdx.x < HD) {
+  if (tid < HD) {
     float a = 0.0f;
 #pragma unroll
-    for (int k = 0; k < KG; k++) a += red[k][threadIdx.x];
-    part[2 + threadIdx.x] = a;
+    for (int k = 0; k < KG; k++) a += red[k][tid];
+    part[2 + tid] = a;
   }
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     part[0] = stat[0];
     part[1] = stat[1];
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = atomicAdd(&p.counter[head], 1u) == (unsigned)nsplit - 1;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
+}
+
+// Combines the per-chunk (max, sum, partial output) of one head:
+// M = max m_i, out = sum_i o_i e^(m_i - M) / sum_i l_i e^(m_i - M).
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_decode_combine_kernel(AttnParams p) {
+  const int head = blockIdx.x, d = threadIdx.x;
+  const int nsplit = (*p.pos + 1 + 63) / 64;
   const float* pb = p.partial + (size_t)head * p.splits * (HD + 2);
   float M = -INFINITY;
-  for (int i = 0; i < nsplit; i++) M = fmaxf(M, __builtin_nontemporal_load(&pb[(size_t)i * (HD + 2)]));
-  if (threadIdx.x < HD) {
-    float L = 0.0f, o = 0.0f;
-    for (int i = 0; i < nsplit; i++) {
-      const float* q = pb + (size_t)i * (HD + 2);
-      const float w = expf(__builtin_nontemporal_load(&q[0]) - M);
-      L = fmaf(__builtin_nontemporal_load(&q[1]), w, L);
-      o = fmaf(__builtin_nontemporal_load(&q[2 + threadIdx.x]), w, o);
-    }
-    p.out[(size_t)head * HD + threadIdx.x] = o / L;
+  for (int i = 0; i < nsplit; i++) M = fmaxf(M, pb[(size_t)i * (HD + 2)]);
+  float L = 0.0f, o = 0.0f;
+  for (int i = 0; i < nsplit; i++) {
+    const float* q = pb + (size_t)i * (HD + 2);
+    const float w = expf(q[0] - M);
+    L = fmaf(q[1], w, L);
+    o = fmaf(q[2 + d], w, o);
   }
-  if (threadIdx.x == 0) p.counter[head] = 0u;
+  p.out[(size_t)head * HD + d] = o / L;
 }
 
 }  // namespace
@@ -317,10 +328,16 @@ void attention_decode(const AttnParams& p, hipStream_t s) {
   if (p.splits != attention_decode_splits(p.ctx, p.chunk)) ST_DIE("decode split count mismatch");
   dim3 grid(p.splits, p.q_heads);
   switch (p.hd) {
-    case 16: hipLaunchKernelGGL(attn_decode_kernel<16>, grid, dim3(256), 0, s, p); break;
-    case 32: hipLaunchKernelGGL(attn_decode_kernel<32>, grid, dim3(256), 0, s, p); break;
-    case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, s, p); break;
-    case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, s, p); break;
+#define DECODE_CASE(HD)                                                                 \
+  case HD:                                                                              \
+    hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, s, p);               \
+    hipLaunchKernelGGL(attn_decode_combine_kernel<HD>, dim3(p.q_heads), dim3(HD), 0, s, p); \
+    break;
+    DECODE_CASE(16)
+    DECODE_CASE(32)
+    DECODE_CASE(64)
+    DECODE_CASE(128)
+#undef DECODE_CASE
     default: ST_DIE("attention supports head_dim 16, 32, 64 or 128");
   }
   HIP_CHECK(hipGetLastError());

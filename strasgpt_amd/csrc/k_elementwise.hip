@@ -80,10 +80,26 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(ArgmaxParams p) {
+// Per-block (value, index) of the best element of a contiguous slice.
+__device__ void block_best(float& bv, int& bi, float* sv, int* si) {
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (threadIdx.x < st &&
+        better(sv[threadIdx.x + st], si[threadIdx.x + st], sv[threadIdx.x], si[threadIdx.x])) {
+      sv[threadIdx.x] = sv[threadIdx.x + st];
+      si[threadIdx.x] = si[threadIdx.x + st];
+    }
+    __syncthreads();
+  }
+  bv = sv[0];
+  bi = si[0];
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(ArgmaxParams p) {
   __shared__ float sv[256];
   __shared__ int si[256];
-  __shared__ bool last;
   const int n = p.n;
   const int per = (n + gridDim.x - 1) / gridDim.x;
   const int lo = blockIdx.x * per, hi = min(n, lo + per);
@@ -96,49 +112,30 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxParams p) {
       bi = i;
     }
   }
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if (threadIdx.x < st && better(sv[threadIdx.x + st], si[threadIdx.x + st], sv[threadIdx.x], si[threadIdx.x])) {
-      sv[threadIdx.x] = sv[threadIdx.x + st];
-      si[threadIdx.x] = si[threadIdx.x + st];
-    }
-    __syncthreads();
-  }
+  block_best(bv, bi, sv, si);
   if (threadIdx.x == 0) {
-    p.part_v[blockIdx.x] = sv[0];
-    p.part_i[blockIdx.x] = si[0];
-    __threadfence();
-    last = atomicAdd(p.counter, 1u) == gridDim.x - 1;
+    p.part_v[blockIdx.x] = bv;
+    p.part_i[blockIdx.x] = bi;
   }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  bv = -INFINITY;
-  bi = n;
-  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) {
-    const float v = __builtin_nontemporal_load(&p.part_v[b]);
-    const int i = __builtin_nontemporal_load(&p.part_i[b]);
-    if (better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(ArgmaxParams p, int parts) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int n = p.n;
+  float bv = -INFINITY;
+  int bi = n;
+  for (int b = threadIdx.x; b < parts; b += 256) {
+    if (better(p.part_v[b], p.part_i[b], bv, bi)) {
+      bv = p.part_v[b];
+      bi = p.part_i[b];
     }
   }
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if (threadIdx.x < st && better(sv[threadIdx.x + st], si[threadIdx.x + st], sv[threadIdx.x], si[threadIdx.x])) {
-      sv[threadIdx.x] = sv[threadIdx.x + st];
-      si[threadIdx.x] = si[threadIdx.x + st];
-    }
-    __syncthreads();
-  }
+  block_best(bv, bi, sv, si);
   if (threadIdx.x == 0) {
-    int best = si[0];
     // Sequential-scan semantics: a NaN at index 0 is never replaced, and
     // when nothing compares greater than element 0 the answer is 0.
+    int best = bi;
     if (best >= n || p.x[0] != p.x[0]) best = 0;
     *p.out = best;
     if (p.seq) {
@@ -147,7 +144,6 @@ __global__ __launch_bounds__(256) void argmax_kernel(ArgmaxParams p) {
       *p.seq_len = k + 1;
     }
     if (p.pos_inc) *p.pos_inc += 1;
-    *p.counter = 0u;
   }
 }
 
@@ -184,7 +180,8 @@ int argmax_blocks() { return kArgmaxBlocks; }
 void argmax(const ArgmaxParams& p, hipStream_t s) {
   if (p.n <= 0) ST_DIE("argmax needs n > 0");
   const int blocks = p.n < kArgmaxBlocks * 256 ? (p.n + 255) / 256 : kArgmaxBlocks;
-  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, p, blocks);
   HIP_CHECK(hipGetLastError());
 }
 

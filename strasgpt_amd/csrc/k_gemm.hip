@@ -228,6 +228,20 @@ void dispatch(const GemmParams& p, int epi, hipStream_t s) {
 
 }  // namespace
 
+int gemm_variant_count() { return 2; }
+
+void gemm_variant(const GemmParams& p, int prec, int v, hipStream_t s) {
+  if (p.K % BK) ST_DIE("GEMM needs K to be a multiple of 32");
+  if (prec == GEMM_SPLIT2) {
+    if (v == 0) launch<128, 128, GEMM_STORE, GEMM_SPLIT2>(p, s);
+    else launch<64, 64, GEMM_STORE, GEMM_SPLIT2>(p, s);
+  } else {
+    if (v == 0) launch<128, 128, GEMM_STORE, GEMM_BF16>(p, s);
+    else launch<64, 64, GEMM_STORE, GEMM_BF16>(p, s);
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
 void gemm(const GemmParams& p, int epi, int prec, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) ST_DIE("GEMM needs M, N > 0");
   if (p.K <= 0 || p.K % BK != 0) ST_DIE("GEMM needs K to be a positive multiple of 32");

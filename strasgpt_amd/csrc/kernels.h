@@ -106,7 +106,6 @@ struct AttnParams {
   const float* rope;
   int pair_bound, pair_offset, pair_stride;
   float* partial;        // [q_heads][splits][hd + 2]
-  unsigned* counter;     // [q_heads], zero on entry, left zero on exit
   int chunk, splits;
 };
 void attention_prefill(const AttnParams& p, hipStream_t s);
@@ -114,15 +113,14 @@ void attention_decode(const AttnParams& p, hipStream_t s);
 int attention_decode_splits(int ctx, int chunk);
 
 // ------------------------------------------------------------- argmax --
-// First index of the maximum (reference source/sampler.c:92-102). The last
-// block to finish writes out[0], appends to seq[*seq_len] (if seq) and
-// bumps *pos_inc (if given) so that a replayed decode step advances.
+// First index of the maximum (reference source/sampler.c:92-102): block
+// partials, then one block writes out[0], appends to seq[*seq_len] (if seq)
+// and bumps *pos_inc (if given) so that a replayed decode step advances.
 struct ArgmaxParams {
   const float* x;
   int n;
   float* part_v;   // [blocks]
   int* part_i;     // [blocks]
-  unsigned* counter;
   int* out;        // next token
   int* seq;        // token log or null
   int* seq_len;    // device counter or null

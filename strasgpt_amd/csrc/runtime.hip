@@ -130,15 +130,14 @@ struct transformer_device {
   float *kraw = nullptr, *logits = nullptr;
   int logits_rows = 0;
   size_t host_pos = 0;  // host mirror of *pos (profiling byte counts)
+  bool use_graph = true;  // STRASGPT_DECODE_GRAPH=0: eager decode steps
   float *kc = nullptr, *vc = nullptr, *rope = nullptr;
   int *tok = nullptr, *pos = nullptr, *next = nullptr, *seq = nullptr, *seq_len = nullptr;
   int seq_cap = 0;
   float* attn_part = nullptr;
-  unsigned* attn_cnt = nullptr;
   int attn_splits = 0;
   float* am_v = nullptr;
   int* am_i = nullptr;
-  unsigned* am_cnt = nullptr;
   int* h_tok = nullptr;
   int* h_pos = nullptr;
   int* h_next = nullptr;
@@ -407,7 +406,6 @@ void layer_decode(Dev* D, int l) {
   a.pair_offset = D->po;
   a.pair_stride = D->pst;
   a.partial = D->attn_part;
-  a.counter = D->attn_cnt;
   a.chunk = 64;
   a.splits = D->attn_splits;
   {
@@ -630,7 +628,6 @@ void argmax_to(Dev* D, const float* row, bool log_seq, bool bump_pos) {
   p.n = D->V;
   p.part_v = D->am_v;
   p.part_i = D->am_i;
-  p.counter = D->am_cnt;
   p.out = D->next;
   p.seq = log_seq ? D->seq : nullptr;
   p.seq_len = log_seq ? D->seq_len : nullptr;
@@ -681,7 +678,7 @@ void build_decode_graph(Dev* D) {
   hipGraph_t g;
   float* cap = D->cap_out;  // hidden-state capture is never part of the graph
   D->cap_out = nullptr;
-  HIP_CHECK(hipStreamBeginCapture(D->stream, hipStreamCaptureModeThreadLocal));
+  HIP_CHECK(hipStreamBeginCapture(D->stream, hipStreamCaptureModeRelaxed));
   forward_chunk(D, D->next, 1, 1);
   argmax_to(D, D->logits, true, true);
   HIP_CHECK(hipStreamEndCapture(D->stream, &g));
@@ -771,6 +768,10 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
     ST_DIE("MoE model needs num_local_experts and num_experts_per_tok");
 
   HIP_CHECK(hipStreamCreateWithFlags(&D->stream, hipStreamNonBlocking));
+  {
+    const char* g = getenv("STRASGPT_DECODE_GRAPH");
+    D->use_graph = !(g && g[0] == '0');
+  }
 
   // Per-layer byte sizes of each weight class.
   const size_t d = D->d, hd = D->hd, H = D->H, E = D->E, V = D->V;
@@ -931,12 +932,8 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->seq_len = dalloc<int>(1);
   D->attn_splits = sg::attention_decode_splits(D->ctx, 64);
   D->attn_part = dalloc<float>((size_t)D->qh * D->attn_splits * (hd + 2));
-  D->attn_cnt = dalloc<unsigned>(D->qh);
-  HIP_CHECK(hipMemsetAsync(D->attn_cnt, 0, D->qh * sizeof(unsigned), D->stream));
   D->am_v = dalloc<float>(sg::argmax_blocks());
   D->am_i = dalloc<int>(sg::argmax_blocks());
-  D->am_cnt = dalloc<unsigned>(1);
-  HIP_CHECK(hipMemsetAsync(D->am_cnt, 0, sizeof(unsigned), D->stream));
   if (moe) {
     D->moe_sel = dalloc<int>(T * D->topk);
     D->moe_w = dalloc<float>(T * D->topk);
@@ -973,7 +970,7 @@ extern "C" void sg_free(transformer_t* t) {
     }
     void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
                     D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part,
-                    D->attn_cnt, D->am_v, D->am_i, D->am_cnt, D->cap_dev, D->cap_final_dev,
+                    D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
                     D->moe_sel, D->moe_w, D->moe_act};
     for (void* b : bufs)
       if (b) HIP_CHECK(hipFree(b));
@@ -1068,10 +1065,11 @@ extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* toke
     stop = *D->h_next == eos;
   }
   if (steps > 1 && !stop) {
-    if (!D->prof) build_decode_graph(D);
+    const bool eager = D->prof || !D->use_graph;
+    if (!eager) build_decode_graph(D);
     set_pos(D, t->state->cached_count);
     for (size_t i = 1; i < steps && !stop; i++) {
-      if (D->prof) {
+      if (eager) {
         // Eager step (events around every launch); same kernels as the graph.
         D->host_pos = t->state->cached_count + produced - 1;
         forward_chunk(D, D->next, 1, 1);
