@@ -18,6 +18,11 @@ extern "C" {
 int strasgpt_kbench_gemv(int n, int k, int dual, int variant, int iters,
                          double* avg_us, double* rel_err);
 int strasgpt_kbench_gemv_variants(void);
+/* Same with the input RMSNorm prologue (norm != 0). Launches cycle
+ * through enough weight copies (over 1 GiB) that every launch streams its
+ * weights from HBM rather than from the Infinity Cache. */
+int strasgpt_kbench_gemv2(int n, int k, int dual, int norm, int variant, int iters,
+                          double* avg_us, double* rel_err);
 
 /* Prefill GEMM C = A W^T, A fp32 [M][K], W bf16 [N][K]; precision 0 is
  * bf16x2 (split activations), 1 is bf16. */

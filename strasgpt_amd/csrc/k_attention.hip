@@ -8,9 +8,9 @@
 // sum per query row), P kept in LDS for the P.V product.
 //
 // Decode: split-K over the cached positions ("flash decoding"): one block
-// per (64-key chunk, q head) writes (max, sum, partial output); a second
-// small kernel combines the chunks of each head (the kernel boundary is
-// the only synchronisation: no device-wide fences).
+// per (64-key chunk, query head) writes (max, sum, partial output); a
+// second small kernel combines the chunks of each head (the kernel boundary
+// is the only synchronisation: no device-wide fences).
 // The block also applies this step's QK RMSNorm + RoPE to q and to the new
 // key (read raw from the QKV projection), and one block per KV head writes
 // the processed key into the cache.
@@ -147,13 +147,19 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
       }
     }
   }
+  // Output as the bf16 hi/lo planes of the O-projection GEMM's input.
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int t = q0 + ty * 4 + i;
     if (t >= T) continue;
 #pragma unroll
-    for (int u = 0; u < DU; u++)
-      p.out[(size_t)t * qd + head * HD + tx + 16 * u] = o[i][u] / l[i];
+    for (int u = 0; u < DU; u++) {
+      const float v = o[i][u] / l[i];
+      const size_t idx = (size_t)t * qd + head * HD + tx + 16 * u;
+      const uint16_t h = f32_to_bf16_rne(v);
+      p.out_hi[idx] = h;
+      if (p.out_lo) p.out_lo[idx] = f32_to_bf16_rne(v - bf16_to_f32(h));
+    }
   }
 }
 
@@ -197,9 +203,17 @@ __device__ void norm_rope_wave(const float* src, const uint16_t* nw, float eps,
   }
 }
 
+// One block per (64-key chunk, query head). Every global load of the block
+// (this chunk's keys and values, the query row, the step's raw key) is
+// issued in one round at kernel start, four lanes per key row (128-bit,
+// coalesced): the key quarter stays in registers for the scores, the value
+// quarter goes to LDS for P.V. The block holding position P uses the
+// processed new key for that row and (for the first query head of its
+// group) writes it to the cache.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
-  constexpr int CH = 64;
+  constexpr int CH = 64, Q4 = HD / 4, NV = Q4 / 4;  // dims per lane, float4 per lane
+  __shared__ __attribute__((aligned(16))) float vs[CH * HD];
   __shared__ __attribute__((aligned(16))) float qs[HD];
   __shared__ __attribute__((aligned(16))) float kn[HD];
   __shared__ float sc[CH];
@@ -213,44 +227,49 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
   if (split >= nsplit) return;
   const int s0 = split * CH, s1 = min(s0 + CH, total), n = s1 - s0;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-  const float* cs = p.rope + (size_t)P * HD;
+  const int j = tid / 4, qt = tid % 4;
   const bool has_new = s1 == total;
+  const float* kbase = p.kcache + (size_t)kvh * p.ctx * HD;
+  const float* vbase = p.vcache + (size_t)kvh * p.ctx * HD;
 
+  float4 kr[NV], vr[NV];
+  const bool row = j < n;
+  const bool cached = row && s0 + j != P;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    kr[i] = cached ? *(const float4*)(kbase + (size_t)(s0 + j) * HD + qt * Q4 + 4 * i)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    vr[i] = row ? *(const float4*)(vbase + (size_t)(s0 + j) * HD + qt * Q4 + 4 * i)
+                : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float* cs = p.rope + (size_t)P * HD;
   if (wave == 0)
     norm_rope_wave<HD>(p.q + (size_t)head * HD, p.qn, p.eps, cs, p.pair_bound, p.pair_offset,
                        p.pair_stride, qs);
   if (wave == 1 && has_new)
     norm_rope_wave<HD>(p.kraw + (size_t)kvh * HD, p.kn, p.eps, cs, p.pair_bound,
                        p.pair_offset, p.pair_stride, kn);
+#pragma unroll
+  for (int i = 0; i < NV; i++) *(float4*)&vs[j * HD + qt * Q4 + 4 * i] = vr[i];
   __syncthreads();
-  const float* kbase = p.kcache + (size_t)kvh * p.ctx * HD;
-  const float* vbase = p.vcache + (size_t)kvh * p.ctx * HD;
   if (has_new && head % G == 0) {
     for (int e = tid; e < HD; e += 256) p.kcache_w[((size_t)kvh * p.ctx + P) * HD + e] = kn[e];
   }
-
-  // Scores: 4 lanes per key, each a contiguous quarter of the head
-  // (coalesced 128-bit loads of consecutive key rows).
-  {
-    const int key = tid / 4, sub = tid % 4;
-    constexpr int Q4 = HD / 4;
-    float a = 0.0f;
-    const int s = s0 + key;
-    if (key < n) {
-      const float* kr = s == P ? kn : kbase + (size_t)s * HD;
+  if (row && !cached) {
 #pragma unroll
-      for (int e = sub * Q4; e < (sub + 1) * Q4; e += 4) {
-        const float4 kv = *(const float4*)(kr + e);
-        const float4 qv = *(const float4*)(qs + e);
-        a = fmaf(qv.x, kv.x, a);
-        a = fmaf(qv.y, kv.y, a);
-        a = fmaf(qv.z, kv.z, a);
-        a = fmaf(qv.w, kv.w, a);
-      }
-    }
-    a = group_sum<4>(a);
-    if (sub == 0 && key < n) sc[key] = a / sqrtf((float)HD);
+    for (int i = 0; i < NV; i++) kr[i] = *(const float4*)&kn[qt * Q4 + 4 * i];
   }
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const float4 q = *(const float4*)&qs[qt * Q4 + 4 * i];
+    a = fmaf(q.x, kr[i].x, a);
+    a = fmaf(q.y, kr[i].y, a);
+    a = fmaf(q.z, kr[i].z, a);
+    a = fmaf(q.w, kr[i].w, a);
+  }
+  a = group_sum<4>(a);
+  if (qt == 0 && row) sc[j] = a / sqrtf((float)HD);
   __syncthreads();
   if (wave == 0) {
     const float v = lane < n ? sc[lane] : -INFINITY;
@@ -267,18 +286,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
   constexpr int KG = 256 / HD;
   const int d = tid % HD, kg = tid / HD;
   {
-    float a = 0.0f;
+    float acc = 0.0f;
 #pragma unroll 8
-    for (int s = kg; s < n; s += KG) a = fmaf(sc[s], vbase[(size_t)(s0 + s) * HD + d], a);
-    red[kg][d] = a;
+    for (int jj = kg; jj < n; jj += KG) acc = fmaf(sc[jj], vs[jj * HD + d], acc);
+    red[kg][d] = acc;
   }
   __syncthreads();
   float* part = p.partial + ((size_t)head * p.splits + split) * (HD + 2);
   if (tid < HD) {
-    float a = 0.0f;
+    float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < KG; k++) a += red[k][tid];
-    part[2 + tid] = a;
+    for (int k = 0; k < KG; k++) acc += red[k][tid];
+    part[2 + tid] = acc;
   }
   if (tid == 0) {
     part[0] = stat[0];
@@ -290,17 +309,32 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
 // M = max m_i, out = sum_i o_i e^(m_i - M) / sum_i l_i e^(m_i - M).
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_decode_combine_kernel(AttnParams p) {
+  __shared__ float wts[1024];
+  __shared__ float red[HD / WAVE > 0 ? HD / WAVE : 1];
   const int head = blockIdx.x, d = threadIdx.x;
   const int nsplit = (*p.pos + 1 + 63) / 64;
   const float* pb = p.partial + (size_t)head * p.splits * (HD + 2);
-  float M = -INFINITY;
-  for (int i = 0; i < nsplit; i++) M = fmaxf(M, pb[(size_t)i * (HD + 2)]);
+  // chunk maxima in parallel, then M = max, weights e^(m_i - M)
+  float mx = -INFINITY;
+  for (int i = d; i < nsplit; i += HD) {
+    wts[i] = pb[(size_t)i * (HD + 2)];
+    mx = fmaxf(mx, wts[i]);
+  }
+  mx = wave_max(mx);
+  if (HD > WAVE) {
+    if (d % WAVE == 0) red[d / WAVE] = mx;
+    __syncthreads();
+    for (int w = 0; w < HD / WAVE; w++) mx = fmaxf(mx, red[w]);
+  }
+  __syncthreads();
+  for (int i = d; i < nsplit; i += HD) wts[i] = expf(wts[i] - mx);
+  __syncthreads();
   float L = 0.0f, o = 0.0f;
+#pragma unroll 4
   for (int i = 0; i < nsplit; i++) {
     const float* q = pb + (size_t)i * (HD + 2);
-    const float w = expf(q[0] - M);
-    L = fmaf(q[1], w, L);
-    o = fmaf(q[2 + d], w, o);
+    L = fmaf(q[1], wts[i], L);
+    o = fmaf(q[2 + d], wts[i], o);
   }
   p.out[(size_t)head * HD + d] = o / L;
 }
@@ -311,6 +345,7 @@ int attention_decode_splits(int ctx, int chunk) { return (ctx + chunk - 1) / chu
 
 void attention_prefill(const AttnParams& p, hipStream_t s) {
   if (p.T <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
+  if (!p.out_hi) ST_DIE("prefill attention writes bf16 planes");
   dim3 grid((p.T + BQ - 1) / BQ, p.q_heads);
   switch (p.hd) {
     case 16: hipLaunchKernelGGL(attn_prefill_kernel<16>, grid, dim3(256), 0, s, p); break;
@@ -326,6 +361,7 @@ void attention_decode(const AttnParams& p, hipStream_t s) {
   if (p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
   if (p.chunk != 64) ST_DIE("decode attention chunk must be 64");
   if (p.splits != attention_decode_splits(p.ctx, p.chunk)) ST_DIE("decode split count mismatch");
+  if (p.splits > 1024) ST_DIE("decode attention supports contexts up to 65536");
   dim3 grid(p.splits, p.q_heads);
   switch (p.hd) {
 #define DECODE_CASE(HD)                                                                 \

@@ -29,6 +29,41 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const uint
   for (int e = threadIdx.x; e < d; e += 256) yr[e] = (xr[e] * s) * bf16_to_f32(w[e]);
 }
 
+// Residual add of a split-K projection and RMSNorm of the updated row. The
+// split partial sums are added in split order first, so x gains one
+// rounded term like the reference's x += dot (source/transformer.c:
+// 1439-1445, 1498-1504); then the reference RMSNorm (source/transformer.c:
+// 978-999) is written as fp32 and/or as the bf16 hi/lo planes that the next
+// GEMM consumes (hi = bf16(y), lo = bf16(y - hi)).
+__global__ __launch_bounds__(256) void residual_norm_kernel(NormParams p) {
+  __shared__ float red[4];
+  const int row = blockIdx.x, d = p.d;
+  float* xr = p.x + (size_t)row * d;
+  float ss = 0.0f;
+  for (int e = threadIdx.x; e < d; e += 256) {
+    float v = xr[e];
+    if (p.splits > 0) {
+      float o = p.part[(size_t)row * d + e];
+      for (int sp = 1; sp < p.splits; sp++) o += p.part[((size_t)sp * p.rows + row) * d + e];
+      v += o;
+      xr[e] = v;
+    }
+    ss = fmaf(v, v, ss);
+  }
+  if (!p.w) return;
+  const float s = rms_scale(block_sum<256>(ss, red), d, p.eps);
+  for (int e = threadIdx.x; e < d; e += 256) {
+    const float y = (xr[e] * s) * bf16_to_f32(p.w[e]);
+    const size_t i = (size_t)row * d + e;
+    if (p.y) p.y[i] = y;
+    if (p.y_hi) {
+      const uint16_t h = f32_to_bf16_rne(y);
+      p.y_hi[i] = h;
+      if (p.y_lo) p.y_lo[i] = f32_to_bf16_rne(y - bf16_to_f32(h));
+    }
+  }
+}
+
 // One wavefront per (token, head): optional per-head RMSNorm with the
 // layer's q/k norm weight (source/transformer.c:1293-1307, 1340-1356), then
 // the pair rotation v0' = v0 cos - v1 sin, v1' = v0 sin + v1 cos with the
@@ -159,6 +194,13 @@ void rmsnorm_rows(const float* x, const uint16_t* w, float* y, int rows, int d, 
                   hipStream_t s) {
   if (rows <= 0) ST_DIE("rmsnorm needs rows > 0");
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, w, y, d, eps);
+  HIP_CHECK(hipGetLastError());
+}
+
+void residual_norm(const NormParams& p, hipStream_t s) {
+  if (p.rows <= 0 || p.d <= 0) ST_DIE("residual_norm needs rows, d > 0");
+  if (p.splits > 0 && !p.part) ST_DIE("residual_norm needs the partial sums");
+  hipLaunchKernelGGL(residual_norm_kernel, dim3(p.rows), dim3(256), 0, s, p);
   HIP_CHECK(hipGetLastError());
 }
 

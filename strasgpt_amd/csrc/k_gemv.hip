@@ -25,6 +25,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / WAVE;
 constexpr int kMaxLdsK = 16384;  // fp32 row staged in LDS up to 64 KiB
 constexpr int kStep = 8 * WAVE;  // K elements per wavefront step
+constexpr int kXcds = 8;
 
 __device__ __forceinline__ float dot8(uint4 w, const float4& a, const float4& b, float acc) {
   acc = fmaf(bf16_lo(w.x), a.x, acc);
@@ -120,15 +121,24 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const int K = p.K, N = p.N;
   const int nchunks = (K + U * kStep - 1) / (U * kStep);
-  const int stride = gridDim.x * kWaves * R;
-  int row0 = (blockIdx.x * kWaves + wave) * R;
+  // Each block owns a contiguous range of row groups. Blocks are dispatched
+  // round-robin over the 8 XCDs; renumbering gives every XCD a contiguous
+  // slice of the matrix, so each XCD's TLB and L2 see 1/8 of its pages.
+  const int groups = (N + kWaves * R - 1) / (kWaves * R);
+  const int G = gridDim.x, per = (groups + G - 1) / G;
+  const int v = (G % kXcds == 0) ? (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds
+                                 : blockIdx.x;
+  const int g_end = min(groups, (v + 1) * per);
+  const int stride = kWaves * R;  // rows per group
+  int row0 = (v * per * kWaves + wave) * R;
+  const int row_end = g_end * kWaves * R;
 
   Chunk<R, U, DUAL> cur, nxt;
-  if (row0 < N) load_chunk<R, U, DUAL>(p, row0, 0, lane, cur);
+  if (row0 < min(N, row_end)) load_chunk<R, U, DUAL>(p, row0, 0, lane, cur);
   if (LDS) stage_row<NORM>(p, xs, red);
   const float* xr = LDS ? xs : p.x;
 
-  for (; row0 < N; row0 += stride) {
+  for (; row0 < min(N, row_end); row0 += stride) {
     float acc[R], acc2[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = acc2[r] = 0.0f;
@@ -137,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
       // next one) before multiplying the current one.
       const bool more = c + 1 < nchunks;
       const int nrow = more ? row0 : row0 + stride;
-      if (more || nrow < N) load_chunk<R, U, DUAL>(p, nrow, more ? c + 1 : 0, lane, nxt);
+      if (more || nrow < min(N, row_end)) load_chunk<R, U, DUAL>(p, nrow, more ? c + 1 : 0, lane, nxt);
       mul_chunk<R, U, DUAL>(xr, K, c, lane, cur, acc, acc2);
       cur = nxt;
     }
@@ -173,11 +183,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   }
 }
 
-// Blocks: at most `cap`, and the same number of row groups for each block.
+// Blocks: at most `cap`, the same number of row groups for each block, and
+// a multiple of the XCD count when there are enough groups.
 int balanced_blocks(int groups, int cap) {
-  if (groups <= cap) return groups;
   const int per = (groups + cap - 1) / cap;
-  return (groups + per - 1) / per;
+  int blocks = (groups + per - 1) / per;
+  if (blocks >= kXcds * 4) blocks = (blocks + kXcds - 1) / kXcds * kXcds;
+  return blocks;
 }
 
 template <int R, int U, int EPI>
@@ -209,10 +221,10 @@ void check(const GemvParams& p, int epi) {
 void gemv(const GemvParams& p, int epi, hipStream_t s) {
   check(p, epi);
   switch (epi) {
-    case GEMV_STORE: launch<2, 4, GEMV_STORE>(p, s, 2048); break;
-    case GEMV_RESIDUAL: launch<1, 4, GEMV_RESIDUAL>(p, s, 2048); break;
-    case GEMV_QKV: launch<2, 4, GEMV_QKV>(p, s, 2048); break;
-    case GEMV_SWIGLU: launch<1, 4, GEMV_SWIGLU>(p, s, 2048); break;
+    case GEMV_STORE: launch<1, 2, GEMV_STORE>(p, s, 2048); break;
+    case GEMV_RESIDUAL: launch<1, 4, GEMV_RESIDUAL>(p, s, 4096); break;
+    case GEMV_QKV: launch<1, 2, GEMV_QKV>(p, s, 2048); break;
+    case GEMV_SWIGLU: launch<1, 2, GEMV_SWIGLU>(p, s, 2048); break;
     default: ST_DIE("unknown GEMV epilogue");
   }
   HIP_CHECK(hipGetLastError());

@@ -55,33 +55,57 @@ void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s);
 void moe_gemv_down(const MoeGemvParams& p, hipStream_t s);
 
 // ---------------------------------------------------------------- GEMM --
-// C[M][N] = A[M][K] (fp32) x W[N][K]^T (bf16) on MFMA; A is split into
-// bf16 hi + lo terms (SPLIT2) or rounded once (BF16).
+// C[M][N] = A[M][K] x W[N][K]^T (bf16 weights) on MFMA. A is given as two
+// bf16 planes, hi = bf16(a) and lo = bf16(a - hi), written by the kernel
+// that produced the activations; GEMM_SPLIT2 multiplies both planes,
+// GEMM_BF16 only hi.
 enum GemmPrecision { GEMM_SPLIT2 = 0, GEMM_BF16 = 1 };
 enum GemmEpilogue {
   GEMM_STORE = 0,    // C[m][n] = acc
   GEMM_RESIDUAL = 1, // C[m][n] += acc
   GEMM_QKV = 2,      // q[m][n] | k-cache | v-cache rows at position P+m
-  GEMM_SWIGLU = 3,   // C[m][n] = silu(A.Wg_n) * (A.Wu_n)
+  GEMM_SWIGLU = 3,   // (c_hi, c_lo)[m][n] = split(silu(A.Wg_n) * (A.Wu_n))
+  GEMM_PARTIAL = 4,  // C[split][m][n] = partial sum of this K split
 };
 struct GemmParams {
-  const float* a;  // [M][lda]
+  const uint16_t* a_hi;  // [M][lda] bf16
+  const uint16_t* a_lo;  // [M][lda] bf16 (bf16x2 only)
   int lda;
   const uint16_t* w;   // [N][K]
   const uint16_t* w2;  // up matrix for GEMM_SWIGLU
   int M, N, K;
-  float* c;            // [M][ldc]
+  float* c;            // [M][ldc] (PARTIAL: [splits][M][ldc])
   int ldc;
+  uint16_t* c_hi;      // GEMM_SWIGLU output planes [M][ldc]
+  uint16_t* c_lo;      //   (c_lo may be null: hi plane only)
   // GEMM_QKV
   float* q; float* kcache; float* vcache; const int* pos;
   int q_dim, kv_dim, head_dim, ctx;
 };
-void gemm(const GemmParams& p, int epilogue, int precision, hipStream_t s);
+void gemm(const GemmParams& p, int epilogue, int precision, int splits, hipStream_t s);
+// Split-K factor that fills the CUs for an M x N output (1: no split).
+int gemm_splits(int M, int N, int K);
 
 // -------------------------------------------------------- elementwise --
 void embed(const int* tok, int T, const uint16_t* table, int d, float* x, hipStream_t s);
 void rmsnorm_rows(const float* x, const uint16_t* w, float* y, int rows, int d,
                   float eps, hipStream_t s);
+// Row-wise: x += sum over s < splits of part[s] (in order; residual add of a
+// split-K projection), then, if w is given, the reference RMSNorm of x
+// written as fp32 (y, optional) and/or as bf16 hi/lo planes (y_hi, y_lo
+// optional) for the next GEMM.
+struct NormParams {
+  float* x;
+  const float* part;  // [splits][rows][d] or null
+  int splits;
+  const uint16_t* w;  // norm weight or null (residual only)
+  float eps;
+  int rows, d;
+  float* y;
+  uint16_t* y_hi;
+  uint16_t* y_lo;
+};
+void residual_norm(const NormParams& p, hipStream_t s);
 // Per-head RMSNorm (if norm weights given) and RoPE, in place, on T rows of
 // q ([T][heads*hd]) and on the T new key rows of one layer's k-cache.
 void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T,
@@ -94,7 +118,9 @@ struct AttnParams {
   const float* q;        // [T][q_heads*hd]
   const float* kcache;   // layer base [kv_heads][ctx][hd]
   const float* vcache;
-  float* out;            // [T][q_heads*hd]
+  float* out;            // decode: [q_heads*hd] fp32
+  uint16_t* out_hi;      // prefill: [T][q_heads*hd] bf16 planes (O-GEMM input)
+  uint16_t* out_lo;      //   (out_lo may be null)
   const int* pos;        // device: position of the first query (cached count)
   int T, q_heads, kv_heads, hd, ctx;
   // decode only: raw key of this step and QK-norm/RoPE inputs

@@ -127,6 +127,11 @@ struct transformer_device {
   void* w[W_COUNT] = {nullptr};
   // activations [512][...]
   float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *act = nullptr;
+  // prefill GEMM inputs as bf16 hi/lo planes, split-K partial sums
+  uint16_t *xn_hi = nullptr, *xn_lo = nullptr, *att_hi = nullptr, *att_lo = nullptr;
+  uint16_t *act_hi = nullptr, *act_lo = nullptr;
+  float* ws = nullptr;
+  int ws_splits = 0;
   float *kraw = nullptr, *logits = nullptr;
   int logits_rows = 0;
   size_t host_pos = 0;  // host mirror of *pos (profiling byte counts)
@@ -454,19 +459,66 @@ void layer_decode(Dev* D, int l) {
   }
 }
 
-void layer_prefill(Dev* D, int l, int T) {
+// Residual add of a projection (split-K partial sums in D->ws, or already
+// added) and the RMSNorm with weight w of the updated rows into the bf16
+// planes of the next GEMM (and the fp32 rows for the MoE experts).
+void prefill_norm(Dev* D, int T, int splits, const uint16_t* w) {
+  sg::NormParams n{};
+  n.x = D->x;
+  n.part = splits > 1 ? D->ws : nullptr;
+  n.splits = splits > 1 ? splits : 0;
+  n.w = w;
+  n.eps = D->eps;
+  n.rows = T;
+  n.d = D->d;
+  n.y = D->moe ? D->xn : nullptr;
+  n.y_hi = D->xn_hi;
+  n.y_lo = D->precision == sg::GEMM_SPLIT2 ? D->xn_lo : nullptr;
+  Prof pr(D, K_ELEM, (double)T * D->d * (8 + 4.0 * n.splits), 0);
+  sg::residual_norm(n, D->stream);
+}
+
+// Projection whose result is added to the residual stream: split-K into
+// D->ws when that fills the GPU (summed by the next prefill_norm), else a
+// direct residual epilogue. Returns the split count.
+int residual_gemm(Dev* D, const uint16_t* a_hi, const uint16_t* a_lo, int lda,
+                  const uint16_t* w, int T, int N, int K, int cls) {
+  sg::GemmParams g{};
+  g.a_hi = a_hi;
+  g.a_lo = a_lo;
+  g.lda = lda;
+  g.w = w;
+  g.M = T;
+  g.N = N;
+  g.K = K;
+  g.ldc = N;
+  int splits = sg::gemm_splits(T, N, K);
+  if (splits > D->ws_splits) splits = D->ws_splits;
+  Prof pr(D, cls, (double)N * K * 2, 2.0 * T * N * K);
+  if (splits > 1) {
+    g.c = D->ws;
+    sg::gemm(g, sg::GEMM_PARTIAL, D->precision, splits, D->stream);
+  } else {
+    g.c = D->x;
+    sg::gemm(g, sg::GEMM_RESIDUAL, D->precision, 1, D->stream);
+  }
+  return splits;
+}
+
+// One layer over T > 1 rows. On entry D->xn_hi/lo hold the layer's input
+// RMSNorm; on exit x holds the layer output and, if next_norm is given, the
+// planes hold its RMSNorm with that weight.
+void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
   hipStream_t s = D->stream;
   const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
   float* kc = D->kc + l * cache_layer;
   float* vc = D->vc + l * cache_layer;
   const double d = D->d, M = T;
+  const bool split = D->precision == sg::GEMM_SPLIT2;
 
-  {
-    Prof pr(D, K_ELEM, 2.0 * M * d * 4, 0);
-    sg::rmsnorm_rows(D->x, W16(D, W_MHA_NORM, l), D->xn, T, D->d, D->eps, s);
-  }
   sg::GemmParams g{};
-  g.a = D->xn;
+  g.a_hi = D->xn_hi;
+  g.a_lo = split ? D->xn_lo : nullptr;
   g.lda = D->d;
   g.w = W16(D, W_Q, l);
   g.M = T;
@@ -482,7 +534,7 @@ void layer_prefill(Dev* D, int l, int T) {
   g.ctx = D->ctx;
   {
     Prof pr(D, K_QKV_GEMM, (double)D->qkv_rows * d * 2, 2.0 * M * D->qkv_rows * d);
-    sg::gemm(g, sg::GEMM_QKV, D->precision, s);
+    sg::gemm(g, sg::GEMM_QKV, D->precision, 1, s);
   }
   {
     Prof pr(D, K_ELEM, 2.0 * M * (D->qd + D->kvd) * 4, 0);
@@ -495,7 +547,8 @@ void layer_prefill(Dev* D, int l, int T) {
   a.q = D->q;
   a.kcache = kc;
   a.vcache = vc;
-  a.out = D->att;
+  a.out_hi = D->att_hi;
+  a.out_lo = split ? D->att_lo : nullptr;
   a.pos = D->pos;
   a.T = T;
   a.q_heads = D->qh;
@@ -509,53 +562,32 @@ void layer_prefill(Dev* D, int l, int T) {
             4.0 * D->qh * D->hd * pairs);
     sg::attention_prefill(a, s);
   }
-  sg::GemmParams o{};
-  o.a = D->att;
-  o.lda = D->qd;
-  o.w = W16(D, W_O, l);
-  o.M = T;
-  o.N = D->d;
-  o.K = D->qd;
-  o.c = D->x;
-  o.ldc = D->d;
-  {
-    Prof pr(D, K_O_GEMM, d * D->qd * 2, 2.0 * M * d * D->qd);
-    sg::gemm(o, sg::GEMM_RESIDUAL, D->precision, s);
-  }
+  const int so = residual_gemm(D, D->att_hi, split ? D->att_lo : nullptr, D->qd, W16(D, W_O, l),
+                               T, D->d, D->qd, K_O_GEMM);
+  prefill_norm(D, T, so, W16(D, W_FFN_NORM, l));
   if (!D->moe) {
-    {
-      Prof pr(D, K_ELEM, 2.0 * M * d * 4, 0);
-      sg::rmsnorm_rows(D->x, W16(D, W_FFN_NORM, l), D->xn, T, D->d, D->eps, s);
-    }
     sg::GemmParams f{};
-    f.a = D->xn;
+    f.a_hi = D->xn_hi;
+    f.a_lo = split ? D->xn_lo : nullptr;
     f.lda = D->d;
     f.w = W16(D, W_GATE, l);
     f.w2 = W16(D, W_UP, l);
     f.M = T;
     f.N = D->H;
     f.K = D->d;
-    f.c = D->act;
     f.ldc = D->H;
+    f.c_hi = D->act_hi;
+    f.c_lo = split ? D->act_lo : nullptr;
     {
       Prof pr(D, K_GU_GEMM, 2.0 * D->H * d * 2, 4.0 * M * D->H * d);
-      sg::gemm(f, sg::GEMM_SWIGLU, D->precision, s);
+      sg::gemm(f, sg::GEMM_SWIGLU, D->precision, 1, s);
     }
-    sg::GemmParams dn{};
-    dn.a = D->act;
-    dn.lda = D->H;
-    dn.w = W16(D, W_DOWN, l);
-    dn.M = T;
-    dn.N = D->d;
-    dn.K = D->H;
-    dn.c = D->x;
-    dn.ldc = D->d;
-    {
-      Prof pr(D, K_DOWN_GEMM, d * D->H * 2, 2.0 * M * d * D->H);
-      sg::gemm(dn, sg::GEMM_RESIDUAL, D->precision, s);
-    }
+    const int sd = residual_gemm(D, D->act_hi, split ? D->act_lo : nullptr, D->H,
+                                 W16(D, W_DOWN, l), T, D->d, D->H, K_DOWN_GEMM);
+    prefill_norm(D, T, sd, next_norm);
   } else {
     ffn_moe(D, l, T);
+    prefill_norm(D, T, 0, next_norm);
   }
 }
 
@@ -583,9 +615,10 @@ void forward_chunk(Dev* D, const int* tok, int T, int lc) {
     sg::embed(tok, T, W16(D, W_EMB), D->d, D->x, D->stream);
   }
   const bool capture = D->cap_out != nullptr;
+  if (T > 1) prefill_norm(D, T, 0, W16(D, W_MHA_NORM, 0));
   for (int l = 0; l < D->L; l++) {
     if (T == 1) layer_decode(D, l);
-    else layer_prefill(D, l, T);
+    else layer_prefill(D, l, T, l + 1 < D->L ? W16(D, W_MHA_NORM, l + 1) : nullptr);
     if (capture)
       HIP_CHECK(hipMemcpyAsync(D->cap_dev + (size_t)l * T * D->d, D->x,
                                (size_t)T * D->d * sizeof(float), hipMemcpyDeviceToDevice,
@@ -915,6 +948,14 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->att = dalloc<float>(T * D->qd);
   D->act = dalloc<float>(T * wide);
   D->kraw = dalloc<float>(D->kvd);
+  D->xn_hi = dalloc<uint16_t>(T * d);
+  D->xn_lo = dalloc<uint16_t>(T * d);
+  D->att_hi = dalloc<uint16_t>(T * D->qd);
+  D->att_lo = dalloc<uint16_t>(T * D->qd);
+  D->act_hi = dalloc<uint16_t>(T * H);
+  D->act_lo = dalloc<uint16_t>(T * H);
+  D->ws_splits = 8;
+  D->ws = dalloc<float>((size_t)D->ws_splits * T * d);
   const size_t cache = (size_t)D->L * D->kvh * D->ctx * hd;
   D->kc = dalloc<float>(cache);
   D->vc = dalloc<float>(cache);
@@ -971,7 +1012,8 @@ extern "C" void sg_free(transformer_t* t) {
     void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
                     D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part,
                     D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
-                    D->moe_sel, D->moe_w, D->moe_act};
+                    D->moe_sel, D->moe_w, D->moe_act, D->xn_hi, D->xn_lo,
+                    D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws};
     for (void* b : bufs)
       if (b) HIP_CHECK(hipFree(b));
     if (D->h_tok) HIP_CHECK(hipHostFree(D->h_tok));
