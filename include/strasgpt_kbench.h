@@ -18,10 +18,15 @@ extern "C" {
 int strasgpt_kbench_gemv(int n, int k, int dual, int variant, int iters,
                          double* avg_us, double* rel_err);
 int strasgpt_kbench_gemv_variants(void);
-/* Same with the input RMSNorm prologue (norm != 0). Launches cycle
- * through enough weight copies (over 1 GiB) that every launch streams its
- * weights from HBM rather than from the Infinity Cache. */
-int strasgpt_kbench_gemv2(int n, int k, int dual, int norm, int variant, int iters,
+/* Same with options in `flags`. Launches cycle through enough weight
+ * copies (over 1 GiB) that every launch streams its weights from HBM
+ * rather than from the Infinity Cache.
+ *   bit 0: input RMSNorm prologue;
+ *   bit 1: before each timed launch, an untimed kernel reads one word per
+ *          64 KiB of that launch's weights (warms address translation);
+ *   bit 2: time all launches back to back between two events instead of
+ *          one event pair per launch. */
+int strasgpt_kbench_gemv2(int n, int k, int dual, int flags, int variant, int iters,
                           double* avg_us, double* rel_err);
 
 /* Prefill GEMM C = A W^T, A fp32 [M][K], W bf16 [N][K]; precision 0 is
@@ -29,6 +34,15 @@ int strasgpt_kbench_gemv2(int n, int k, int dual, int norm, int variant, int ite
 int strasgpt_kbench_gemm(int m, int n, int k, int precision, int variant, int iters,
                          double* avg_us, double* rel_err);
 int strasgpt_kbench_gemm_variants(void);
+
+/* Grid barrier cost: one cooperative launch of `blocks` x 256 threads doing
+ * `rounds` barriers, each block writing `words` values before each barrier.
+ * fence 0: plain stores, no fences, no check; 1: fenced barrier, plain
+ * stores and loads; 2: fence-free barrier, agent-coherent stores and loads.
+ * Modes 1 and 2 count stale values read after each barrier in *bad_reads.
+ * Returns -2 if the blocks cannot all be resident. */
+int strasgpt_kbench_barrier(int blocks, int rounds, int fence, int words,
+                            double* us_per_round, int* bad_reads, int* timed_out);
 
 #ifdef __cplusplus
 }

@@ -28,12 +28,15 @@ typedef struct transformer_timing {
 /* The reference driver's greedy loop (source/strasgpt.c:206-252 with
  * --temp 0): one prefill over the prompt, then step_count - 1 single-token
  * steps, each feeding back the argmax. The loop stays on the device: the
- * next token never leaves HBM between steps (decode steps are replayed
- * from a captured HIP graph). Writes step_count token ids to out. Stops
+ * next token never leaves HBM between steps. By default the step's
+ * kernels are replayed from a captured HIP graph; a dense model can instead
+ * run each step as one persistent kernel launch (see
+ * transformer_set_decode_mode). Writes step_count token ids to out. Stops
  * early (like the reference) when eos_token_id >= 0 is produced; returns
- * the number of ids written. timing may be NULL. With the environment
- * variable STRASGPT_DECODE_GRAPH=0 the same kernels are launched eagerly
- * per step instead (for tools that do not follow graph launches). */
+ * the number of ids written. timing may be NULL. Environment:
+ * STRASGPT_DECODE_PERSISTENT=1 selects the persistent step by default;
+ * STRASGPT_DECODE_GRAPH=0 launches the graph path's kernels eagerly
+ * instead (for tools that do not follow graph launches). */
 size_t transformer_generate_greedy(
     transformer_t* transformer,
     size_t token_count,
@@ -67,6 +70,43 @@ void transformer_capture_hidden(
  *    move by about 1e-3 so greedy tokens can differ from the reference).
  * Returns the previous mode. */
 int transformer_set_prefill_precision(transformer_t* transformer, int mode);
+
+/* Decode step implementation used by transformer_generate_greedy and by
+ * single-token transformer_predict calls (no reference counterpart):
+ *   TRANSFORMER_DECODE_PERSISTENT: one launch per token, all blocks
+ *     resident, phases separated by grid barriers (dense models; others
+ *     fall back to the graph path),
+ *   TRANSFORMER_DECODE_GRAPH (default): one kernel per operation, replayed
+ *     from a captured HIP graph by transformer_generate_greedy,
+ *   TRANSFORMER_DECODE_EAGER: the same kernels launched one by one.
+ * Returns the previous mode. Profiling (transformer_profile) always uses
+ * the eager path. */
+enum transformer_decode_mode {
+  TRANSFORMER_DECODE_PERSISTENT = 0,
+  TRANSFORMER_DECODE_GRAPH = 1,
+  TRANSFORMER_DECODE_EAGER = 2
+};
+int transformer_set_decode_mode(transformer_t* transformer, int mode);
+
+/* 1 when the loaded model can use TRANSFORMER_DECODE_PERSISTENT. */
+int transformer_decode_persistent_supported(const transformer_t* transformer);
+
+/* Phase tracer of the persistent decode step (measurement hook, no
+ * reference counterpart). While enabled, the first worker block of every
+ * step records wall-clock times around each grid barrier. transformer_decode_trace_read
+ * returns the barrier count n (0 when the tracer was never enabled) and
+ * writes up to max_values per-step averages in microseconds as 5 rows of n:
+ *   row 0: work before the barrier (since leaving the previous one),
+ *   row 1: wait inside the barrier,
+ *   rows 2-4: for the GEMV phase the barrier starts, time from leaving the
+ *          barrier to the end of input staging, of the weight loop and of
+ *          the epilogue (0 for other phases).
+ * Barriers are in launch order: for layer 0 those that start attention,
+ * combine, O, gate/up and down; for each further layer the one that starts
+ * its QKV phase, then the same five; then the logits barrier and the final
+ * argmax barrier (n = 6 x layer_count + 1). */
+void transformer_decode_trace(transformer_t* transformer, int enable);
+int transformer_decode_trace_read(transformer_t* transformer, double* us, int max_values);
 
 /* Measurement hooks (no reference counterpart; the reference only times
  * whole predict calls, source/strasgpt.c:206-274). While enabled, every

@@ -46,8 +46,27 @@ __device__ __forceinline__ float e8m0_scale(uint32_t s) {
 }
 
 // 16-byte streaming load of weights that are read once per step.
+// Plain accesses through pointers known to address global memory.
+__device__ __forceinline__ float gload(const float* p) {
+  return *(__attribute__((address_space(1))) const float*)p;
+}
+__device__ __forceinline__ float4 gload4(const float* p) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 v = *(__attribute__((address_space(1))) const f4*)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint16_t gload(const uint16_t* p) {
+  return *(__attribute__((address_space(1))) const uint16_t*)p;
+}
+__device__ __forceinline__ void gstore(float* p, float v) {
+  *(__attribute__((address_space(1))) float*)p = v;
+}
+
+// 128-bit non-temporal load from global memory (global, not flat,
+// instructions whatever the compiler knows of where `p` came from).
 __device__ __forceinline__ uint4 load_nt_u4(const void* p) {
-  const uint4* q = (const uint4*)p;
+  typedef __attribute__((address_space(1))) const uint4 guint4;
+  const guint4* q = (const guint4*)p;
   uint4 r;
   r.x = __builtin_nontemporal_load(&q->x);
   r.y = __builtin_nontemporal_load(&q->y);
@@ -89,6 +108,27 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   for (int i = 0; i < NT / WAVE; i++) s += red[i];
   __syncthreads();
   return s;
+}
+
+// acc + dot(8 bf16 weights packed in w, fp32 a[0..3] and b[0..3]), in
+// element order.
+__device__ __forceinline__ float dot8(uint4 w, const float4& a, const float4& b, float acc) {
+  acc = fmaf(bf16_lo(w.x), a.x, acc);
+  acc = fmaf(bf16_hi(w.x), a.y, acc);
+  acc = fmaf(bf16_lo(w.y), a.z, acc);
+  acc = fmaf(bf16_hi(w.y), a.w, acc);
+  acc = fmaf(bf16_lo(w.z), b.x, acc);
+  acc = fmaf(bf16_hi(w.z), b.y, acc);
+  acc = fmaf(bf16_lo(w.w), b.z, acc);
+  acc = fmaf(bf16_hi(w.w), b.w, acc);
+  return acc;
+}
+
+// SwiGLU of one element: silu(g) * u (reference source/transformer.c:
+// 1477-1486).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  g *= 1.0f / (1.0f + expf(-g));
+  return g * u;
 }
 
 // RMSNorm scale exactly as the reference computes it from the sum of

@@ -33,11 +33,6 @@ constexpr int BK = 32;
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  g *= 1.0f / (1.0f + expf(-g));
-  return g * u;
-}
-
 __device__ __forceinline__ void store_split(uint16_t* hi, uint16_t* lo, size_t i, float v,
                                             bool split) {
   const uint16_t h = f32_to_bf16_rne(v);

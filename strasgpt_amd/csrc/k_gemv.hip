@@ -27,24 +27,6 @@ constexpr int kMaxLdsK = 16384;  // fp32 row staged in LDS up to 64 KiB
 constexpr int kStep = 8 * WAVE;  // K elements per wavefront step
 constexpr int kXcds = 8;
 
-__device__ __forceinline__ float dot8(uint4 w, const float4& a, const float4& b, float acc) {
-  acc = fmaf(bf16_lo(w.x), a.x, acc);
-  acc = fmaf(bf16_hi(w.x), a.y, acc);
-  acc = fmaf(bf16_lo(w.y), a.z, acc);
-  acc = fmaf(bf16_hi(w.y), a.w, acc);
-  acc = fmaf(bf16_lo(w.z), b.x, acc);
-  acc = fmaf(bf16_hi(w.z), b.y, acc);
-  acc = fmaf(bf16_lo(w.w), b.z, acc);
-  acc = fmaf(bf16_hi(w.w), b.w, acc);
-  return acc;
-}
-
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  // reference source/transformer.c:1477-1486
-  g *= 1.0f / (1.0f + expf(-g));
-  return g * u;
-}
-
 template <bool NORM>
 __device__ __forceinline__ void stage_row(const GemvParams& p, float* xs, float* red) {
   const int K = p.K;

@@ -21,11 +21,6 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / WAVE;
 constexpr int kRowsPerWave = 4;
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  g *= 1.0f / (1.0f + expf(-g));
-  return g * u;
-}
-
 // Dot of one MXFP4 row with an fp32 vector in LDS (K multiple of 32).
 __device__ __forceinline__ float mx_row_dot(const uint8_t* blocks, const uint8_t* scales,
                                             const float* xs, int K, int lane) {

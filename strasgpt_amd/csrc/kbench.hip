@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "device_common.h"
+#include "grid_sync.h"
 #include "hip_check.h"
 #include "kernels.h"
 #include "strasgpt_kbench.h"
@@ -39,6 +40,15 @@ __global__ void fill_bf16(uint16_t* w, size_t n, uint32_t seed) {
 __global__ void fill_f32(float* x, size_t n, uint32_t seed) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     x[i] = (hash32((uint32_t)i * 2246822519u + seed) >> 8) / 8388608.0f - 1.0f;
+}
+
+// One 4-byte read per 64 KiB of [p, p + bytes).
+__global__ void touch_pages(const uint32_t* p, size_t bytes, uint32_t* sink) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i * 65536 < bytes) {
+    const uint32_t v = __builtin_nontemporal_load(p + i * 16384);
+    if (v == 0x7fc00001u) sink[0] = v;
+  }
 }
 
 __global__ void naive_gemv(const uint16_t* w, const uint16_t* w2, const float* x, int n, int k,
@@ -78,13 +88,35 @@ double rel_error(const std::vector<float>& got, const std::vector<float>& ref) {
   return m > 0 ? e / m : e;
 }
 
+// Average of `iters` launches timed back to back between two events.
 template <typename F>
-double time_launches(hipStream_t s, int iters, F launch) {
+double time_batch(hipStream_t s, int iters, F launch) {
+  launch();
+  launch();
+  hipEvent_t a, b;
+  HIP_CHECK(hipEventCreate(&a));
+  HIP_CHECK(hipEventCreate(&b));
+  HIP_CHECK(hipEventRecord(a, s));
+  for (int i = 0; i < iters; i++) launch();
+  HIP_CHECK(hipEventRecord(b, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  float ms;
+  HIP_CHECK(hipEventElapsedTime(&ms, a, b));
+  HIP_CHECK(hipEventDestroy(a));
+  HIP_CHECK(hipEventDestroy(b));
+  return ms / iters * 1e3;
+}
+
+// Average of `iters` launches, each timed by its own event pair; `before`
+// runs ahead of each pair, untimed.
+template <typename B, typename F>
+double time_launches(hipStream_t s, int iters, B before, F launch) {
   launch();
   launch();
   std::vector<hipEvent_t> ev(2 * iters);
   for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
   for (int i = 0; i < iters; i++) {
+    before();
     HIP_CHECK(hipEventRecord(ev[2 * i], s));
     launch();
     HIP_CHECK(hipEventRecord(ev[2 * i + 1], s));
@@ -100,7 +132,87 @@ double time_launches(hipStream_t s, int iters, F launch) {
   return total / iters * 1e3;
 }
 
+// `rounds` grid barriers; before each one every block writes `words`
+// 32-bit values of its own slot (two slots per block, alternating by
+// round), and after it checks every value of the next block's slot.
+// MODE 0: plain stores, no fences, no check (barrier cost alone);
+// MODE 1: plain stores and loads with the fenced barrier;
+// MODE 2: agent-coherent stores and loads with the fence-free barrier.
+template <int MODE>
+__global__ __launch_bounds__(256) void barrier_bench_kernel(sg::GridSync g, int rounds,
+                                                           unsigned* data, int words,
+                                                           unsigned* bad) {
+  const unsigned b = blockIdx.x, nb = gridDim.x;
+  for (int r = 0; r < rounds; r++) {
+    unsigned* mine = data + ((size_t)(r & 1) * nb + b) * words;
+    for (int i = threadIdx.x; i < words; i += blockDim.x) {
+      if (MODE == 2)
+        sg::sync_store(mine + i, r + 1);
+      else
+        mine[i] = r + 1;
+    }
+    sg::grid_sync<MODE == 1>(g);
+    if (MODE != 0) {
+      const unsigned* other = data + ((size_t)(r & 1) * nb + (b + 1) % nb) * words;
+      unsigned miss = 0;
+      for (int i = threadIdx.x; i < words; i += blockDim.x)
+        miss += (MODE == 2 ? sg::sync_load(other + i) : other[i]) != (unsigned)r + 1;
+      if (miss) atomicAdd(bad, miss);
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int strasgpt_kbench_barrier(int blocks, int rounds, int fence, int words,
+                                       double* us_per_round, int* bad_reads, int* timed_out) {
+  if (blocks <= 0 || rounds <= 0 || words <= 0 || words > 65536) return -1;
+  int dev, cus, per_cu = 0;
+  HIP_CHECK(hipGetDevice(&dev));
+  HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (fence < 0 || fence > 2) return -1;
+  const void* fn = fence == 0   ? (const void*)barrier_bench_kernel<0>
+                   : fence == 1 ? (const void*)barrier_bench_kernel<1>
+                                : (const void*)barrier_bench_kernel<2>;
+  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0));
+  if (blocks > per_cu * cus) return -2;  // not all blocks resident at once
+  hipStream_t s;
+  HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  if (blocks > sg::kSyncMaxBlocks) return -1;
+  unsigned *state, *flags, *data;
+  HIP_CHECK(hipMalloc(&state, sg::kSyncStateWords * 4));
+  HIP_CHECK(hipMalloc(&flags, 64));
+  HIP_CHECK(hipMalloc(&data, (size_t)2 * blocks * words * 4));
+  HIP_CHECK(hipMemsetAsync(state, 0, sg::kSyncStateWords * 4, s));
+  HIP_CHECK(hipMemsetAsync(flags, 0, 64, s));
+  HIP_CHECK(hipMemsetAsync(data, 0, (size_t)2 * blocks * words * 4, s));
+  sg::GridSync g{state, flags, 1u};
+  unsigned* bad = flags + 1;
+  void* args[] = {&g, &rounds, &data, &words, &bad};
+  hipEvent_t a, b;
+  HIP_CHECK(hipEventCreate(&a));
+  HIP_CHECK(hipEventCreate(&b));
+  HIP_CHECK(hipLaunchCooperativeKernel(fn, dim3(blocks), dim3(256), args, 0, s));  // warm-up
+  g.seq += rounds;
+  HIP_CHECK(hipEventRecord(a, s));
+  HIP_CHECK(hipLaunchCooperativeKernel(fn, dim3(blocks), dim3(256), args, 0, s));
+  HIP_CHECK(hipEventRecord(b, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  float ms;
+  HIP_CHECK(hipEventElapsedTime(&ms, a, b));
+  *us_per_round = ms * 1e3 / rounds;
+  unsigned h[2];
+  HIP_CHECK(hipMemcpy(h, flags, 8, hipMemcpyDeviceToHost));
+  *timed_out = (int)h[0];
+  *bad_reads = (int)h[1];
+  HIP_CHECK(hipEventDestroy(a));
+  HIP_CHECK(hipEventDestroy(b));
+  HIP_CHECK(hipFree(state));
+  HIP_CHECK(hipFree(flags));
+  HIP_CHECK(hipFree(data));
+  HIP_CHECK(hipStreamDestroy(s));
+  return 0;
+}
 
 extern "C" int strasgpt_kbench_gemv_variants(void) { return sg::gemv_variant_count(); }
 extern "C" int strasgpt_kbench_gemm_variants(void) { return sg::gemm_variant_count(); }
@@ -110,8 +222,9 @@ extern "C" int strasgpt_kbench_gemv(int n, int k, int dual, int variant, int ite
   return strasgpt_kbench_gemv2(n, k, dual, 0, variant, iters, avg_us, rel_err);
 }
 
-extern "C" int strasgpt_kbench_gemv2(int n, int k, int dual, int norm, int variant, int iters,
+extern "C" int strasgpt_kbench_gemv2(int n, int k, int dual, int flags, int variant, int iters,
                                      double* avg_us, double* rel_err) {
+  const bool norm = flags & 1, touch = flags & 2, batch = flags & 4;
   if (n <= 0 || k <= 0 || k % 8 || k > 16384 || iters <= 0 || variant < 0 ||
       variant >= sg::gemv_variant_count())
     return -1;
@@ -124,6 +237,8 @@ extern "C" int strasgpt_kbench_gemv2(int n, int k, int dual, int norm, int varia
   std::vector<uint16_t*> w(copies), w2(copies, nullptr);
   uint16_t* nw = nullptr;
   float *x, *y, *yr, *xn;
+  uint32_t* sink;
+  HIP_CHECK(hipMalloc(&sink, 4));
   for (int c = 0; c < copies; c++) {
     HIP_CHECK(hipMalloc(&w[c], (size_t)n * k * 2));
     hipLaunchKernelGGL(fill_bf16, dim3(1024), dim3(256), 0, s, w[c], (size_t)n * k, 1u);
@@ -149,12 +264,23 @@ extern "C" int strasgpt_kbench_gemv2(int n, int k, int dual, int norm, int varia
   p.K = k;
   p.y = y;
   int it = 0;
-  *avg_us = time_launches(s, iters, [&] {
+  const size_t mat = (size_t)n * k * 2, pages = (mat + 65535) / 65536;
+  auto run = [&] {
     p.w = w[it % copies];
     p.w2 = w2[it % copies];
     it++;
     sg::gemv_variant(p, dual != 0, variant, s);
-  });
+  };
+  auto warm = [&] {
+    if (!touch) return;
+    const int c = it % copies;
+    hipLaunchKernelGGL(touch_pages, dim3((pages + 255) / 256), dim3(256), 0, s,
+                       (const uint32_t*)w[c], mat, sink);
+    if (dual)
+      hipLaunchKernelGGL(touch_pages, dim3((pages + 255) / 256), dim3(256), 0, s,
+                         (const uint32_t*)w2[c], mat, sink);
+  };
+  *avg_us = batch ? time_batch(s, iters, run) : time_launches(s, iters, warm, run);
   // reference on the last matrix used
   const float* xin = x;
   if (norm) {
@@ -176,6 +302,7 @@ extern "C" int strasgpt_kbench_gemv2(int n, int k, int dual, int norm, int varia
   HIP_CHECK(hipFree(xn));
   HIP_CHECK(hipFree(y));
   HIP_CHECK(hipFree(yr));
+  HIP_CHECK(hipFree(sink));
   HIP_CHECK(hipStreamDestroy(s));
   return 0;
 }
@@ -208,7 +335,7 @@ extern "C" int strasgpt_kbench_gemm(int m, int n, int k, int precision, int vari
   p.K = k;
   p.c = c;
   p.ldc = n;
-  *avg_us = time_launches(s, iters, [&] { sg::gemm_variant(p, precision, variant, s); });
+  *avg_us = time_launches(s, iters, [] {}, [&] { sg::gemm_variant(p, precision, variant, s); });
   hipLaunchKernelGGL(naive_gemm, dim3((n + 255) / 256, m), dim3(256), 0, s, a, w, m, n, k, cr);
   std::vector<float> x(m * (size_t)n), y(m * (size_t)n);
   HIP_CHECK(hipMemcpyAsync(x.data(), c, x.size() * 4, hipMemcpyDeviceToHost, s));

@@ -92,6 +92,14 @@ def lib():
     L.transformer_capture_hidden.argtypes = [TP, fp, fp]
     L.transformer_set_prefill_precision.restype = ctypes.c_int
     L.transformer_set_prefill_precision.argtypes = [TP, ctypes.c_int]
+    L.transformer_set_decode_mode.restype = ctypes.c_int
+    L.transformer_set_decode_mode.argtypes = [TP, ctypes.c_int]
+    L.transformer_decode_persistent_supported.restype = ctypes.c_int
+    L.transformer_decode_persistent_supported.argtypes = [TP]
+    L.transformer_decode_trace.argtypes = [TP, ctypes.c_int]
+    dp = ctypes.POINTER(ctypes.c_double)
+    L.transformer_decode_trace_read.restype = ctypes.c_int
+    L.transformer_decode_trace_read.argtypes = [TP, dp, ctypes.c_int]
     L.transformer_hip_version.restype = ctypes.c_char_p
     L.transformer_profile.argtypes = [TP, ctypes.c_int]
     L.transformer_profile_read.restype = ctypes.c_int
@@ -110,6 +118,9 @@ def _ints(seq: Sequence[int]):
 
 
 # Kernel classes reported by transformer_profile_read (include/transformer_hip.h).
+# transformer_set_decode_mode (include/transformer_hip.h)
+DECODE_PERSISTENT, DECODE_GRAPH, DECODE_EAGER = 0, 1, 2
+
 PROFILE_KERNELS = ["qkv_gemv", "attention_decode", "o_gemv", "gate_up_gemv", "down_gemv",
                    "logits_gemv", "argmax", "moe_route", "moe_gate_up", "moe_down",
                    "qkv_gemm", "attention_prefill", "o_gemm", "gate_up_gemm", "down_gemm",
@@ -186,6 +197,28 @@ class Transformer:
 
     def set_prefill_precision(self, mode: int) -> int:
         return int(self._lib.transformer_set_prefill_precision(self._t, mode))
+
+    def set_decode_mode(self, mode: int) -> int:
+        """DECODE_PERSISTENT, DECODE_GRAPH or DECODE_EAGER; returns the old mode."""
+        return int(self._lib.transformer_set_decode_mode(self._t, mode))
+
+    @property
+    def decode_persistent_supported(self) -> bool:
+        return bool(self._lib.transformer_decode_persistent_supported(self._t))
+
+    def decode_trace(self, enable: bool):
+        self._lib.transformer_decode_trace(self._t, 1 if enable else 0)
+
+    def decode_trace_read(self) -> np.ndarray:
+        """[5][n] per-step average microseconds per grid barrier of the
+        persistent step (rows: work, wait, staged, loop end, epilogue end;
+        see transformer_decode_trace_read); empty if never traced."""
+        n = self._lib.transformer_decode_trace_read(self._t, None, 0)
+        out = np.zeros((5, n), dtype=np.float64)
+        if n:
+            self._lib.transformer_decode_trace_read(
+                self._t, out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), out.size)
+        return out
 
     def profile(self, enable: bool):
         self._lib.transformer_profile(self._t, int(enable))

@@ -90,6 +90,10 @@ TINY: Dict[str, ModelShape] = {
                             std=0.25),
     "tiny-chunk": ModelShape("tiny-chunk", 64, 96, 2, 4, 1, 32, 128, 500000.0, 1e-5,
                              520, 4, ctx=600, std=0.25),
+    # Long context, 8 query heads on one kv head: decode attention over
+    # 32 key chunks of more than one 64-key tile each.
+    "tiny-long": ModelShape("tiny-long", 64, 96, 2, 8, 1, 32, 128, 500000.0, 1e-5,
+                            2200, 6, ctx=2300, std=0.25),
     "tiny-moe": ModelShape("tiny-moe", 64, 64, 2, 4, 2, 16, 256, 150000.0, 1e-5, 8, 8,
                            untied=True, experts=8, experts_per_tok=2,
                            model_type="stras_moe", std=0.25),

@@ -107,6 +107,99 @@ def test_predict_host_loop_equals_device_loop(model_dir):
     assert host == dev
 
 
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk", "tiny-long"])
+def test_decode_modes_agree(name, model_dir):
+    """The persistent decode step (one launch per token), the graph-replayed
+    per-kernel step and the same kernels launched eagerly give identical
+    greedy tokens, equal to the oracle's; a second persistent run after
+    reset repeats the first (barrier state carried across launches)."""
+    rt = runtime()
+    d = model_dir(name)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, 31)
+    steps = shp.decode_len + 1
+    om = oracle_model(d, 4)
+    otok = om.generate(prompt, steps)
+    with rt.Transformer(d) as t:
+        assert t.decode_persistent_supported
+        got = {}
+        for mode in (rt.DECODE_PERSISTENT, rt.DECODE_GRAPH, rt.DECODE_EAGER):
+            t.set_decode_mode(mode)
+            t.reset()
+            got[mode], _ = t.generate(prompt, steps)
+        t.set_decode_mode(rt.DECODE_PERSISTENT)
+        t.reset()
+        again, _ = t.generate(prompt, steps)
+    log(f"{name}: oracle {otok}")
+    log(f"{name}: persistent {got[rt.DECODE_PERSISTENT]} graph {got[rt.DECODE_GRAPH]}")
+    assert got[rt.DECODE_PERSISTENT] == otok
+    assert got[rt.DECODE_GRAPH] == otok
+    assert got[rt.DECODE_EAGER] == otok
+    assert again == otok
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-long"])
+def test_persistent_step_logits(name, model_dir):
+    """Single-token transformer_predict in DECODE_PERSISTENT mode runs the
+    persistent decode step; its logits (every layer, attention over the
+    cache, final norm) and its captured hidden states agree with the
+    oracle's at each of several positions, and the logits with the
+    per-kernel path's (DECODE_EAGER)."""
+    rt = runtime()
+    d = model_dir(name)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, 5)
+    nxt = synth.prompt_tokens(shp.vocab, 4, 6)
+    om = oracle_model(d, 4)
+    om.predict(prompt)
+    with rt.Transformer(d) as t:
+        assert t.decode_persistent_supported
+        t.set_decode_mode(rt.DECODE_PERSISTENT)
+        t.predict(prompt)
+        for i, tok in enumerate(nxt):
+            capture = i == len(nxt) - 1  # residual stream after every layer too
+            if capture:
+                ol, oh, of = om.predict([tok], capture=True)
+                gl, gh, gf = t.predict([tok], capture=True)
+                np.testing.assert_allclose(gh, oh, rtol=RTOL, atol=ATOL)
+                np.testing.assert_allclose(gf, of, rtol=RTOL, atol=ATOL)
+            else:
+                ol = om.predict([tok])
+                gl = t.predict([tok])
+            err = np.abs(gl - ol).max()
+            log(f"{name}: persistent step logits max |error| {err:.3g}")
+            np.testing.assert_allclose(gl, ol, rtol=RTOL, atol=ATOL)
+            assert err < 1e-3
+        t.reset()
+        t.set_decode_mode(rt.DECODE_EAGER)
+        t.predict(prompt)
+        el = [t.predict([tok]) for tok in nxt]
+        t.reset()
+        t.set_decode_mode(rt.DECODE_PERSISTENT)
+        t.predict(prompt)
+        pl = [t.predict([tok]) for tok in nxt]
+    for a, b in zip(el, pl):
+        np.testing.assert_allclose(b, a, rtol=1e-4, atol=1e-5)
+
+
+def test_grid_barrier_visibility():
+    """The fence-free grid barrier of the persistent decode step: values
+    written with agent-coherent stores before a barrier are read back by
+    another block after it, on every round (no stale value, no time-out)."""
+    import ctypes
+    rt = runtime()
+    L = rt.lib()
+    d = ctypes.c_double
+    fn = L.strasgpt_kbench_barrier
+    fn.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(d), ctypes.POINTER(ctypes.c_int),
+                                        ctypes.POINTER(ctypes.c_int)]
+    for blocks in (64, 256):
+        us, bad, to = d(), ctypes.c_int(), ctypes.c_int()
+        rc = fn(blocks, 300, 2, 256, ctypes.byref(us), ctypes.byref(bad), ctypes.byref(to))
+        log(f"barrier: {blocks} blocks, {us.value:.2f} us/round")
+        assert rc == 0 and bad.value == 0 and to.value == 0
+
+
 def test_logits_window_and_chunking(model_dir):
     """logits_count > 1 returns the last rows; a prompt split across calls
     matches one call (chunk invariance)."""
@@ -135,6 +228,7 @@ def test_moe_tiny_against_oracle(model_dir):
     om.reset()
     otok = om.generate(prompt, 9)
     with rt.Transformer(d) as t:
+        assert not t.decode_persistent_supported  # MoE layers: per-kernel path
         gl = t.predict(prompt)
         t.reset()
         gtok, _ = t.generate(prompt, 9)
