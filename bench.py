@@ -71,6 +71,38 @@ def cpu_baseline(d, shp, prompt, threads, decode_tokens):
     }
 
 
+COPY_PROBE_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_decode_kernels_qwen3-4b.json")
+
+
+def probe_traffic(t, prompt):
+    """Kernels for the HBM traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then
+    WRITE_SIZE): copy_probe_kernel of known size, then eager decode steps."""
+    import ctypes
+    from strasgpt_amd import runtime
+    lib = runtime.lib()
+    lib.strasgpt_kbench_copy.argtypes = [ctypes.c_size_t, ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_double)]
+    us = ctypes.c_double()
+    lib.strasgpt_kbench_copy(COPY_PROBE_BYTES, 3, ctypes.byref(us))
+    log(f"copy probe: {COPY_PROBE_BYTES} bytes in {us.value:.1f} us")
+    t.set_decode_mode(runtime.DECODE_EAGER)
+    t.reset()
+    t.generate(prompt[:16], 5)
+    log("probe decode done")
+
+
+def traffic_for(kernel):
+    """HBM bytes per launch of a decode kernel class from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on copy_probe_kernel), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            table = json.load(f)
+        return table["kernels"][kernel]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -82,6 +114,9 @@ def main():
     ap.add_argument("--cpu-decode-tokens", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--precision", type=int, default=0, help="prefill GEMM: 0 bf16x2, 1 bf16")
+    ap.add_argument("--probe-traffic", action="store_true",
+                    help="only launch the kernels an HBM-counter run needs (a 256 MiB copy, "
+                         "then a 16-token prefill and 4 eager decode steps); prints nothing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU runs are "
@@ -98,6 +133,10 @@ def main():
     t = runtime.Transformer(d)
     t.set_prefill_precision(args.precision)
     log(f"loaded into HBM in {time.time() - t0:.1f}s; {runtime.version()}")
+
+    if args.probe_traffic:
+        probe_traffic(t, prompt)
+        return
 
     for i in range(args.warmup):
         t.reset()
@@ -143,7 +182,7 @@ def main():
     kd = kernels[dom]
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(kd["gbs"], 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kd["gbs"] / HBM_PEAK_GBS, 4),
-                "traffic": None, "avg_us": round(kd["avg_us"], 2),
+                "traffic": traffic_for(dom), "avg_us": round(kd["avg_us"], 2),
                 "bytes_per_launch": kd["bytes_per_launch"]}
     pre = {k: stats[k] for k in prefill_kernels if k in stats}
     roofline_prefill = None

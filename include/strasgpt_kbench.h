@@ -35,6 +35,11 @@ int strasgpt_kbench_gemm(int m, int n, int k, int precision, int variant, int it
                          double* avg_us, double* rel_err);
 int strasgpt_kbench_gemm_variants(void);
 
+/* Copy of `bytes` (multiple of 16) between two device buffers, `iters`
+ * launches of copy_probe_kernel (reads and writes exactly `bytes` each):
+ * the calibration kernel for HBM traffic counters. */
+int strasgpt_kbench_copy(size_t bytes, int iters, double* avg_us);
+
 /* Grid barrier cost: one cooperative launch of `blocks` x 256 threads doing
  * `rounds` barriers, each block writing `words` values before each barrier.
  * fence 0: plain stores, no fences, no check; 1: fenced barrier, plain

@@ -51,6 +51,15 @@ __global__ void touch_pages(const uint32_t* p, size_t bytes, uint32_t* sink) {
   }
 }
 
+// Plain copy dst = src of n float4 (the calibration kernel for HBM traffic
+// counters: it reads and writes exactly 16 n bytes).
+__global__ __launch_bounds__(256) void copy_probe_kernel(const float4* __restrict__ src,
+                                                         float4* __restrict__ dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
 __global__ void naive_gemv(const uint16_t* w, const uint16_t* w2, const float* x, int n, int k,
                            float* y) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
@@ -210,6 +219,25 @@ extern "C" int strasgpt_kbench_barrier(int blocks, int rounds, int fence, int wo
   HIP_CHECK(hipFree(state));
   HIP_CHECK(hipFree(flags));
   HIP_CHECK(hipFree(data));
+  HIP_CHECK(hipStreamDestroy(s));
+  return 0;
+}
+
+extern "C" int strasgpt_kbench_copy(size_t bytes, int iters, double* avg_us) {
+  if (bytes < 16 || bytes % 16 || iters <= 0) return -1;
+  hipStream_t s;
+  HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  float4 *a, *b;
+  HIP_CHECK(hipMalloc(&a, bytes));
+  HIP_CHECK(hipMalloc(&b, bytes));
+  hipLaunchKernelGGL(fill_f32, dim3(1024), dim3(256), 0, s, (float*)a, bytes / 4, 7u);
+  const size_t n = bytes / 16;
+  *avg_us = time_launches(s, iters, [] {}, [&] {
+    hipLaunchKernelGGL(copy_probe_kernel, dim3(2048), dim3(256), 0, s, a, b, n);
+  });
+  HIP_CHECK(hipStreamSynchronize(s));
+  HIP_CHECK(hipFree(a));
+  HIP_CHECK(hipFree(b));
   HIP_CHECK(hipStreamDestroy(s));
   return 0;
 }
