@@ -375,6 +375,29 @@ __device__ __forceinline__ void norm_rope_vec(const float* src, const uint16_t* 
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// N consecutive floats from LDS (16-byte aligned when N % 4 == 0, 8-byte
+// when N == 2), in the widest reads.
+template <int N>
+__device__ __forceinline__ void lds_vec(const float* src, float* dst) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const float4 f = *(const float4*)(src + i);
+      dst[i] = f.x;
+      dst[i + 1] = f.y;
+      dst[i + 2] = f.z;
+      dst[i + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      const float2 f = *(const float2*)(src + i);
+      dst[i] = f.x;
+      dst[i + 1] = f.y;
+    }
+  }
+}
+
 // LDS floats used by the attention phase before its K/V tile buffers.
 template <int HD>
 constexpr int attn_lds_head() { return 10 * HD + kMaxG * 64 + 4 * kMaxG + kT * kMaxG; }
@@ -461,6 +484,8 @@ __device__ __forceinline__ void attention_phase(const DecodeParams* lp, const De
   mark(2);
   const float* kb = ly.kcache + (size_t)g * U(lp->ctx) * HD;
   const float* vb = ly.vcache + (size_t)g * U(lp->ctx) * HD;
+  // Scores: 8 lanes per key (KP dims each). P.V: thread (d, kg) takes the
+  // tile's keys kg*KP .. kg*KP + KP - 1 (64 / KG = KP keys per group).
   const int d = tid % HD, kg = tid / HD, kk = tid / 8, pp = tid % 8;
   float acc[kMaxG];
 #pragma unroll
@@ -468,20 +493,28 @@ __device__ __forceinline__ void attention_phase(const DecodeParams* lp, const De
   for (int t0 = s0; t0 < s1; t0 += 64) {
     const int n = min(64, s1 - t0);
     if (t0 != s0) {  // later tiles (contexts over 64 keys per chunk)
+      __syncthreads();  // previous tile fully read
       dma_kv_tile<HD>(kb, vb, t0, n, kt, vt);
       __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
       __syncthreads();
     }
-    const float* krow = (kk < n && t0 + kk == P) ? kn + pp * KP : kt + kk * HD + pp * KP;
+    if (has_new && P >= t0 && P < t0 + n) {  // row P: this step's key and value
+      for (int e = tid; e < HD; e += kT) {
+        kt[(P - t0) * HD + e] = kn[e];
+        vt[(P - t0) * HD + e] = vn[e];
+      }
+      __syncthreads();
+    }
     float kv[KP];
-#pragma unroll
-    for (int i = 0; i < KP; i++) kv[i] = kk < n ? krow[i] : 0.0f;
+    lds_vec<KP>(kt + kk * HD + pp * KP, kv);
 #pragma unroll
     for (int h = 0; h < kMaxG; h++) {
       if (h < G) {
+        float q[KP];
+        lds_vec<KP>(qs + h * HD + pp * KP, q);
         float a = 0.0f;
 #pragma unroll
-        for (int i = 0; i < KP; i++) a = fmaf(qs[h * HD + pp * KP + i], kv[i], a);
+        for (int i = 0; i < KP; i++) a = fmaf(q[i], kv[i], a);
         a = group_sum<8>(a);
         if (pp == 0 && kk < n) sc[h * 64 + kk] = a / inv;
       }
@@ -491,7 +524,7 @@ __device__ __forceinline__ void attention_phase(const DecodeParams* lp, const De
       const float s = lane < n ? sc[wave * 64 + lane] : -INFINITY;
       const float mo = st[wave], mn = fmaxf(mo, wave_max(s));
       const float e = lane < n ? expf(s - mn) : 0.0f;
-      sc[wave * 64 + lane] = e;
+      sc[wave * 64 + lane] = e;  // 0 past the tile's keys
       const float sum = wave_sum(e);
       if (lane == 0) {
         const float f = expf(mo - mn);
@@ -501,20 +534,20 @@ __device__ __forceinline__ void attention_phase(const DecodeParams* lp, const De
       }
     }
     __syncthreads();
+    float v[KP];
 #pragma unroll
-    for (int h = 0; h < kMaxG; h++)
-      if (h < G) acc[h] *= st[2 * kMaxG + h];
+    for (int i = 0; i < KP; i++) v[i] = kg * KP + i < n ? vt[(kg * KP + i) * HD + d] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < KP; i++) {
-      const int jj = kg + i * KG;
-      if (jj < n) {
-        const float v = t0 + jj == P ? vn[d] : vt[jj * HD + d];
+    for (int h = 0; h < kMaxG; h++) {
+      if (h < G) {
+        float w[KP];
+        lds_vec<KP>(sc + h * 64 + kg * KP, w);
+        float a = acc[h] * st[2 * kMaxG + h];
 #pragma unroll
-        for (int h = 0; h < kMaxG; h++)
-          if (h < G) acc[h] = fmaf(sc[h * 64 + jj], v, acc[h]);
+        for (int i = 0; i < KP; i++) a = fmaf(w[i], v[i], a);
+        acc[h] = a;
       }
     }
-    __syncthreads();
   }
   mark(3);
 #pragma unroll
