@@ -138,3 +138,20 @@ __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
   ss /= (float)n;
   return (float)(1.0 / (double)sqrtf(ss + eps));
 }
+
+// Agent-coherent scalar access: relaxed atomics at device scope, which
+// bypass the per-XCD L2 for data exchanged between blocks of one launch.
+// A store is visible to another block's cload once the storing wave has
+// waited for its vector memory operations to complete.
+__device__ __forceinline__ float cload(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int cload(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void cstore(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void cstore(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}

@@ -7,13 +7,15 @@
 // LDS; 4x4 register-blocked fp32 scores, online softmax (running max and
 // sum per query row), P kept in LDS for the P.V product.
 //
-// Decode: split-K over the cached positions ("flash decoding"): one block
-// per (64-key chunk, query head) writes (max, sum, partial output); a
-// second small kernel combines the chunks of each head (the kernel boundary
-// is the only synchronisation: no device-wide fences).
-// The block also applies this step's QK RMSNorm + RoPE to q and to the new
-// key (read raw from the QKV projection), and one block per KV head writes
-// the processed key into the cache.
+// Decode: split-K over the cached positions ("flash decoding") in one
+// launch: one block per (key chunk, kv head) for all query heads of the
+// group writes (max, sum, partial output) per head, and the last block of
+// each kv head to finish combines the chunks. The blocks also apply this
+// step's QK RMSNorm + RoPE to q and to the new key (read raw from the QKV
+// projection); the block holding the newest position writes the processed
+// key into the cache.
+#include <algorithm>
+
 #include "device_common.h"
 #include "hip_check.h"
 #include "kernels.h"
@@ -23,6 +25,23 @@ namespace sg {
 namespace {
 
 constexpr int BQ = 64, BKV = 64;
+
+// Decode: threads per block, keys per LDS tile, query heads per kv head
+// and key chunks per kv head, at most.
+constexpr int kDecThreads = 256;
+constexpr int kDecTile = 32;
+constexpr int kDecMaxG = 8;
+constexpr int kDecMaxChunks = 32;
+constexpr int kDecMinChunk = 16;  // keys per chunk, at least
+
+// Split of `total` keys into nch chunks of len keys (the last may be
+// shorter, none is empty): as many chunks as allowed, each of at least
+// kDecMinChunk keys.
+__host__ __device__ inline void attention_decode_split(int total, int max_chunks, int& nch, int& len) {
+  nch = total < max_chunks * kDecMinChunk ? (total + kDecMinChunk - 1) / kDecMinChunk : max_chunks;
+  len = (total + nch - 1) / nch;
+  nch = (total + len - 1) / len;
+}
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
@@ -163,185 +182,361 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
   }
 }
 
-// RMSNorm (optional) + RoPE of one head vector by one wavefront, result in
-// LDS `dst`. Same arithmetic as the reference (source/transformer.c:
-// 1293-1323).
+// LDS layout of the decode kernel (floats).
 template <int HD>
-__device__ void norm_rope_wave(const float* src, const uint16_t* nw, float eps,
-                               const float* cs, int pb, int po, int pst, float* dst) {
-#pragma clang fp contract(off)
-  const int lane = threadIdx.x % WAVE;
-  float ss = 0.0f;
-  for (int e = lane; e < HD; e += WAVE) {
-    const float x = src[e];
-    dst[e] = x;
-    ss = fmaf(x, x, ss);
-  }
-  ss = wave_sum(ss);
-  if (nw) {
-    const float s = rms_scale(ss, HD, eps);
-    for (int e = lane; e < HD; e += WAVE) dst[e] = (dst[e] * s) * bf16_to_f32(nw[e]);
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  float r0[4], r1[4];
-  int hh[4];
-  int cnt = 0;
-  for (int i = lane; i * pst < pb; i += WAVE) {
-    const int h = i * pst;
-    const float fr = cs[h], fi = cs[h + po];
-    const float v0 = dst[h], v1 = dst[h + po];
-    r0[cnt] = v0 * fr - v1 * fi;
-    r1[cnt] = v0 * fi + v1 * fr;
-    hh[cnt] = h;
-    cnt++;
-  }
-  __builtin_amdgcn_wave_barrier();
-  for (int c = 0; c < cnt; c++) {
-    dst[hh[c]] = r0[c];
-    dst[hh[c] + po] = r1[c];
-  }
-}
+struct DecLds {
+  static constexpr int KG = kDecThreads / HD;  // key groups for P.V
+  static constexpr int qs = 0;                                 // [kDecMaxG][HD]
+  static constexpr int kn = qs + kDecMaxG * HD;                // [HD] new key
+  static constexpr int sc = kn + HD;                           // [kDecMaxG][kDecTile]
+  static constexpr int st = sc + kDecMaxG * kDecTile;          // [3][kDecMaxG] m, l, rescale
+  static constexpr int flag = st + 4 * kDecMaxG;               // [4]
+  static constexpr int tiles = flag + 4;                       // [2][K|V][kDecTile][HD]
+  // After the last tile, over the tile buffers:
+  static constexpr int red = tiles;                            // [KG][kDecMaxG][HD]
+  static constexpr int wts = red + KG * kDecMaxG * HD;         // [kDecMaxG][kDecMaxChunks + 1]
+  static constexpr int total = std::max(tiles + 4 * kDecTile * HD, wts + kDecMaxG * (kDecMaxChunks + 1));
+};
 
-// One block per (64-key chunk, query head). Every global load of the block
-// (this chunk's keys and values, the query row, the step's raw key) is
-// issued in one round at kernel start, four lanes per key row (128-bit,
-// coalesced): the key quarter stays in registers for the scores, the value
-// quarter goes to LDS for P.V. The block holding position P uses the
-// processed new key for that row and (for the first query head of its
-// group) writes it to the cache.
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Keys [t0, t0 + n) of a kv head (rows of HD floats, contiguous) into the
+// LDS tiles kt / vt by the global-to-LDS DMA: 16 bytes per lane, each wave
+// filling 1 KiB of LDS per instruction. No registers are held; the caller
+// waits for vector memory operations and syncs the block before reading.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p) {
-  constexpr int CH = 64, Q4 = HD / 4, NV = Q4 / 4;  // dims per lane, float4 per lane
-  __shared__ __attribute__((aligned(16))) float vs[CH * HD];
-  __shared__ __attribute__((aligned(16))) float qs[HD];
-  __shared__ __attribute__((aligned(16))) float kn[HD];
-  __shared__ float sc[CH];
-  __shared__ float red[256 / HD][HD];
-  __shared__ float stat[2];
-
-  const int split = blockIdx.x, head = blockIdx.y;
-  const int G = p.q_heads / p.kv_heads, kvh = head / G;
-  const int P = *p.pos, total = P + 1;
-  const int nsplit = (total + CH - 1) / CH;
-  if (split >= nsplit) return;
-  const int s0 = split * CH, s1 = min(s0 + CH, total), n = s1 - s0;
-  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-  const int j = tid / 4, qt = tid % 4;
-  const bool has_new = s1 == total;
-  const float* kbase = p.kcache + (size_t)kvh * p.ctx * HD;
-  const float* vbase = p.vcache + (size_t)kvh * p.ctx * HD;
-
-  float4 kr[NV], vr[NV];
-  const bool row = j < n;
-  const bool cached = row && s0 + j != P;
-#pragma unroll
-  for (int i = 0; i < NV; i++) {
-    kr[i] = cached ? *(const float4*)(kbase + (size_t)(s0 + j) * HD + qt * Q4 + 4 * i)
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
-    vr[i] = row ? *(const float4*)(vbase + (size_t)(s0 + j) * HD + qt * Q4 + 4 * i)
-                : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  const float* cs = p.rope + (size_t)P * HD;
-  if (wave == 0)
-    norm_rope_wave<HD>(p.q + (size_t)head * HD, p.qn, p.eps, cs, p.pair_bound, p.pair_offset,
-                       p.pair_stride, qs);
-  if (wave == 1 && has_new)
-    norm_rope_wave<HD>(p.kraw + (size_t)kvh * HD, p.kn, p.eps, cs, p.pair_bound,
-                       p.pair_offset, p.pair_stride, kn);
-#pragma unroll
-  for (int i = 0; i < NV; i++) *(float4*)&vs[j * HD + qt * Q4 + 4 * i] = vr[i];
-  __syncthreads();
-  if (has_new && head % G == 0) {
-    for (int e = tid; e < HD; e += 256) p.kcache_w[((size_t)kvh * p.ctx + P) * HD + e] = kn[e];
-  }
-  if (row && !cached) {
-#pragma unroll
-    for (int i = 0; i < NV; i++) kr[i] = *(const float4*)&kn[qt * Q4 + 4 * i];
-  }
-  float a = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NV; i++) {
-    const float4 q = *(const float4*)&qs[qt * Q4 + 4 * i];
-    a = fmaf(q.x, kr[i].x, a);
-    a = fmaf(q.y, kr[i].y, a);
-    a = fmaf(q.z, kr[i].z, a);
-    a = fmaf(q.w, kr[i].w, a);
-  }
-  a = group_sum<4>(a);
-  if (qt == 0 && row) sc[j] = a / sqrtf((float)HD);
-  __syncthreads();
-  if (wave == 0) {
-    const float v = lane < n ? sc[lane] : -INFINITY;
-    const float mx = wave_max(v);
-    const float e = lane < n ? expf(v - mx) : 0.0f;
-    if (lane < n) sc[lane] = e;
-    const float sum = wave_sum(e);
-    if (lane == 0) {
-      stat[0] = mx;
-      stat[1] = sum;
+__device__ __forceinline__ void dma_kv(const float* kb, const float* vb, int t0, int n, float* kt,
+                                       float* vt) {
+  const int units = n * HD / 4;
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const float* ks = kb + (size_t)t0 * HD;
+  const float* vs = vb + (size_t)t0 * HD;
+  for (int u0 = wave * WAVE; u0 < units; u0 += kDecThreads) {
+    const int u = u0 + lane;
+    if (u < units) {
+      __builtin_amdgcn_global_load_lds((const void*)(ks + u * 4), (lds_ptr)(kt + u0 * 4), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vs + u * 4), (lds_ptr)(vt + u0 * 4), 16, 0, 0);
     }
   }
-  __syncthreads();
-  constexpr int KG = 256 / HD;
-  const int d = tid % HD, kg = tid / HD;
-  {
-    float acc = 0.0f;
-#pragma unroll 8
-    for (int jj = kg; jj < n; jj += KG) acc = fmaf(sc[jj], vs[jj * HD + d], acc);
-    red[kg][d] = acc;
-  }
-  __syncthreads();
-  float* part = p.partial + ((size_t)head * p.splits + split) * (HD + 2);
-  if (tid < HD) {
-    float acc = 0.0f;
+}
+
+// N consecutive floats of LDS into registers, in 16-byte (8-byte for N == 2)
+// reads.
+template <int N>
+__device__ __forceinline__ void lds_read(const float* src, float* dst) {
+  if constexpr (N % 4 == 0) {
 #pragma unroll
-    for (int k = 0; k < KG; k++) acc += red[k][tid];
-    part[2 + tid] = acc;
-  }
-  if (tid == 0) {
-    part[0] = stat[0];
-    part[1] = stat[1];
+    for (int i = 0; i < N; i += 4) {
+      const float4 f = *(const float4*)(src + i);
+      dst[i] = f.x;
+      dst[i + 1] = f.y;
+      dst[i + 2] = f.z;
+      dst[i + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      const float2 f = *(const float2*)(src + i);
+      dst[i] = f.x;
+      dst[i + 1] = f.y;
+    }
   }
 }
 
-// Combines the per-chunk (max, sum, partial output) of one head:
-// M = max m_i, out = sum_i o_i e^(m_i - M) / sum_i l_i e^(m_i - M).
+// RMSNorm (when nw is given) and RoPE of one head vector held by a wave:
+// xv / wv are the lane's elements lane + i*64 of the vector and of the norm
+// weights, fr / fi the rotation of the lane's pair (element lane*pst and
+// lane*pst + po, when lane*pst < pb). Result in LDS dst. Same arithmetic as
+// the reference (source/transformer.c:1293-1323).
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_decode_combine_kernel(AttnParams p) {
-  __shared__ float wts[1024];
-  __shared__ float red[HD / WAVE > 0 ? HD / WAVE : 1];
-  const int head = blockIdx.x, d = threadIdx.x;
-  const int nsplit = (*p.pos + 1 + 63) / 64;
-  const float* pb = p.partial + (size_t)head * p.splits * (HD + 2);
-  // chunk maxima in parallel, then M = max, weights e^(m_i - M)
-  float mx = -INFINITY;
-  for (int i = d; i < nsplit; i += HD) {
-    wts[i] = pb[(size_t)i * (HD + 2)];
-    mx = fmaxf(mx, wts[i]);
+__device__ __forceinline__ void norm_rope_regs(const float* xv, const float* wv, bool norm, float eps,
+                                               float fr, float fi, int pb, int po, int pst, float* dst) {
+#pragma clang fp contract(off)
+  constexpr int PER = (HD + WAVE - 1) / WAVE;
+  const int lane = threadIdx.x % WAVE;
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; i++)
+    if (lane + i * WAVE < HD) ss = fmaf(xv[i], xv[i], ss);
+  ss = wave_sum(ss);
+  const float s = norm ? rms_scale(ss, HD, eps) : 1.0f;
+#pragma unroll
+  for (int i = 0; i < PER; i++)
+    if (lane + i * WAVE < HD) dst[lane + i * WAVE] = norm ? (xv[i] * s) * wv[i] : xv[i];
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  const int h = lane * pst;
+  float r0 = 0.0f, r1 = 0.0f;
+  if (h < pb) {
+    const float v0 = dst[h], v1 = dst[h + po];
+    r0 = v0 * fr - v1 * fi;
+    r1 = v0 * fi + v1 * fr;
   }
-  mx = wave_max(mx);
-  if (HD > WAVE) {
-    if (d % WAVE == 0) red[d / WAVE] = mx;
+  __builtin_amdgcn_wave_barrier();
+  if (h < pb) {
+    dst[h] = r0;
+    dst[h + po] = r1;
+  }
+}
+
+// Decode attention in one launch. Block (chunk c, kv head g) takes keys
+// [c*len, min(P+1, (c+1)*len)) for the G query heads of kv head g (the K/V
+// rows are read once for the group), in tiles of kDecTile keys brought to
+// LDS by DMA, double-buffered: tile t+1 is in flight while tile t is used.
+// Per tile: scores (8 lanes per key), an online softmax per head (running
+// max m, sum l, rescale of the accumulators), P.V (thread = output dim x
+// key group). The block stores (m, l, unnormalised output) per head with
+// agent-coherent stores, then counts itself done on the kv head's counter;
+// the last block of the head reads all chunks' partials and writes
+//   att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c,  M = max_c m_c,
+// and resets the counter for the next launch. The block holding position
+// P also normalises and rotates this step's key and writes it to the
+// cache (the value row was written by the QKV projection). Each stage
+// issues all its global loads before using any (one memory round trip per
+// stage: inputs, partial stores, counter, partial loads).
+template <int HD>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(AttnParams p) {
+  using L = DecLds<HD>;
+  constexpr int KP = HD / 8;  // dims per lane for scores; keys per group for P.V
+  constexpr int KG = L::KG;
+  constexpr int NW = kDecThreads / WAVE;
+  constexpr int PER = (HD + WAVE - 1) / WAVE;
+  constexpr int MAXV = (kDecMaxG + 1 + NW - 1) / NW;  // head vectors per wave
+  static_assert(kDecTile * 8 == kDecThreads && KG * KP == kDecTile, "tile shape");
+  static_assert(kDecMaxChunks <= WAVE, "one lane per chunk in the combine");
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* qs = lds + L::qs;
+  float* kn = lds + L::kn;
+  float* sc = lds + L::sc;
+  float* st = lds + L::st;
+  float* wts = lds + L::wts;
+  float* red = lds + L::red;
+  int* flag = (int*)(lds + L::flag);
+  float* tiles = lds + L::tiles;
+
+  const int c = blockIdx.x, g = blockIdx.y;
+  const int G = p.q_heads / p.kv_heads;
+  const int P = *p.pos, total = P + 1;
+  int nch, len;
+  attention_decode_split(total, p.splits, nch, len);
+  if (c >= nch) return;  // not counted: the last block waits for nch arrivals
+  const int s0 = c * len, s1 = min(total, s0 + len);
+  const bool has_new = s1 == total;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const float* kb = p.kcache + (size_t)g * p.ctx * HD;
+  const float* vb = p.vcache + (size_t)g * p.ctx * HD;
+
+  // Stage 1 loads: the first K/V tile, the raw q (and new k) vectors, their
+  // norm weights and the rotation of position P.
+  dma_kv<HD>(kb, vb, s0, min(kDecTile, s1 - s0), tiles, tiles + kDecTile * HD);
+  const float* cs = p.rope + (size_t)P * HD;
+  const int nvec = G + (has_new ? 1 : 0);
+  const int hp = lane * p.pair_stride;
+  // Loads are unconditional (out-of-range ones read a valid element and are
+  // discarded), so that the compiler issues them all before the first use.
+  float xv[MAXV][PER], wv[MAXV][PER], fr[MAXV], fi[MAXV];
+  const int hq = hp < p.pair_bound ? hp : 0;
+#pragma unroll
+  for (int j = 0; j < MAXV; j++) {
+    const int v = wave + j * NW;
+    const bool key = v == G;
+    const float* src = key ? p.kraw + (size_t)g * HD : p.q + (size_t)(g * G + (v < G ? v : 0)) * HD;
+    const uint16_t* nw = key ? p.kn : p.qn;
+    const uint16_t* nws = nw ? nw : (const uint16_t*)src;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int e = min(lane + i * WAVE, HD - 1);
+      xv[j][i] = src[e];
+      wv[j][i] = bf16_to_f32(nws[e]);
+    }
+    fr[j] = cs[hq];
+    fi[j] = cs[hq + p.pair_offset];
+  }
+#pragma unroll
+  for (int j = 0; j < MAXV; j++) {
+    const int v = wave + j * NW;
+    if (v < nvec)
+      norm_rope_regs<HD>(xv[j], wv[j], (v == G ? p.kn : p.qn) != nullptr, p.eps, fr[j], fi[j],
+                         p.pair_bound, p.pair_offset, p.pair_stride, v == G ? kn : qs + v * HD);
+  }
+  if (tid < kDecMaxG) {
+    st[tid] = -INFINITY;
+    st[kDecMaxG + tid] = 0.0f;
+  }
+  const float scale = sqrtf((float)HD);
+  const int d = tid % HD, kg = tid / HD, kk = tid / 8, pp = tid % 8;
+  float acc[kDecMaxG];
+#pragma unroll
+  for (int h = 0; h < kDecMaxG; h++) acc[h] = 0.0f;
+
+  for (int t0 = s0, buf = 0; t0 < s1; t0 += kDecTile, buf ^= 1) {
+    const int n = min(kDecTile, s1 - t0);
+    float* kt = tiles + buf * 2 * kDecTile * HD;
+    float* vt = kt + kDecTile * HD;
+    __builtin_amdgcn_s_waitcnt(0);  // this tile (and the q/k loads) landed
+    __syncthreads();                // ... for every wave; previous tile consumed
+    if (t0 + kDecTile < s1) {
+      float* nk = tiles + (buf ^ 1) * 2 * kDecTile * HD;
+      dma_kv<HD>(kb, vb, t0 + kDecTile, min(kDecTile, s1 - t0 - kDecTile), nk, nk + kDecTile * HD);
+    }
+    if (has_new && P >= t0 && P < t0 + n) {  // row P: this step's processed key
+      for (int e = tid; e < HD; e += kDecThreads) kt[(P - t0) * HD + e] = kn[e];
+      __syncthreads();
+    }
+    float kv[KP];
+    lds_read<KP>(kt + kk * HD + pp * KP, kv);
+#pragma unroll
+    for (int h = 0; h < kDecMaxG; h++) {
+      if (h < G) {
+        float q[KP];
+        lds_read<KP>(qs + h * HD + pp * KP, q);
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KP; i++) a = fmaf(q[i], kv[i], a);
+        a = group_sum<8>(a);
+        if (pp == 0) sc[h * kDecTile + kk] = a / scale;
+      }
+    }
     __syncthreads();
-    for (int w = 0; w < HD / WAVE; w++) mx = fmaxf(mx, red[w]);
+    for (int h = wave; h < G; h += kDecThreads / WAVE) {  // online softmax of head h
+      const float s = lane < n ? sc[h * kDecTile + lane] : -INFINITY;
+      const float mo = st[h], mn = fmaxf(mo, wave_max(s));
+      const float e = lane < n ? expf(s - mn) : 0.0f;
+      if (lane < kDecTile) sc[h * kDecTile + lane] = e;  // 0 past the tile's keys
+      const float sum = wave_sum(e);
+      if (lane == 0) {
+        const float f = expf(mo - mn);
+        st[2 * kDecMaxG + h] = f;
+        st[kDecMaxG + h] = st[kDecMaxG + h] * f + sum;
+        st[h] = mn;
+      }
+    }
+    __syncthreads();
+    float v[KP];
+#pragma unroll
+    for (int i = 0; i < KP; i++) v[i] = kg * KP + i < n ? vt[(kg * KP + i) * HD + d] : 0.0f;
+#pragma unroll
+    for (int h = 0; h < kDecMaxG; h++) {
+      if (h < G) {
+        float w[KP];
+        lds_read<KP>(sc + h * kDecTile + kg * KP, w);
+        float a = acc[h] * st[2 * kDecMaxG + h];
+#pragma unroll
+        for (int i = 0; i < KP; i++) a = fmaf(w[i], v[i], a);
+        acc[h] = a;
+      }
+    }
+  }
+  __syncthreads();  // last tile consumed (red overlaps the tiles)
+#pragma unroll
+  for (int h = 0; h < kDecMaxG; h++)
+    if (h < G) red[(kg * kDecMaxG + h) * HD + d] = acc[h];
+  __syncthreads();
+  for (int o = tid; o < G * HD; o += kDecThreads) {
+    const int h = o / HD, dd = o % HD;
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KG; k++) a += red[(k * kDecMaxG + h) * HD + dd];
+    float* part = p.partial + ((size_t)(g * G + h) * p.splits + c) * (HD + 2);
+    cstore(part + 2 + dd, a);
+    if (dd == 0) {
+      cstore(part, st[h]);
+      cstore(part + 1, st[kDecMaxG + h]);
+    }
+  }
+  if (has_new) {  // cache row P of kv head g, read by later steps
+    float* kc = p.kcache_w + ((size_t)g * p.ctx + P) * HD;
+    for (int e = tid; e < HD; e += kDecThreads) kc[e] = kn[e];
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // partials stored (agent-coherent)
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned done = __hip_atomic_fetch_add(p.counters + g, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    flag[0] = done == (unsigned)(nch - 1);
   }
   __syncthreads();
-  for (int i = d; i < nsplit; i += HD) wts[i] = expf(wts[i] - mx);
-  __syncthreads();
-  float L = 0.0f, o = 0.0f;
-#pragma unroll 4
-  for (int i = 0; i < nsplit; i++) {
-    const float* q = pb + (size_t)i * (HD + 2);
-    L = fmaf(q[1], wts[i], L);
-    o = fmaf(q[2 + d], wts[i], o);
+  if (!flag[0]) return;
+
+  // Last block of kv head g: combine the nch chunks of its G heads, two
+  // outputs per thread at a time (one round for G * HD <= 512). The
+  // statistics and the first round's partials are loaded before any use.
+  float m[MAXV], l[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; j++) {
+    const int h = wave + j * NW;
+    const float* pb = p.partial + (size_t)(g * G + h) * p.splits * (HD + 2) + (size_t)lane * (HD + 2);
+    const bool ok = h < G && lane < nch;
+    m[j] = ok ? cload(pb) : -INFINITY;
+    l[j] = ok ? cload(pb + 1) : 0.0f;
   }
-  p.out[(size_t)head * HD + d] = o / L;
+  for (int o0 = 0; o0 < G * HD; o0 += 2 * kDecThreads) {
+    float x[2][kDecMaxChunks];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int o = o0 + tid + r * kDecThreads, h = o / HD, dd = o % HD;
+      const float* pb = p.partial + (size_t)(g * G + h) * p.splits * (HD + 2) + 2 + dd;
+#pragma unroll
+      for (int i = 0; i < kDecMaxChunks; i++)
+        x[r][i] = o < G * HD && i < nch ? cload(pb + (size_t)i * (HD + 2)) : 0.0f;
+    }
+    if (o0 == 0) {
+#pragma unroll
+      for (int j = 0; j < MAXV; j++) {
+        const int h = wave + j * NW;
+        if (h < G) {
+          const float M = wave_max(m[j]);
+          const float w = lane < nch ? expf(m[j] - M) : 0.0f;
+          if (lane < kDecMaxChunks) wts[h * (kDecMaxChunks + 1) + lane] = w;
+          const float wl = wave_sum(w * l[j]);
+          if (lane == 0) wts[h * (kDecMaxChunks + 1) + kDecMaxChunks] = wl;
+        }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int o = o0 + tid + r * kDecThreads, h = o / HD, dd = o % HD;
+      if (o < G * HD) {
+        const float* w = wts + h * (kDecMaxChunks + 1);
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kDecMaxChunks; i++)
+          if (i < nch) a = fmaf(w[i], x[r][i], a);
+        p.out[(size_t)(g * G + h) * HD + dd] = a / w[kDecMaxChunks];
+      }
+    }
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
 
-int attention_decode_splits(int ctx, int chunk) { return (ctx + chunk - 1) / chunk; }
+// Chunks per kv head: up to 512 blocks (two per CU fit at once).
+int attention_decode_chunks(int kv_heads) {
+  return std::max(1, std::min(kDecMaxChunks, 512 / std::max(1, kv_heads)));
+}
+
+void attention_init() {
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(DecLds<16>::total * sizeof(float))));
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<32>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(DecLds<32>::total * sizeof(float))));
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(DecLds<64>::total * sizeof(float))));
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(DecLds<128>::total * sizeof(float))));
+}
+
+size_t attention_decode_lds_bytes(int hd) {
+  switch (hd) {
+    case 16: return DecLds<16>::total * sizeof(float);
+    case 32: return DecLds<32>::total * sizeof(float);
+    case 64: return DecLds<64>::total * sizeof(float);
+    case 128: return DecLds<128>::total * sizeof(float);
+    default: return 0;
+  }
+}
 
 void attention_prefill(const AttnParams& p, hipStream_t s) {
   if (p.T <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
@@ -358,16 +553,20 @@ void attention_prefill(const AttnParams& p, hipStream_t s) {
 }
 
 void attention_decode(const AttnParams& p, hipStream_t s) {
-  if (p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
-  if (p.chunk != 64) ST_DIE("decode attention chunk must be 64");
-  if (p.splits != attention_decode_splits(p.ctx, p.chunk)) ST_DIE("decode split count mismatch");
-  if (p.splits > 1024) ST_DIE("decode attention supports contexts up to 65536");
-  dim3 grid(p.splits, p.q_heads);
+  const int G = p.kv_heads > 0 ? p.q_heads / p.kv_heads : 0;
+  if (G <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
+  if (G > kDecMaxG) ST_DIE("decode attention supports at most 8 query heads per kv head");
+  if (p.splits < 1 || p.splits > kDecMaxChunks) ST_DIE("decode attention chunk count out of range");
+  if (!p.counters || !p.partial) ST_DIE("decode attention needs its partial buffer and counters");
+  if (p.pair_stride < 1 || (p.pair_bound + p.pair_stride - 1) / p.pair_stride > WAVE ||
+      p.pair_bound - p.pair_stride + p.pair_offset >= p.hd)
+    ST_DIE("decode attention: RoPE pairs must fit one per lane within the head");
+  const dim3 grid(p.splits, p.kv_heads);
+  const size_t shm = attention_decode_lds_bytes(p.hd);
   switch (p.hd) {
-#define DECODE_CASE(HD)                                                                 \
-  case HD:                                                                              \
-    hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(256), 0, s, p);               \
-    hipLaunchKernelGGL(attn_decode_combine_kernel<HD>, dim3(p.q_heads), dim3(HD), 0, s, p); \
+#define DECODE_CASE(HD)                                                              \
+  case HD:                                                                           \
+    hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(kDecThreads), shm, s, p); \
     break;
     DECODE_CASE(16)
     DECODE_CASE(32)

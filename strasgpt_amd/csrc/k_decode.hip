@@ -54,19 +54,6 @@ constexpr int kMaxG = 8;            // q heads per kv head
 constexpr int kMinChunk = 16;       // keys per attention item, at least
 constexpr size_t kMinLds = 81 * 1024;  // more than half of a CU's LDS
 
-__device__ __forceinline__ float cload(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int cload(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void cstore(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void cstore(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Parameters are read from a copy in LDS (made at kernel start) and made
 // wave-uniform at each use: no parameter stays live in scalar registers
 // across the step (the step's code is large; long-lived scalars spill), and

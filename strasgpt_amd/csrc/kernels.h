@@ -132,11 +132,14 @@ struct AttnParams {
   const float* rope;
   int pair_bound, pair_offset, pair_stride;
   float* partial;        // [q_heads][splits][hd + 2]
-  int chunk, splits;
+  int splits;            // key chunks per kv head, at most (attention_decode_chunks)
+  unsigned* counters;    // [kv_heads], zero between launches
 };
 void attention_prefill(const AttnParams& p, hipStream_t s);
 void attention_decode(const AttnParams& p, hipStream_t s);
-int attention_decode_splits(int ctx, int chunk);
+int attention_decode_chunks(int kv_heads);
+// Sets the decode kernels' LDS limits; called once per device before use.
+void attention_init();
 
 // ------------------------------------------------------------- argmax --
 // First index of the maximum (reference source/sampler.c:92-102): block

@@ -155,6 +155,7 @@ struct transformer_device {
   int seq_cap = 0;
   float* attn_part = nullptr;
   int attn_splits = 0;
+  unsigned* attn_cnt = nullptr;  // [kvh] decode attention arrivals
   float* am_v = nullptr;
   int* am_i = nullptr;
   int* h_tok = nullptr;
@@ -425,8 +426,8 @@ void layer_decode(Dev* D, int l) {
   a.pair_offset = D->po;
   a.pair_stride = D->pst;
   a.partial = D->attn_part;
-  a.chunk = 64;
   a.splits = D->attn_splits;
+  a.counters = D->attn_cnt;
   {
     const double keys = (double)D->host_pos + 1;
     Prof pr(D, K_ATT_DEC, 2.0 * D->kvh * keys * D->hd * 4, 4.0 * D->qh * keys * D->hd);
@@ -1112,8 +1113,11 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->seq_cap = D->ctx + 1;
   D->seq = dalloc<int>(D->seq_cap);
   D->seq_len = dalloc<int>(1);
-  D->attn_splits = sg::attention_decode_splits(D->ctx, 64);
+  D->attn_splits = sg::attention_decode_chunks(D->kvh);
   D->attn_part = dalloc<float>((size_t)D->qh * D->attn_splits * (hd + 2));
+  D->attn_cnt = dalloc<unsigned>(D->kvh);
+  HIP_CHECK(hipMemset(D->attn_cnt, 0, D->kvh * sizeof(unsigned)));
+  sg::attention_init();
   D->am_v = dalloc<float>(sg::argmax_blocks());
   D->am_i = dalloc<int>(sg::argmax_blocks());
   if (moe) {
@@ -1152,7 +1156,7 @@ extern "C" void sg_free(transformer_t* t) {
       if (D->w[k] && !(k == W_OUT && D->tied)) HIP_CHECK(hipFree(D->w[k]));
     }
     void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
-                    D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part,
+                    D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part, D->attn_cnt,
                     D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
                     D->moe_sel, D->moe_w, D->moe_act, D->xn_hi, D->xn_lo,
                     D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws,
