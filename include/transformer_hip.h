@@ -95,16 +95,18 @@ int transformer_decode_persistent_supported(const transformer_t* transformer);
  * reference counterpart). While enabled, the first worker block of every
  * step records wall-clock times around each grid barrier. transformer_decode_trace_read
  * returns the barrier count n (0 when the tracer was never enabled) and
- * writes up to max_values per-step averages in microseconds as 5 rows of n:
- *   row 0: work before the barrier (since leaving the previous one),
- *   row 1: wait inside the barrier,
- *   rows 2-4: for the GEMV phase the barrier starts, time from leaving the
- *          barrier to the end of input staging, of the weight loop and of
- *          the epilogue (0 for other phases).
- * Barriers are in launch order: for layer 0 those that start attention,
- * combine, O, gate/up and down; for each further layer the one that starts
- * its QKV phase, then the same five; then the logits barrier and the final
- * argmax barrier (n = 6 x layer_count + 1). */
+ * writes up to max_values per-step averages in microseconds as 8 rows of n:
+ *   row 0: work before barrier k (since leaving the previous one),
+ *   row 1: wait inside barrier k,
+ *   rows 2-4: for the phase that barrier k starts, time from leaving the
+ *          barrier to the end of input staging, of the weight loop (for
+ *          attention: of the key tiles) and of the epilogue (attention: of
+ *          the work item),
+ *   rows 5-7: for a GEMV phase started by barrier k, time from leaving the
+ *          barrier until the first stream wave starts its weight loop,
+ *          ends it, and has issued the next phase's first loads.
+ * Barrier k ends phase k; phases are in launch order: per layer QKV,
+ * attention, O, gate/up, down, then the logits (n = 5 x layer_count + 1). */
 void transformer_decode_trace(transformer_t* transformer, int enable);
 int transformer_decode_trace_read(transformer_t* transformer, double* us, int max_values);
 

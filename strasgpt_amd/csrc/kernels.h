@@ -205,25 +205,31 @@ struct DecodeParams {
   // byte offset trace_lds (decode_lds_bytes)
   unsigned long long* trace;
   size_t trace_lds;
-  int max_chunks;  // attention key chunks per kv head
-  int comb_outputs;  // attention outputs combined per block per pass
+  int layer_lds;        // LDS float offset of the layer table (decode_work_floats)
+  int max_chunks;       // attention key chunks per kv head (decode_max_chunks)
+  unsigned* att_cnt;    // [kvh] attention items done per kv head, zero between launches
   DecodeGemvPlan p_qkv, p_o, p_gu, p_down, p_logits;
 };
 
 // Host helpers: plan for an N x K GEMV over `blocks` blocks; LDS bytes the
 // kernel needs; whether the model shape is supported; the launch.
 DecodeGemvPlan decode_gemv_plan(int N, int K, int blocks);
+size_t decode_work_floats(const DecodeParams& p);
 size_t decode_lds_bytes(const DecodeParams& p);
 size_t decode_trace_lds_bytes(int L);
-bool decode_supported(int d, int H, int qh, int kvh, int hd, int qd, int V, int blocks,
+bool decode_supported(int L, int d, int H, int qh, int kvh, int hd, int qd, int V, int blocks,
                       size_t lds_limit);
 int decode_blocks();  // compute units of the current device
-__host__ __device__ inline int decode_barriers(int L) { return 6 * L + 1; }
-constexpr int kDecodeTraceRows = 5;
+int decode_max_chunks(int kvh, int blocks);
+// Phases per layer (QKV, attention, O, gate/up, down), each ended by a grid
+// barrier, plus the logits phase.
+constexpr int kDecodePhases = 5;
+__host__ __device__ inline int decode_barriers(int L) { return kDecodePhases * L + 1; }
+constexpr int kDecodeTraceRows = 8;
 // `p` is the host copy, `dp` the same parameters already in device memory
 // (stream-ordered before the launch).
 void decode_step(const DecodeParams& p, const DecodeParams* dp, int blocks, hipStream_t s);
-constexpr int kDecodeThreads = 512;
+constexpr int kDecodeThreads = 768;
 constexpr int kDecodePartMax = 2048;  // per-block slice sums held in LDS
 
 }  // namespace sg

@@ -749,7 +749,7 @@ void init_decode(Dev* D) {
                                   dev));
   const int blocks = sg::decode_blocks();
   if (blocks > sg::kSyncMaxBlocks ||
-      !sg::decode_supported(D->d, D->H, D->qh, D->kvh, D->hd, D->qd, D->V, blocks,
+      !sg::decode_supported(D->L, D->d, D->H, D->qh, D->kvh, D->hd, D->qd, D->V, blocks,
                             (size_t)lds_limit))
     return;
   sg::DecodeParams& p = D->dec;
@@ -799,13 +799,8 @@ void init_decode(Dev* D) {
   p.seq_len = D->seq_len;
   p.logits = nullptr;
   const int workers = blocks - 1;  // block 0 coordinates the grid barriers
-  p.max_chunks = std::max(1, std::min(32, workers / D->kvh));
-  {
-    const int need = (D->qd + workers - 1) / workers;
-    int opb = 1;
-    while (opb < need) opb *= 2;
-    p.comb_outputs = std::min(opb, std::min(D->hd, sg::kDecodeThreads / p.max_chunks));
-  }
+  p.max_chunks = sg::decode_max_chunks(D->kvh, blocks);
+  p.layer_lds = (int)sg::decode_work_floats(p);
   const size_t part = (size_t)D->qh * p.max_chunks * (D->hd + 2);
   const size_t nbuf = (size_t)D->d + D->qkv_rows + D->qd + D->H + part + blocks;
   D->dec_buf = dalloc<float>(nbuf);
@@ -817,11 +812,14 @@ void init_decode(Dev* D) {
   p.am_v = p.part + part;
   D->dec_am_i = dalloc<int>(blocks);
   p.am_i = D->dec_am_i;
-  D->dec_sync = dalloc<unsigned>(sg::kSyncStateWords + 2);
-  HIP_CHECK(hipMemset(D->dec_sync, 0, (sg::kSyncStateWords + 2) * sizeof(unsigned)));
+  // barrier state, error flag, epoch, attention counters
+  const size_t nsync = sg::kSyncStateWords + 2 + D->kvh;
+  D->dec_sync = dalloc<unsigned>(nsync);
+  HIP_CHECK(hipMemset(D->dec_sync, 0, nsync * sizeof(unsigned)));
   p.sync_state = D->dec_sync;
   p.sync_err = D->dec_sync + sg::kSyncStateWords;
   p.epoch = D->dec_sync + sg::kSyncStateWords + 1;
+  p.att_cnt = D->dec_sync + sg::kSyncStateWords + 2;
   p.p_qkv = sg::decode_gemv_plan(D->qkv_rows, D->d, workers);
   p.p_o = sg::decode_gemv_plan(D->d, D->qd, workers);
   p.p_gu = sg::decode_gemv_plan(D->H, D->d, workers);

@@ -210,11 +210,12 @@ class Transformer:
         self._lib.transformer_decode_trace(self._t, 1 if enable else 0)
 
     def decode_trace_read(self) -> np.ndarray:
-        """[5][n] per-step average microseconds per grid barrier of the
-        persistent step (rows: work, wait, staged, loop end, epilogue end;
-        see transformer_decode_trace_read); empty if never traced."""
+        """[8][n] per-step average microseconds per grid barrier of the
+        persistent step (rows: work, wait, staged, loop end, epilogue end,
+        stream-wave loop start, loop end, next-phase loads issued; see
+        transformer_decode_trace_read); empty if never traced."""
         n = self._lib.transformer_decode_trace_read(self._t, None, 0)
-        out = np.zeros((5, n), dtype=np.float64)
+        out = np.zeros((8, n), dtype=np.float64)
         if n:
             self._lib.transformer_decode_trace_read(
                 self._t, out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), out.size)
