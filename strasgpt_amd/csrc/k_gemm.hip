@@ -248,10 +248,14 @@ void launch(const GemmParams& p, int splits, hipStream_t s) {
 
 template <int EPI, int PREC>
 void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
-  // 128 x 128 tiles when that gives at least ~one block per CU, else 64 x 64.
+  // Measured on MI355X (prefill shapes, M = 512): with two blocks of tiles
+  // per CU or more, 128 x 128 tiles with a 2-stage ring (48 KiB of LDS:
+  // three blocks per CU) beat deeper rings; from about one block per CU,
+  // 64 x 128 tiles with 4 stages; below that 64 x 64.
   const int cols = EPI == GEMM_SWIGLU ? 64 : 128;
   const long big = (long)((p.N + cols - 1) / cols) * ((p.M + 127) / 128) * splits;
-  if (big >= 192) launch<128, 128, 4, EPI, PREC>(p, splits, s);
+  if (big >= 512) launch<128, 128, 2, EPI, PREC>(p, splits, s);
+  else if (big >= 192) launch<64, 128, 4, EPI, PREC>(p, splits, s);
   else launch<64, 64, 4, EPI, PREC>(p, splits, s);
 }
 
