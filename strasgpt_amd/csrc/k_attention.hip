@@ -3,9 +3,7 @@
 // source/transformer.c:1375-1422: score = (q . k) / sqrtf(hd), softmax
 // with max subtraction and expf, out = sum_s p[s] v[s].
 //
-// Prefill: one block per (64-query tile, q head); key tiles of 64 staged in
-// LDS; 4x4 register-blocked fp32 scores, online softmax (running max and
-// sum per query row), P kept in LDS for the P.V product.
+// Prefill: fp32 matrix-core flash attention (attn_prefill_mfma_kernel).
 //
 // Decode: split-K over the cached positions ("flash decoding") in one
 // launch: one block per (key chunk, kv head) for all query heads of the
@@ -24,7 +22,7 @@ namespace sg {
 
 namespace {
 
-constexpr int BQ = 64, BKV = 64;
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // Decode: threads per block, keys per LDS tile, query heads per kv head
 // and key chunks per kv head, at most.
@@ -43,141 +41,164 @@ __host__ __device__ inline void attention_decode_split(int total, int max_chunks
   nch = (total + len - 1) / len;
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
-  constexpr int LD = HD + 4;
-  constexpr int DU = HD / 16;  // output dims per thread
-  __shared__ __attribute__((aligned(16))) float qs[BQ * LD];
-  __shared__ __attribute__((aligned(16))) float ks[BKV * LD];
-  __shared__ __attribute__((aligned(16))) float vs[BKV * LD];
-  __shared__ float ps[BQ * (BKV + 4)];
+// Prefill attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32:
+// fp32 products accumulated in fp32, as the reference computes them; only
+// the summation order differs). Block = 64 queries of one head (4 waves x
+// 16 queries), key tiles of 64 brought to LDS by DMA, double-buffered.
+// Per tile and wave: S^T = K Q^T (keys as rows: the MFMA output then holds,
+// in lane (g, c) = (lane / 16, lane % 16), keys 4g + i of each 16-key
+// sub-tile for query c, which is exactly the B operand layout of the P.V
+// product's k-steps, so P never leaves registers), the online softmax per
+// query (a column: reductions across the four lane groups), then
+// O^T += V^T P^T. The head dimension of S^T is walked in an order where a
+// lane's four consecutive k-steps read one 16-byte chunk of a K row; K/V
+// rows are stored with their 16-byte chunks XOR-swizzled by the row index
+// so that the 16 rows read by one instruction hit distinct banks.
+constexpr int PQ = 64, PK = 64;
 
-  const int tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
-  const int head = blockIdx.y, q0 = blockIdx.x * BQ;
+template <int HD>
+__device__ __forceinline__ int pre_swz(int row) {
+  return row & ((HD / 4 < 16 ? HD / 4 : 16) - 1);
+}
+
+// Float offset of (row, d) in a swizzled [PK][HD] tile.
+template <int HD>
+__device__ __forceinline__ int pre_off(int row, int d) {
+  return row * HD + (((d >> 2) ^ pre_swz<HD>(row)) << 2) + (d & 3);
+}
+
+// Rows [kv0, kv0 + PK) of a kv head's K and V (clamped to key `last`: the
+// rows past it are masked) into swizzled LDS tiles by DMA, 1 KiB per wave
+// instruction; lane i of instruction n lands at tile float n*256 + 4i and
+// fetches the chunk that belongs there.
+template <int HD>
+__device__ __forceinline__ void pre_dma(const float* kb, const float* vb, int kv0, int last, float* kt,
+                                        float* vt) {
+  constexpr int CH = HD / 4, RPK = 256 / HD, NI = PK * HD / 256;
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  for (int n = wave; n < NI; n += 4) {
+    const int row = n * RPK + lane / CH, phys = lane % CH;
+    const int c = phys ^ pre_swz<HD>(row);
+    const size_t key = (size_t)min(kv0 + row, last);
+    __builtin_amdgcn_global_load_lds((const void*)(kb + key * HD + c * 4), (lds_ptr)(kt + n * 256), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(vb + key * HD + c * 4), (lds_ptr)(vt + n * 256), 16, 0, 0);
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnParams p) {
+  constexpr int DJ = HD / 16;  // 16-wide slices of the head dimension
+  extern __shared__ __attribute__((aligned(16))) float plds[];
+  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, g = lane / 16, c = lane % 16;
+  const int nqb = (p.T + PQ - 1) / PQ;
+  const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
+  const int head = blockIdx.y;
   const int G = p.q_heads / p.kv_heads, kvh = head / G;
   const int P = *p.pos, T = p.T;
   const int qd = p.q_heads * HD;
-  const float* kbase = p.kcache + (size_t)kvh * p.ctx * HD;
-  const float* vbase = p.vcache + (size_t)kvh * p.ctx * HD;
+  const int t = qb * PQ + wave * 16 + c;  // this lane's query (column)
+  const float* kb = p.kcache + (size_t)kvh * p.ctx * HD;
+  const float* vb = p.vcache + (size_t)kvh * p.ctx * HD;
+  const int kv_end = P + min(qb * PQ + PQ, T);  // keys visible to the block's last query
+  const int ntiles = (kv_end + PK - 1) / PK;
   const float scale = sqrtf((float)HD);
 
-  for (int i = tid; i < BQ * HD / 4; i += 256) {
-    const int r = i / (HD / 4), c = (i % (HD / 4)) * 4;
-    const int t = q0 + r;
-    float4 v = t < T ? *(const float4*)(p.q + (size_t)t * qd + head * HD + c)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-    *(float4*)&qs[r * LD + c] = v;
-  }
-
-  float m[4], l[4], o[4][DU];
+  pre_dma<HD>(kb, vb, 0, kv_end - 1, plds, plds + PK * HD);
+  // Q^T operand: lane (g, c) holds q[t][16j + 4g + e] for k-step 4j + e.
+  float4 qv[DJ];
+  {
+    const float* qr = p.q + (size_t)min(t, T - 1) * qd + head * HD + 4 * g;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    m[i] = -INFINITY;
-    l[i] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < DU; u++) o[i][u] = 0.0f;
+    for (int j = 0; j < DJ; j++) qv[j] = *(const float4*)(qr + 16 * j);
   }
+  f32x4 o[DJ];
+#pragma unroll
+  for (int j = 0; j < DJ; j++) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
 
-  const int kv_end = min(P + q0 + BQ, P + T);  // keys visible to this tile
-  for (int kv0 = 0; kv0 < kv_end; kv0 += BKV) {
-    __syncthreads();
-    for (int i = tid; i < BKV * HD / 4; i += 256) {
-      const int r = i / (HD / 4), c = (i % (HD / 4)) * 4;
-      const int s = kv0 + r;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (s < kv_end) {
-        kv = *(const float4*)(kbase + (size_t)s * HD + c);
-        vv = *(const float4*)(vbase + (size_t)s * HD + c);
-      }
-      *(float4*)&ks[r * LD + c] = kv;
-      *(float4*)&vs[r * LD + c] = vv;
+  for (int it = 0; it < ntiles; it++) {
+    float* kt = plds + (it & 1) * 2 * PK * HD;
+    float* vt = kt + PK * HD;
+    __builtin_amdgcn_s_waitcnt(0);  // this tile's DMA (and the q loads) landed
+    __syncthreads();                // for every wave; the other buffer is free
+    if (it + 1 < ntiles) {
+      float* nk = plds + ((it + 1) & 1) * 2 * PK * HD;
+      pre_dma<HD>(kb, vb, (it + 1) * PK, kv_end - 1, nk, nk + PK * HD);
     }
-    __syncthreads();
-
-    float sc[4][4];
+    const int kv0 = it * PK;
+    // S^T[key][query] for the tile's four 16-key sub-tiles.
+    f32x4 sc[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int s4 = 0; s4 < 4; s4++) sc[s4] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; j++) sc[i][j] = 0.0f;
-    for (int h = 0; h < HD; h += 4) {
-      float4 qv[4], kv[4];
+    for (int j = 0; j < DJ; j++) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) qv[i] = *(const float4*)&qs[(ty * 4 + i) * LD + h];
+      for (int s4 = 0; s4 < 4; s4++) {
+        const float4 kv = *(const float4*)(kt + pre_off<HD>(16 * s4 + c, 16 * j + 4 * g));
+        sc[s4] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qv[j].x, sc[s4], 0, 0, 0);
+        sc[s4] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qv[j].y, sc[s4], 0, 0, 0);
+        sc[s4] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qv[j].z, sc[s4], 0, 0, 0);
+        sc[s4] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qv[j].w, sc[s4], 0, 0, 0);
+      }
+    }
+    // Scale, causal mask, online softmax of column t.
+    float mx = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 4; j++) kv[j] = *(const float4*)&ks[(tx + 16 * j) * LD + h];
+    for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = kv0 + 16 * s4 + 4 * g + i;
+        const float v = key <= P + t && key < kv_end ? sc[s4][i] / scale : -INFINITY;
+        sc[s4][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+    const float mn = fmaxf(m, mx);
+    const float corr = mn == -INFINITY ? 1.0f : expf(m - mn);
+    float rs = 0.0f;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float e = mn == -INFINITY ? 0.0f : expf(sc[s4][i] - mn);
+        sc[s4][i] = e;
+        rs += e;
+      }
+    rs += __shfl_xor(rs, 16, WAVE);
+    rs += __shfl_xor(rs, 32, WAVE);
+    l = l * corr + rs;
+    m = mn;
+#pragma unroll
+    for (int j = 0; j < DJ; j++) o[j] *= corr;
+    // O^T[d][query] += V[key][d] P^T[key][query]: k-step (s4, i) covers keys
+    // 16 s4 + 4g' + i, g' the lane group, whose P^T values lane (g, c) holds
+    // as sc[s4][i].
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          float a = sc[i][j];
-          a = fmaf(qv[i].x, kv[j].x, a);
-          a = fmaf(qv[i].y, kv[j].y, a);
-          a = fmaf(qv[i].z, kv[j].z, a);
-          a = fmaf(qv[i].w, kv[j].w, a);
-          sc[i][j] = a;
+        for (int j = 0; j < DJ; j++) {
+          const float a = vt[pre_off<HD>(16 * s4 + 4 * g + i, 16 * j + c)];
+          o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, sc[s4][i], o[j], 0, 0, 0);
         }
-    }
-    float corr[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int t = q0 + ty * 4 + i;
-      float rmax = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int s = kv0 + tx + 16 * j;
-        sc[i][j] = (s <= P + t && s < kv_end) ? sc[i][j] / scale : -INFINITY;
-        rmax = fmaxf(rmax, sc[i][j]);
-      }
-      rmax = fmaxf(rmax, __shfl_xor(rmax, 8, WAVE));
-      rmax = fmaxf(rmax, __shfl_xor(rmax, 4, WAVE));
-      rmax = fmaxf(rmax, __shfl_xor(rmax, 2, WAVE));
-      rmax = fmaxf(rmax, __shfl_xor(rmax, 1, WAVE));
-      const float mnew = fmaxf(m[i], rmax);
-      corr[i] = mnew == -INFINITY ? 1.0f : expf(m[i] - mnew);
-      float rsum = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float pv = mnew == -INFINITY ? 0.0f : expf(sc[i][j] - mnew);
-        ps[(ty * 4 + i) * (BKV + 4) + tx + 16 * j] = pv;
-        rsum += pv;
-      }
-      rsum += __shfl_xor(rsum, 8, WAVE);
-      rsum += __shfl_xor(rsum, 4, WAVE);
-      rsum += __shfl_xor(rsum, 2, WAVE);
-      rsum += __shfl_xor(rsum, 1, WAVE);
-      l[i] = l[i] * corr[i] + rsum;
-      m[i] = mnew;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int u = 0; u < DU; u++) o[i][u] *= corr[i];
-    const int nk = min(BKV, kv_end - kv0);
-    for (int c = 0; c < nk; c++) {
-      float pv[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) pv[i] = ps[(ty * 4 + i) * (BKV + 4) + c];
-#pragma unroll
-      for (int u = 0; u < DU; u++) {
-        const float vv = vs[c * LD + tx + 16 * u];
-#pragma unroll
-        for (int i = 0; i < 4; i++) o[i][u] = fmaf(pv[i], vv, o[i][u]);
-      }
-    }
   }
-  // Output as the bf16 hi/lo planes of the O-projection GEMM's input.
+  // lane (g, c) holds O^T[16j + 4g + e][t]: out[t][head*HD + 16j + 4g + e]
+  if (t < T) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int t = q0 + ty * 4 + i;
-    if (t >= T) continue;
+    for (int j = 0; j < DJ; j++) {
+      const size_t idx = (size_t)t * qd + head * HD + 16 * j + 4 * g;
+      uint16_t hi[4], lo[4];
 #pragma unroll
-    for (int u = 0; u < DU; u++) {
-      const float v = o[i][u] / l[i];
-      const size_t idx = (size_t)t * qd + head * HD + tx + 16 * u;
-      const uint16_t h = f32_to_bf16_rne(v);
-      p.out_hi[idx] = h;
-      if (p.out_lo) p.out_lo[idx] = f32_to_bf16_rne(v - bf16_to_f32(h));
+      for (int e = 0; e < 4; e++) {
+        const float v = o[j][e] / l;
+        hi[e] = f32_to_bf16_rne(v);
+        lo[e] = f32_to_bf16_rne(v - bf16_to_f32(hi[e]));
+      }
+      *(uint2*)(p.out_hi + idx) = make_uint2(hi[0] | ((unsigned)hi[1] << 16), hi[2] | ((unsigned)hi[3] << 16));
+      if (p.out_lo)
+        *(uint2*)(p.out_lo + idx) = make_uint2(lo[0] | ((unsigned)lo[1] << 16), lo[2] | ((unsigned)lo[3] << 16));
     }
   }
 }
@@ -197,8 +218,6 @@ struct DecLds {
   static constexpr int wts = red + KG * kDecMaxG * HD;         // [kDecMaxG][kDecMaxChunks + 1]
   static constexpr int total = std::max(tiles + 4 * kDecTile * HD, wts + kDecMaxG * (kDecMaxChunks + 1));
 };
-
-typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // Keys [t0, t0 + n) of a kv head (rows of HD floats, contiguous) into the
 // LDS tiles kt / vt by the global-to-LDS DMA: 16 bytes per lane, each wave
@@ -518,6 +537,14 @@ int attention_decode_chunks(int kv_heads) {
 }
 
 void attention_init() {
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_mfma_kernel<16>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 16 * (int)sizeof(float)));
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_mfma_kernel<32>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 32 * (int)sizeof(float)));
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_mfma_kernel<64>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 64 * (int)sizeof(float)));
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_mfma_kernel<128>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 128 * (int)sizeof(float)));
   HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)(DecLds<16>::total * sizeof(float))));
   HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<32>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -541,12 +568,17 @@ size_t attention_decode_lds_bytes(int hd) {
 void attention_prefill(const AttnParams& p, hipStream_t s) {
   if (p.T <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
   if (!p.out_hi) ST_DIE("prefill attention writes bf16 planes");
-  dim3 grid((p.T + BQ - 1) / BQ, p.q_heads);
+  dim3 grid((p.T + PQ - 1) / PQ, p.q_heads);
   switch (p.hd) {
-    case 16: hipLaunchKernelGGL(attn_prefill_kernel<16>, grid, dim3(256), 0, s, p); break;
-    case 32: hipLaunchKernelGGL(attn_prefill_kernel<32>, grid, dim3(256), 0, s, p); break;
-    case 64: hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, s, p); break;
-    case 128: hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, s, p); break;
+#define PREFILL_CASE(HD)                                                                         \
+  case HD:                                                                                       \
+    hipLaunchKernelGGL(attn_prefill_mfma_kernel<HD>, grid, dim3(256), 4 * PK * HD * sizeof(float), s, p); \
+    break;
+    PREFILL_CASE(16)
+    PREFILL_CASE(32)
+    PREFILL_CASE(64)
+    PREFILL_CASE(128)
+#undef PREFILL_CASE
     default: ST_DIE("attention supports head_dim 16, 32, 64 or 128");
   }
   HIP_CHECK(hipGetLastError());
