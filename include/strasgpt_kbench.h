@@ -10,6 +10,9 @@
 #ifndef STRASGPT_KBENCH_H
 #define STRASGPT_KBENCH_H
 
+#include <stddef.h>
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -34,6 +37,12 @@ int strasgpt_kbench_gemv2(int n, int k, int dual, int flags, int variant, int it
 int strasgpt_kbench_gemm(int m, int n, int k, int precision, int variant, int iters,
                          double* avg_us, double* rel_err);
 int strasgpt_kbench_gemm_variants(void);
+
+/* The device MXFP4 decode used by the expert kernels, on `nblocks` host
+ * blocks of 32 values (16 code bytes, element 2i in the low nibble of byte
+ * i, and one E8M0 scale byte each): out[32 b + i] = value i of block b. */
+int strasgpt_kbench_mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks,
+                                 float* out);
 
 /* Copy of `bytes` (multiple of 16) between two device buffers, `iters`
  * launches of copy_probe_kernel (reads and writes exactly `bytes` each):

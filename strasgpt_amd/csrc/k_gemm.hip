@@ -83,8 +83,8 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 // consecutive lanes cover 64 banks once. Stages are filled by global_load_lds_dwordx4: one
 // wavefront instruction writes 1 KiB = 16 rows, lane i landing at row i/4,
 // physical chunk i%4, so lane i fetches the logical chunk that belongs there.
-template <int BM, int BN, int NS, int EPI, int PREC>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
+template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false>
+__global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams p) {
   constexpr bool SPLIT = PREC == GEMM_SPLIT2;
   constexpr bool DUAL = EPI == GEMM_SWIGLU;
   constexpr int KS = 32;                       // K per stage
@@ -163,6 +163,66 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   for (int t = 0; t < NS - 1; t++)
     if (t < nk) issue(t);
   const int fr = lane % 16;
+  if constexpr (PIPE) {
+    // Fragments of K step kt+1 are read from LDS while the MFMAs of step kt
+    // run (two register sets, alternating without copies). At step kt:
+    // wait for stage kt+1, barrier (every wave has read stage kt-1's
+    // fragments, so its buffer is free), issue stage kt+NS-1, read step
+    // kt+1's fragments, multiply step kt.
+    static_assert(NS >= 3, "fragment pipelining needs three stages");
+    struct Frags {
+      bf16x8 b[NT];
+      bf16x8 ahi[MT];
+      bf16x8 alo[SPLIT ? MT : 1];
+    };
+    auto read_frags = [&](int kt, Frags& F) {
+      const unsigned char* st = smem + (kt % NS) * STAGE;
+#pragma unroll
+      for (int j = 0; j < NT; j++) F.b[j] = frag(st + A_ROWS * 64, b_tile_row(j) + fr);
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        const int r = wm * WM + i * 16 + fr;
+        F.ahi[i] = frag(st, r);
+        if (SPLIT) F.alo[i] = frag(st + BM * 64, r);
+      }
+    };
+    auto mma = [&](const Frags& F) {
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(F.ahi[i], F.b[j], acc[i][j], 0, 0, 0);
+        if (SPLIT) {
+#pragma unroll
+          for (int j = 0; j < NT; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(F.alo[i], F.b[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    };
+    auto step = [&](int kt, const Frags& cur, Frags& nxt) {
+      if (kt + 1 < nk) {
+        // stages issued so far: 0 .. min(kt + NS - 2, nk - 1); keep those
+        // after kt + 1 in flight
+        const int ahead = min(kt + NS - 2, nk - 1) - (kt + 1);
+        wait_vmcnt(ahead * PER_WAVE);
+        __builtin_amdgcn_s_barrier();
+        if (kt + NS - 1 < nk) issue(kt + NS - 1);
+        read_frags(kt + 1, nxt);
+      }
+      mma(cur);
+    };
+    Frags f0, f1;
+    if (nk > 0) {
+      wait_vmcnt(min(NS - 2, nk - 1) * PER_WAVE);
+      __builtin_amdgcn_s_barrier();
+      read_frags(0, f0);
+    }
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(kt, f0, f1);
+      if (kt + 1 >= nk) break;
+      step(kt + 1, f1, f0);
+    }
+  } else
   for (int kt = 0; kt < nk; kt++) {
     const int ahead = min(NS - 2, nk - 1 - kt);  // stages still allowed in flight
     wait_vmcnt(ahead * PER_WAVE);
@@ -229,7 +289,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   }
 }
 
-template <int BM, int BN, int NS, int EPI, int PREC>
+template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false>
 void launch(const GemmParams& p, int splits, hipStream_t s) {
   const int cols = EPI == GEMM_SWIGLU ? BN / 2 : BN;
   const int tiles = ((p.N + cols - 1) / cols) * ((p.M + BM - 1) / BM);
@@ -238,11 +298,11 @@ void launch(const GemmParams& p, int splits, hipStream_t s) {
   static_assert(shm <= 160 * 1024, "GEMM stages exceed LDS");
   static bool attr = false;
   if (!attr) {
-    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC>,
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC, PIPE>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
     attr = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC>), dim3(tiles, 1, splits), dim3(kThreads),
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC, PIPE>), dim3(tiles, 1, splits), dim3(kThreads),
                      shm, s, p);
 }
 
@@ -303,10 +363,14 @@ void gemm(const GemmParams& p, int epi, int prec, int splits, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
-int gemm_variant_count() { return 9; }
+int gemm_variant_count() { return 14; }
 
 void gemm_variant(const GemmParams& p, int prec, int v, hipStream_t s) {
   check(p, GEMM_STORE, prec, 1);
+#define GP(BM, BN, NS)                                                                \
+  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, true>(p, 1, s); \
+  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, true>(p, 1, s);                      \
+  break;
 #define G(BM, BN, NS)                                                        \
   if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2>(p, 1, s); \
   else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16>(p, 1, s);                   \
@@ -321,9 +385,15 @@ void gemm_variant(const GemmParams& p, int prec, int v, hipStream_t s) {
     case 6: G(128, 256, 2)
     case 7: G(128, 256, 3)
     case 8: G(64, 256, 3)
+    case 9: GP(128, 128, 3)
+    case 10: GP(128, 128, 4)
+    case 11: GP(64, 128, 4)
+    case 12: GP(128, 256, 3)
+    case 13: GP(64, 128, 3)
     default: ST_DIE("unknown GEMM variant");
   }
 #undef G
+#undef GP
   HIP_CHECK(hipGetLastError());
 }
 

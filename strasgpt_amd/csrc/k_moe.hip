@@ -7,8 +7,16 @@
 //            out = sum_j w_j (D_e a_j), accumulated in top-k order as
 //            acc = fmaf(w_j, D_e a_j, acc), then x += acc.
 // MXFP4 rows are [K/32] blocks of 16 code bytes (element 2i in the low
-// nibble) and one E8M0 exponent each: one 128-bit load per lane covers a
-// whole 32-value block, decoded in registers (exact in fp32).
+// nibble of byte i) and one E8M0 exponent each.
+//
+// Decode mapping: half a wavefront (32 lanes) per weight row, one 32-value
+// block per lane per step (one 128-bit load plus its scale byte), every
+// load of the wave's rows issued before the first is used; the block is
+// decoded with v_cvt_scalef32_pk_f32_fp4 (E2M1 times the E8M0 scale, exact
+// in fp32) and multiplied with the activation row staged in LDS.
+//
+// Algorithmic bytes per launch: the MXFP4 weights of the selected experts,
+// K/2 + K/32 bytes per row.
 #include "device_common.h"
 #include "hip_check.h"
 #include "kernels.h"
@@ -19,112 +27,268 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / WAVE;
-constexpr int kRowsPerWave = 4;
+constexpr int kHalves = 2 * kWaves;  // half-waves per block
+constexpr int kSteps = 3;            // blocks of 32 values per lane per pass (96 per row)
+constexpr int kGuRows = 2;           // rows per half-wave (gate/up)
+constexpr int kDownRows = 2;         // rows per half-wave (down)
 
-// Dot of one MXFP4 row with an fp32 vector in LDS (K multiple of 32).
-__device__ __forceinline__ float mx_row_dot(const uint8_t* blocks, const uint8_t* scales,
-                                            const float* xs, int K, int lane) {
-  float acc = 0.0f;
-  const int nb = K / 32;
-  for (int b = lane; b < nb; b += WAVE) {
-    const uint4 q = load_nt_u4(blocks + (size_t)b * 16);
-    const float sc = e8m0_scale(scales[b]);
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-    const float* xb = xs + b * 32;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t byte = (w[i] >> (8 * j)) & 0xFFu;
-        const int e = (i * 4 + j) * 2;
-        acc = fmaf(e2m1_value(byte & 15u) * sc, xb[e], acc);
-        acc = fmaf(e2m1_value(byte >> 4) * sc, xb[e + 1], acc);
-      }
-    }
-  }
-  return wave_sum(acc);
+// Two values of byte `B` of `w` times `sc` (low nibble first).
+template <int B>
+__device__ __forceinline__ float2v fp4_pair(uint32_t w, float sc) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, B);
 }
 
-// Router + top-k + softmax, one block per token.
-__global__ __launch_bounds__(kThreads) void route_kernel(const float* xn, const uint16_t* router,
-                                                         int E, int d, int k, int* sel,
-                                                         float* sel_w) {
-  extern __shared__ float sm[];
+// acc + (block of 32 MXFP4 values, scale sc) . xb[0, 32), in element order.
+__device__ __forceinline__ float mx_block_dot(uint4 q, float sc, const float* xb, float acc) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float4 xa = *(const float4*)(xb + 8 * i);
+    const float4 xc = *(const float4*)(xb + 8 * i + 4);
+    const float2v v0 = fp4_pair<0>(w[i], sc), v1 = fp4_pair<1>(w[i], sc);
+    const float2v v2 = fp4_pair<2>(w[i], sc), v3 = fp4_pair<3>(w[i], sc);
+    acc = fmaf(v0.x, xa.x, acc);
+    acc = fmaf(v0.y, xa.y, acc);
+    acc = fmaf(v1.x, xa.z, acc);
+    acc = fmaf(v1.y, xa.w, acc);
+    acc = fmaf(v2.x, xc.x, acc);
+    acc = fmaf(v2.y, xc.y, acc);
+    acc = fmaf(v3.x, xc.z, acc);
+    acc = fmaf(v3.y, xc.w, acc);
+  }
+  return acc;
+}
+
+// Sum over the 32 lanes of a half-wave, the same in each of them.
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+// One pass of a half-wave over blocks [b0 + hl, b0 + hl + 32 * kSteps) of
+// row `row` (blocks past nb are not loaded): codes and scales into registers.
+struct RowLoad {
+  uint4 q[kSteps];
+  float sc[kSteps];
+};
+
+__device__ __forceinline__ void row_load(const uint8_t* blocks, const uint8_t* scales, size_t row,
+                                         int nb, int b0, int hl, RowLoad& r) {
+  const uint8_t* bq = blocks + row * (size_t)nb * 16;
+  const uint8_t* bs = scales + row * (size_t)nb;
+#pragma unroll
+  for (int i = 0; i < kSteps; i++) {
+    const int b = min(b0 + hl + 32 * i, nb - 1);  // past the row: a loaded block, never used
+    r.q[i] = load_nt_u4(bq + (size_t)b * 16);
+    r.sc[i] = e8m0_scale(bs[b]);
+  }
+}
+
+__device__ __forceinline__ float row_dot(const RowLoad& r, const float* xs, int nb, int b0, int hl,
+                                         float acc) {
+#pragma unroll
+  for (int i = 0; i < kSteps; i++) {
+    const int b = b0 + hl + 32 * i;
+    if (b < nb) acc = mx_block_dot(r.q[i], r.sc[i], xs + b * 32, acc);
+  }
+  return acc;
+}
+
+// Router + top-k + softmax, one block of kRouteThreads per token: each
+// wave takes experts w, w + 8, ..., kRouteE at a time with every 128-bit
+// weight load of those experts in flight before the first is used; wave 0
+// then selects.
+constexpr int kRouteThreads = 512;
+constexpr int kRouteWaves = kRouteThreads / WAVE;
+constexpr int kRouteE = 4;     // experts per wave per pass
+constexpr int kRouteLd = 6;    // 8-value chunks per lane per expert per pass
+
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, const uint16_t* router,
+                                                              int E, int d, int k, int* sel,
+                                                              float* sel_w) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
   float* xs = sm;        // [d]
   float* lg = sm + d;    // [E]
   const int t = blockIdx.x, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  for (int i = threadIdx.x; i < d; i += kThreads) xs[i] = xn[(size_t)t * d + i];
+  for (int i = threadIdx.x * 4; i < d; i += kRouteThreads * 4)
+    *(float4*)(xs + i) = *(const float4*)(xn + (size_t)t * d + i);
   __syncthreads();
-  for (int e = wave; e < E; e += kWaves) {
-    const uint16_t* wr = router + (size_t)e * d;
-    float acc = 0.0f;
-    for (int i = lane; i < d; i += WAVE) acc = fmaf(bf16_to_f32(wr[i]), xs[i], acc);
-    acc = wave_sum(acc);
-    if (lane == 0) lg[e] = acc;
+  const int chunks = d / 8;
+  for (int e0 = wave * kRouteE; e0 < E; e0 += kRouteWaves * kRouteE) {
+    float acc[kRouteE];
+#pragma unroll
+    for (int i = 0; i < kRouteE; i++) acc[i] = 0.0f;
+    for (int c0 = 0; c0 < chunks; c0 += kRouteLd * WAVE) {
+      uint4 w[kRouteE][kRouteLd];
+#pragma unroll
+      for (int i = 0; i < kRouteE; i++) {
+        const uint16_t* wr = router + (size_t)min(e0 + i, E - 1) * d;
+#pragma unroll
+        for (int u = 0; u < kRouteLd; u++) w[i][u] = load_nt_u4(wr + min(c0 + u * WAVE + lane, chunks - 1) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < kRouteE; i++)
+#pragma unroll
+        for (int u = 0; u < kRouteLd; u++) {
+          const int c = c0 + u * WAVE + lane;
+          if (c < chunks)
+            acc[i] = dot8(w[i][u], *(const float4*)(xs + c * 8), *(const float4*)(xs + c * 8 + 4), acc[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kRouteE; i++) {
+      const float v = wave_sum(acc[i]);
+      if (lane == 0 && e0 + i < E) lg[e0 + i] = v;
+    }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (wave == 0) {
+    // k rounds of a wave-wide selection with the semantics of a sequential
+    // scan over the experts not yet taken: start from the first, replace
+    // on strictly greater (ties keep the lower id; a NaN first candidate
+    // stays, later NaNs never win). Lane l holds experts l + 64 m.
+    constexpr int kMaxPer = 1024 / WAVE;
+    unsigned taken = 0;  // bit m: expert lane + 64 m taken
     int idx[64];
-    float val[64];
     for (int j = 0; j < k; j++) {
-      int best = -1;
-      for (int e = 0; e < E; e++) {
-        bool taken = false;
-        for (int q = 0; q < j; q++) taken |= idx[q] == e;
-        if (taken) continue;
-        if (best < 0 || lg[e] > lg[best]) best = e;
+      int first = 0x7fffffff, bi = 0x7fffffff;
+      float bv = -INFINITY;
+#pragma unroll
+      for (int m = 0; m < kMaxPer; m++) {
+        const int e = lane + WAVE * m;
+        if (e < E && !((taken >> m) & 1u)) {
+          first = min(first, e);
+          const float v = lg[e];
+          if (v > bv || (v == bv && e < bi)) {
+            bv = v;
+            bi = e;
+          }
+        }
       }
-      idx[j] = best;
-      val[j] = lg[best];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        first = min(first, __shfl_xor(first, off, WAVE));
+        const float ov = __shfl_xor(bv, off, WAVE);
+        const int oi = __shfl_xor(bi, off, WAVE);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      const float fv = lg[first];
+      const int pick = (fv != fv || bi == 0x7fffffff) ? first : bi;
+      idx[j] = pick;
+      if (pick % WAVE == lane) taken |= 1u << (pick / WAVE);
     }
-    float sum = 0.0f;
-    for (int j = 0; j < k; j++) {
-      val[j] = expf(val[j] - lg[idx[0]]);
-      sum += val[j];
-    }
-    for (int j = 0; j < k; j++) {
-      sel[t * k + j] = idx[j];
-      sel_w[t * k + j] = val[j] / sum;
+    if (lane == 0) {
+      float val[64];
+      float sum = 0.0f;
+      for (int j = 0; j < k; j++) {
+        val[j] = expf(lg[idx[j]] - lg[idx[0]]);
+        sum += val[j];
+      }
+      for (int j = 0; j < k; j++) {
+        sel[t * k + j] = idx[j];
+        sel_w[t * k + j] = val[j] / sum;
+      }
     }
   }
 }
 
-// act[s][h] = silu(gate_e[h] . x_s) * (up_e[h] . x_s), slot s = (token, j).
+// act[s][h] = silu(gate_e[h] . x_s) * (up_e[h] . x_s), slot s = (token, j):
+// block (row group, slot); each half-wave takes kGuRows rows of both
+// matrices, all their loads of a pass in flight at once.
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(MoeGemvParams p) {
-  extern __shared__ float xs[];
+  extern __shared__ __attribute__((aligned(16))) float xs[];
   const int slot = blockIdx.y, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const int half = wave * 2 + lane / 32, hl = lane % 32;
   const float* xr = p.x + (size_t)(slot / p.topk) * p.K;
-  for (int i = threadIdx.x; i < p.K; i += kThreads) xs[i] = xr[i];
+  for (int i = threadIdx.x * 4; i < p.K; i += kThreads * 4) *(float4*)(xs + i) = *(const float4*)(xr + i);
   __syncthreads();
   const int e = p.expert[slot];
-  const size_t rb = (size_t)p.K / 2, rs = (size_t)p.K / 32;
-  const int r0 = (blockIdx.x * kWaves + wave) * kRowsPerWave;
-  for (int r = r0; r < min(r0 + kRowsPerWave, p.N); r++) {
-    const size_t row = (size_t)e * p.N + r;
-    const float g = mx_row_dot(p.blocks + row * rb, p.scales + row * rs, xs, p.K, lane);
-    const float u = mx_row_dot(p.blocks2 + row * rb, p.scales2 + row * rs, xs, p.K, lane);
-    if (lane == 0) p.y[(size_t)slot * p.N + r] = silu_mul(g, u);
+  const int nb = p.K / 32;
+  const int r0 = (blockIdx.x * kHalves + half) * kGuRows;
+  float g[kGuRows], u[kGuRows];
+#pragma unroll
+  for (int r = 0; r < kGuRows; r++) g[r] = u[r] = 0.0f;
+  for (int b0 = 0; b0 < nb; b0 += 32 * kSteps) {
+    RowLoad lg[kGuRows], lu[kGuRows];
+#pragma unroll
+    for (int r = 0; r < kGuRows; r++) {
+      const size_t row = (size_t)e * p.N + min(r0 + r, p.N - 1);
+      row_load(p.blocks, p.scales, row, nb, b0, hl, lg[r]);
+      row_load(p.blocks2, p.scales2, row, nb, b0, hl, lu[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < kGuRows; r++) {
+      g[r] = row_dot(lg[r], xs, nb, b0, hl, g[r]);
+      u[r] = row_dot(lu[r], xs, nb, b0, hl, u[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kGuRows; r++) {
+    const float gs = half_sum(g[r]), us = half_sum(u[r]);
+    if (hl == 0 && r0 + r < p.N) p.y[(size_t)slot * p.N + r0 + r] = silu_mul(gs, us);
   }
 }
 
-// y[t][n] += sum_j fmaf order of w_j * (down_e_j[n] . act[t*k + j]).
+// y[t][n] += sum_j fmaf order of w_j * (down_e_j[n] . act[t*k + j]):
+// block (row group, token); each half-wave takes kDownRows rows in turn, for
+// every slot of the token, all of a row's loads of a pass in flight at once.
+template <int KMAX>
 __global__ __launch_bounds__(kThreads) void down_kernel(MoeGemvParams p) {
-  extern __shared__ float as[];  // [k][K]
+  extern __shared__ __attribute__((aligned(16))) float as[];  // [k][K]
   const int k = p.topk;
   const int t = blockIdx.y, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  for (int i = threadIdx.x; i < k * p.K; i += kThreads) as[i] = p.x[(size_t)t * k * p.K + i];
+  const int half = wave * 2 + lane / 32, hl = lane % 32;
+  for (int i = threadIdx.x * 4; i < k * p.K; i += kThreads * 4)
+    *(float4*)(as + i) = *(const float4*)(p.x + (size_t)t * k * p.K + i);
   __syncthreads();
-  const size_t rb = (size_t)p.K / 2, rs = (size_t)p.K / 32;
-  const int r0 = (blockIdx.x * kWaves + wave) * kRowsPerWave;
-  for (int r = r0; r < min(r0 + kRowsPerWave, p.N); r++) {
-    float acc = 0.0f;
-    for (int j = 0; j < k; j++) {
-      const int e = p.expert[t * k + j];
-      const size_t row = (size_t)e * p.N + r;
-      const float v = mx_row_dot(p.blocks + row * rb, p.scales + row * rs, as + j * p.K, p.K, lane);
-      acc = fmaf(p.weight[t * k + j], v, acc);
+  const int nb = p.K / 32;
+  for (int n = (blockIdx.x * kHalves + half) * kDownRows, n1 = n + kDownRows; n < n1; n++) {
+    float dot[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; j++) dot[j] = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 32 * kSteps) {
+      RowLoad ld[KMAX];
+#pragma unroll
+      for (int j = 0; j < KMAX; j++) {
+        const int e = p.expert[t * k + min(j, k - 1)];
+        row_load(p.blocks, p.scales, (size_t)e * p.N + min(n, p.N - 1), nb, b0, hl, ld[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < KMAX; j++)
+        if (j < k) dot[j] = row_dot(ld[j], as + j * p.K, nb, b0, hl, dot[j]);
     }
-    if (lane == 0) p.y[(size_t)t * p.N + r] += acc;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KMAX; j++)
+      if (j < k) acc = fmaf(p.weight[t * k + j], half_sum(dot[j]), acc);
+    if (hl == 0 && n < p.N) p.y[(size_t)t * p.N + n] += acc;
+  }
+}
+
+// The decode of mx_block_dot, written out: out[32 b + i] = value i of block b.
+__global__ void mxfp4_decode_kernel(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  const uint4 q = *(const uint4*)(codes + (size_t)b * 16);
+  const float sc = e8m0_scale(scales[b]);
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  float* o = out + (size_t)b * 32;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float2v v0 = fp4_pair<0>(w[i], sc), v1 = fp4_pair<1>(w[i], sc);
+    const float2v v2 = fp4_pair<2>(w[i], sc), v3 = fp4_pair<3>(w[i], sc);
+    o[8 * i + 0] = v0.x;
+    o[8 * i + 1] = v0.y;
+    o[8 * i + 2] = v1.x;
+    o[8 * i + 3] = v1.y;
+    o[8 * i + 4] = v2.x;
+    o[8 * i + 5] = v2.y;
+    o[8 * i + 6] = v3.x;
+    o[8 * i + 7] = v3.y;
   }
 }
 
@@ -141,9 +305,10 @@ void set_lds(F kernel, size_t bytes) {
 void moe_route(const float* xn, int T, const uint16_t* router, int E, int d, int k, int* sel,
                float* sel_w, hipStream_t s) {
   if (k > 64 || k > E || E > 1024) ST_DIE("MoE top-k must satisfy k <= 64, k <= E <= 1024");
+  if (d % 8 || (uintptr_t)router % 16 || (uintptr_t)xn % 16) ST_DIE("MoE router rows must be 16-byte aligned");
   const size_t shm = (size_t)(d + E) * sizeof(float);
   set_lds(route_kernel, shm);
-  hipLaunchKernelGGL(route_kernel, dim3(T), dim3(kThreads), shm, s, xn, router, E, d, k, sel, sel_w);
+  hipLaunchKernelGGL(route_kernel, dim3(T), dim3(kRouteThreads), shm, s, xn, router, E, d, k, sel, sel_w);
   HIP_CHECK(hipGetLastError());
 }
 
@@ -152,20 +317,32 @@ void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s) {
   if (p.topk <= 0 || p.tokens <= 0) ST_DIE("MoE GEMV needs tokens and topk");
   const size_t shm = (size_t)p.K * sizeof(float);
   set_lds(swiglu_kernel, shm);
-  const int rows_per_block = kWaves * kRowsPerWave;
+  const int rows_per_block = kHalves * kGuRows;
   dim3 grid((p.N + rows_per_block - 1) / rows_per_block, p.tokens * p.topk);
   hipLaunchKernelGGL(swiglu_kernel, grid, dim3(kThreads), shm, s, p);
+  HIP_CHECK(hipGetLastError());
+}
+
+void mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out, hipStream_t s) {
+  if (nblocks <= 0 || (uintptr_t)codes % 16) ST_DIE("MXFP4 decode needs aligned blocks");
+  hipLaunchKernelGGL(mxfp4_decode_kernel, dim3((nblocks + 255) / 256), dim3(256), 0, s, codes, scales,
+                     nblocks, out);
   HIP_CHECK(hipGetLastError());
 }
 
 void moe_gemv_down(const MoeGemvParams& p, hipStream_t s) {
   if (p.K % 32 || (uintptr_t)p.blocks % 16) ST_DIE("MXFP4 rows must be 32-value aligned");
   if (p.topk <= 0 || p.tokens <= 0) ST_DIE("MoE GEMV needs tokens and topk");
+  if (p.topk > 8) ST_DIE("MoE down projection supports top-k up to 8");
   const size_t shm = (size_t)p.topk * p.K * sizeof(float);
-  set_lds(down_kernel, shm);
-  const int rows_per_block = kWaves * kRowsPerWave;
-  dim3 grid((p.N + rows_per_block - 1) / rows_per_block, p.tokens);
-  hipLaunchKernelGGL(down_kernel, grid, dim3(kThreads), shm, s, p);
+  dim3 grid((p.N + kHalves * kDownRows - 1) / (kHalves * kDownRows), p.tokens);
+  if (p.topk <= 4) {
+    set_lds(down_kernel<4>, shm);
+    hipLaunchKernelGGL(down_kernel<4>, grid, dim3(kThreads), shm, s, p);
+  } else {
+    set_lds(down_kernel<8>, shm);
+    hipLaunchKernelGGL(down_kernel<8>, grid, dim3(kThreads), shm, s, p);
+  }
   HIP_CHECK(hipGetLastError());
 }
 

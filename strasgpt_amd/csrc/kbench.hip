@@ -242,6 +242,24 @@ extern "C" int strasgpt_kbench_copy(size_t bytes, int iters, double* avg_us) {
   return 0;
 }
 
+extern "C" int strasgpt_kbench_mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks,
+                                            float* out) {
+  if (nblocks <= 0) return -1;
+  uint8_t *dc, *ds;
+  float* dout;
+  HIP_CHECK(hipMalloc(&dc, (size_t)nblocks * 16));
+  HIP_CHECK(hipMalloc(&ds, (size_t)nblocks));
+  HIP_CHECK(hipMalloc(&dout, (size_t)nblocks * 32 * sizeof(float)));
+  HIP_CHECK(hipMemcpy(dc, codes, (size_t)nblocks * 16, hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(ds, scales, (size_t)nblocks, hipMemcpyHostToDevice));
+  sg::mxfp4_decode(dc, ds, nblocks, dout, 0);
+  HIP_CHECK(hipMemcpy(out, dout, (size_t)nblocks * 32 * sizeof(float), hipMemcpyDeviceToHost));
+  HIP_CHECK(hipFree(dc));
+  HIP_CHECK(hipFree(ds));
+  HIP_CHECK(hipFree(dout));
+  return 0;
+}
+
 extern "C" int strasgpt_kbench_gemv_variants(void) { return sg::gemv_variant_count(); }
 extern "C" int strasgpt_kbench_gemm_variants(void) { return sg::gemm_variant_count(); }
 

@@ -53,6 +53,9 @@ struct MoeGemvParams {
 };
 void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s);
 void moe_gemv_down(const MoeGemvParams& p, hipStream_t s);
+// The device MXFP4 decode of the expert kernels on `nblocks` blocks of 32
+// values (16 code bytes + 1 E8M0 scale each): out[32 b + i] (test hook).
+void mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out, hipStream_t s);
 
 // ---------------------------------------------------------------- GEMM --
 // C[M][N] = A[M][K] x W[N][K]^T (bf16 weights) on MFMA. A is given as two

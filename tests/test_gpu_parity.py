@@ -200,6 +200,32 @@ def test_grid_barrier_visibility():
         assert rc == 0 and bad.value == 0 and to.value == 0
 
 
+def test_mxfp4_device_decode_exact():
+    """The expert kernels' device MXFP4 decode (hardware E2M1 conversion
+    scaled by the E8M0 exponent) equals the oracle's dequantisation bit for
+    bit on every (code, scale) pair: 16 codes in both nibble positions x
+    256 scales (scale 255 decodes to NaN in both)."""
+    import ctypes
+    from oracle import oracle as orc
+    rt = runtime()
+    L = rt.lib()
+    ol = orc.load_lib()
+    nblocks = 256
+    codes = np.empty((nblocks, 16), np.uint8)
+    for i in range(16):
+        codes[:, i] = i | ((15 - i) << 4)
+    scales = np.arange(256, dtype=np.uint8)
+    got = np.zeros(nblocks * 32, np.float32)
+    fn = L.strasgpt_kbench_mxfp4_decode
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+    assert fn(codes.ctypes.data, scales.ctypes.data, nblocks, orc.fptr(got)) == 0
+    want = np.zeros(nblocks * 32, np.float32)
+    ol.oracle_mxfp4_dequant(codes.ctypes.data, scales.ctypes.data, nblocks * 32, orc.fptr(want))
+    nan_w, nan_g = np.isnan(want), np.isnan(got)
+    np.testing.assert_array_equal(nan_g, nan_w)
+    np.testing.assert_array_equal(got[~nan_w].view(np.uint32), want[~nan_w].view(np.uint32))
+
+
 def test_logits_window_and_chunking(model_dir):
     """logits_count > 1 returns the last rows; a prompt split across calls
     matches one call (chunk invariance)."""
