@@ -292,6 +292,197 @@ __global__ void mxfp4_decode_kernel(const uint8_t* codes, const uint8_t* scales,
   }
 }
 
+// ------------------------------------------------- prefill: grouped GEMM --
+//
+// Slots s = (token, j) are grouped by expert (moe_group: counting sort,
+// stable in slot order), then each expert's slots go through an MFMA GEMM
+// whose B operand is the expert's MXFP4 matrix, decoded into LDS as bf16
+// (exact: an E2M1 value times a power of two has at most two significant
+// bits). The A rows (fp32 activations) are split into bf16 hi + lo planes
+// on the way into LDS, as the dense prefill GEMM does, so both products are
+// exact in the fp32 accumulator. Tile: 32 slots x 64 weight rows (x2 for the
+// gate/up pair), K steps of 32 (one MXFP4 block per row), 4 waves each
+// owning 16 weight rows; LDS double-buffered, the next step's global loads
+// in registers while the current step multiplies.
+
+constexpr int GBM = 32, GBN = 64, GBK = 32, GLD = 40;  // LDS row stride (bf16)
+
+// order[offs[e] .. offs[e+1]) = the slots routed to expert e, increasing.
+__global__ __launch_bounds__(1024) void group_kernel(const int* sel, int n, int E, int* offs, int* order) {
+  extern __shared__ int cnt[];  // [E + 1]
+  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, nw = blockDim.x / WAVE;
+  for (int e = wave; e < E; e += nw) {
+    int c = 0;
+    for (int b = 0; b < n; b += WAVE) {
+      const bool hit = b + lane < n && sel[b + lane] == e;
+      c += __popcll(__ballot(hit));
+    }
+    if (lane == 0) cnt[e] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int e = 0; e < E; e++) {
+      const int c = cnt[e];
+      cnt[e] = run;
+      offs[e] = run;
+      run += c;
+    }
+    offs[E] = run;
+  }
+  __syncthreads();
+  for (int e = wave; e < E; e += nw) {
+    int pos = cnt[e];
+    for (int b = 0; b < n; b += WAVE) {
+      const bool hit = b + lane < n && sel[b + lane] == e;
+      const unsigned long long m = __ballot(hit);
+      if (hit) order[pos + __popcll(m & ((1ull << lane) - 1))] = b + lane;
+      pos += __popcll(m);
+    }
+  }
+}
+
+template <bool DUAL>
+__global__ __launch_bounds__(256) void group_gemm_kernel(MoeGemmParams p) {
+  constexpr int NM = DUAL ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t ahi[2][GBM * GLD], alo[2][GBM * GLD];
+  __shared__ __attribute__((aligned(16))) uint16_t bw[2][NM][GBN * GLD];
+  __shared__ int tile_info[2];
+  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+  // Which expert and which 32-slot tile of it this block computes.
+  if (wave == 0) {
+    int e_found = -1, m0 = 0, base = 0;
+    for (int e0 = 0; e0 < p.E && e_found < 0; e0 += WAVE) {
+      const int e = e0 + lane;
+      const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
+      int tiles = (c + GBM - 1) / GBM, incl = tiles;
+#pragma unroll
+      for (int off = 1; off < WAVE; off <<= 1) {
+        const int v = __shfl_up(incl, off, WAVE);
+        if (lane >= off) incl += v;
+      }
+      const int excl = base + incl - tiles;
+      const bool mine = (int)blockIdx.x >= excl && (int)blockIdx.x < excl + tiles;
+      const unsigned long long m = __ballot(mine);
+      if (m) {
+        const int src = __ffsll((long long)m) - 1;
+        e_found = __shfl(e0 + lane, src, WAVE);
+        m0 = ((int)blockIdx.x - __shfl(excl, src, WAVE)) * GBM;
+      }
+      base += __shfl(incl, WAVE - 1, WAVE);
+    }
+    if (lane == 0) {
+      tile_info[0] = e_found;
+      tile_info[1] = m0;
+    }
+  }
+  __syncthreads();
+  const int e = tile_info[0], m0 = tile_info[1];
+  if (e < 0) return;  // past the last tile (the grid is an upper bound)
+  const int cnt = p.offs[e + 1] - p.offs[e];
+  const int n0 = blockIdx.y * GBN;
+  const int K = p.K, nb = K / 32;
+
+  // loader roles: A: row ar, 4 values at ac; B: matrix bm, row br, half bh
+  const int ar = tid / 8, ac = (tid % 8) * 4;
+  const bool a_ok = m0 + ar < cnt;
+  const int slot = a_ok ? p.order[p.offs[e] + m0 + ar] : 0;
+  const float* arow = p.a + (size_t)(p.a_per_token ? slot / p.topk : slot) * K;
+  const int bm = tid / 128, br = (tid % 128) / 2, bh = tid % 2;
+  const bool b_ok = bm < NM;
+  const size_t brow = (size_t)e * p.N + min(n0 + br, p.N - 1);
+  const uint8_t* bq = (bm == 0 ? p.blocks : p.blocks2) + brow * (size_t)nb * 16 + bh * 8;
+  const uint8_t* bsc = (bm == 0 ? p.scales : p.scales2) + brow * (size_t)nb;
+
+  float4 ra;
+  uint2 rq;
+  unsigned rs;
+  auto fetch = [&](int kb) {
+    ra = a_ok ? *(const float4*)(arow + kb * GBK + ac) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (b_ok) {
+      rq = *(const uint2*)(bq + (size_t)kb * 16);
+      rs = bsc[kb];
+    }
+  };
+  auto stash = [&](int buf) {
+    const float av[4] = {ra.x, ra.y, ra.z, ra.w};
+    uint16_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      h[i] = f32_to_bf16_rne(av[i]);
+      l[i] = f32_to_bf16_rne(av[i] - bf16_to_f32(h[i]));
+    }
+    *(uint2*)(ahi[buf] + ar * GLD + ac) = make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+    *(uint2*)(alo[buf] + ar * GLD + ac) = make_uint2(l[0] | ((unsigned)l[1] << 16), l[2] | ((unsigned)l[3] << 16));
+    if (b_ok) {
+      const float sc = e8m0_scale(rs);
+      const uint32_t w[2] = {rq.x, rq.y};
+      unsigned out[8];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const float2v v0 = fp4_pair<0>(w[i], sc), v1 = fp4_pair<1>(w[i], sc);
+        const float2v v2 = fp4_pair<2>(w[i], sc), v3 = fp4_pair<3>(w[i], sc);
+        out[4 * i + 0] = (__float_as_uint(v0.x) >> 16) | (__float_as_uint(v0.y) & 0xFFFF0000u);
+        out[4 * i + 1] = (__float_as_uint(v1.x) >> 16) | (__float_as_uint(v1.y) & 0xFFFF0000u);
+        out[4 * i + 2] = (__float_as_uint(v2.x) >> 16) | (__float_as_uint(v2.y) & 0xFFFF0000u);
+        out[4 * i + 3] = (__float_as_uint(v3.x) >> 16) | (__float_as_uint(v3.y) & 0xFFFF0000u);
+      }
+      uint4* dst = (uint4*)(bw[buf][bm] + br * GLD + bh * 16);
+      dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+      dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+    }
+  };
+
+  f32x4 acc[NM][2];
+#pragma unroll
+  for (int m = 0; m < NM; m++) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int fr = lane % 16, fk = (lane / 16) * 8;
+  fetch(0);
+  for (int kb = 0; kb < nb; kb++) {
+    const int buf = kb & 1;
+    stash(buf);
+    __syncthreads();
+    if (kb + 1 < nb) fetch(kb + 1);
+    bf16x8 a_h[2], a_l[2], b[NM];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++) {
+      a_h[mi] = *(const bf16x8*)(ahi[buf] + (mi * 16 + fr) * GLD + fk);
+      a_l[mi] = *(const bf16x8*)(alo[buf] + (mi * 16 + fr) * GLD + fk);
+    }
+#pragma unroll
+    for (int m = 0; m < NM; m++) b[m] = *(const bf16x8*)(bw[buf][m] + (wave * 16 + fr) * GLD + fk);
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++) {
+        acc[m][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_h[mi], b[m], acc[m][mi], 0, 0, 0);
+        acc[m][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_l[mi], b[m], acc[m][mi], 0, 0, 0);
+      }
+  }
+  // lane holds C[4 (lane / 16) + i][lane % 16] of each 16 x 16 tile
+  const int n = n0 + wave * 16 + lane % 16;
+  if (n >= p.N) return;
+#pragma unroll
+  for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = mi * 16 + (lane / 16) * 4 + i;
+      if (m0 + r >= cnt) continue;
+      const int s2 = p.order[p.offs[e] + m0 + r];
+      p.y[(size_t)s2 * p.N + n] = DUAL ? silu_mul(acc[0][mi][i], acc[NM - 1][mi][i]) : acc[0][mi][i];
+    }
+}
+
+// x[t][n] += sum over j in top-k order of fmaf(w_j, out[t k + j][n], .).
+__global__ void combine_kernel(const float* out, const float* w, int T, int k, int N, float* x) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)T * N) return;
+  const size_t t = i / N, n = i % N;
+  float acc = 0.0f;
+  for (int j = 0; j < k; j++) acc = fmaf(w[t * k + j], out[(t * k + j) * N + n], acc);
+  x[i] += acc;
+}
+
 template <typename F>
 void set_lds(F kernel, size_t bytes) {
   if (bytes > 160 * 1024) ST_DIE("MoE kernel rows do not fit in LDS");
@@ -343,6 +534,33 @@ void moe_gemv_down(const MoeGemvParams& p, hipStream_t s) {
     set_lds(down_kernel<8>, shm);
     hipLaunchKernelGGL(down_kernel<8>, grid, dim3(kThreads), shm, s, p);
   }
+  HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace sg
+
+namespace sg {
+
+void moe_group(const int* sel, int n, int E, int* offs, int* order, hipStream_t s) {
+  if (n <= 0 || E <= 0 || E > 1024) ST_DIE("MoE grouping needs slots and 1 <= E <= 1024");
+  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), (E + 1) * sizeof(int), s, sel, n, E, offs, order);
+  HIP_CHECK(hipGetLastError());
+}
+
+void moe_group_gemm(const MoeGemmParams& p, hipStream_t s) {
+  if (p.K % 32 || p.N <= 0 || p.slots <= 0) ST_DIE("MoE grouped GEMM shape");
+  if (((uintptr_t)p.a % 16) || p.K % 4) ST_DIE("MoE grouped GEMM rows must be 16-byte aligned");
+  const dim3 grid((p.slots + GBM - 1) / GBM + p.E, (p.N + GBN - 1) / GBN);
+  if (p.blocks2)
+    hipLaunchKernelGGL(group_gemm_kernel<true>, grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(group_gemm_kernel<false>, grid, dim3(256), 0, s, p);
+  HIP_CHECK(hipGetLastError());
+}
+
+void moe_combine(const float* out, const float* w, int T, int k, int N, float* x, hipStream_t s) {
+  const size_t n = (size_t)T * N;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, w, T, k, N, x);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -53,6 +53,22 @@ struct MoeGemvParams {
 };
 void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s);
 void moe_gemv_down(const MoeGemvParams& p, hipStream_t s);
+// Prefill MoE: slots grouped by expert, then grouped MXFP4 GEMMs.
+// order[offs[e] .. offs[e+1]) lists the slots routed to expert e in
+// increasing order (offs has E + 1 entries).
+void moe_group(const int* sel, int n, int E, int* offs, int* order, hipStream_t s);
+struct MoeGemmParams {
+  const uint8_t *blocks, *scales;    // [E][N][K/32] x 16 bytes, [E][N][K/32]
+  const uint8_t *blocks2, *scales2;  // second matrix of a SwiGLU pair, or null
+  const float* a;                    // rows: a[token] (a_per_token) or a[slot], K floats
+  int a_per_token;
+  const int *offs, *order;           // moe_group output
+  int slots, topk, E, N, K;
+  float* y;                          // [slot][N]: silu(g) * u, or the product
+};
+void moe_group_gemm(const MoeGemmParams& p, hipStream_t s);
+// x[t][n] += sum_j in top-k order fmaf(w[t k + j], out[t k + j][n], .)
+void moe_combine(const float* out, const float* w, int T, int k, int N, float* x, hipStream_t s);
 // The device MXFP4 decode of the expert kernels on `nblocks` blocks of 32
 // values (16 code bytes + 1 E8M0 scale each): out[32 b + i] (test hook).
 void mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out, hipStream_t s);

@@ -171,6 +171,9 @@ struct transformer_device {
   int* moe_sel = nullptr;
   float* moe_w = nullptr;
   float* moe_act = nullptr;
+  int* moe_offs = nullptr;   // [E + 1] grouped prefill: slot ranges per expert
+  int* moe_order = nullptr;  // [T * topk] slots sorted by expert
+  float* moe_out = nullptr;  // [T * topk][d] per-slot down projections
   Summary summary[W_COUNT];
   // measurement hooks
   bool prof = false;
@@ -332,6 +335,10 @@ enum {
 
 double mxfp4_bytes(double values) { return values * (0.5 + 1.0 / 32.0); }
 
+// From this many tokens the MoE FFN runs as grouped GEMMs (below: GEMVs
+// per token and slot).
+constexpr int kMoeGroupedMinTokens = 8;
+
 // MoE FFN of T rows: RMSNorm, router top-k, MXFP4 SwiGLU experts, routed
 // down-projection accumulated into the residual stream.
 void ffn_moe(Dev* D, int l, int T) {
@@ -344,6 +351,51 @@ void ffn_moe(Dev* D, int l, int T) {
   {
     Prof pr(D, K_ROUTE, (double)D->E * d * 2, 2.0 * T * D->E * d);
     sg::moe_route(D->xn, T, W16(D, W_ROUTER, l), D->E, D->d, D->topk, D->moe_sel, D->moe_w, s);
+  }
+  if (T >= kMoeGroupedMinTokens) {
+    // prefill: slots grouped by expert, each expert's weights read once per
+    // 32-slot tile (MFMA GEMMs), then the routed sum in top-k order
+    const int n = T * D->topk;
+    const double used = std::min((double)n, (double)D->E);
+    sg::moe_group(D->moe_sel, n, D->E, D->moe_offs, D->moe_order, s);
+    sg::MoeGemmParams g{};
+    g.blocks = W8(D, W_GB, l);
+    g.scales = W8(D, W_GS, l);
+    g.blocks2 = W8(D, W_UB, l);
+    g.scales2 = W8(D, W_US, l);
+    g.a = D->xn;
+    g.a_per_token = 1;
+    g.offs = D->moe_offs;
+    g.order = D->moe_order;
+    g.slots = n;
+    g.topk = D->topk;
+    g.E = D->E;
+    g.N = D->H;
+    g.K = D->d;
+    g.y = D->moe_act;
+    {
+      Prof pr(D, K_MOE_GU, used * mxfp4_bytes(2 * H * d), 4.0 * n * H * d);
+      sg::moe_group_gemm(g, s);
+    }
+    sg::MoeGemmParams dn{};
+    dn.blocks = W8(D, W_DB, l);
+    dn.scales = W8(D, W_DS, l);
+    dn.a = D->moe_act;
+    dn.a_per_token = 0;
+    dn.offs = D->moe_offs;
+    dn.order = D->moe_order;
+    dn.slots = n;
+    dn.topk = D->topk;
+    dn.E = D->E;
+    dn.N = D->d;
+    dn.K = D->H;
+    dn.y = D->moe_out;
+    {
+      Prof pr(D, K_MOE_DOWN, used * mxfp4_bytes(H * d), 2.0 * n * H * d);
+      sg::moe_group_gemm(dn, s);
+      sg::moe_combine(D->moe_out, D->moe_w, T, D->topk, D->d, D->x, s);
+    }
+    return;
   }
   sg::MoeGemvParams g{};
   g.blocks = W8(D, W_GB, l);
@@ -1122,6 +1174,9 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
     D->moe_sel = dalloc<int>(T * D->topk);
     D->moe_w = dalloc<float>(T * D->topk);
     D->moe_act = dalloc<float>(T * D->topk * H);
+    D->moe_offs = dalloc<int>(D->E + 1);
+    D->moe_order = dalloc<int>(T * D->topk);
+    D->moe_out = dalloc<float>(T * D->topk * d);
   }
   HIP_CHECK(hipHostMalloc((void**)&D->h_tok, T * sizeof(int), hipHostMallocDefault));
   HIP_CHECK(hipHostMalloc((void**)&D->h_pos, sizeof(int), hipHostMallocDefault));
@@ -1156,7 +1211,8 @@ extern "C" void sg_free(transformer_t* t) {
     void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
                     D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part, D->attn_cnt,
                     D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
-                    D->moe_sel, D->moe_w, D->moe_act, D->xn_hi, D->xn_lo,
+                    D->moe_sel, D->moe_w, D->moe_act, D->moe_offs, D->moe_order, D->moe_out,
+                    D->xn_hi, D->xn_lo,
                     D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws,
                     D->dec_layers, D->dec_buf, D->dec_am_i, D->dec_sync, D->dec_trace,
                     D->dec_dev};

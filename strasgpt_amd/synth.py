@@ -97,6 +97,11 @@ TINY: Dict[str, ModelShape] = {
     "tiny-moe": ModelShape("tiny-moe", 64, 64, 2, 4, 2, 16, 256, 150000.0, 1e-5, 8, 8,
                            untied=True, experts=8, experts_per_tok=2,
                            model_type="stras_moe", std=0.25),
+    # Enough prompt tokens for several 32-slot tiles per expert in the
+    # grouped prefill GEMMs.
+    "tiny-moe-long": ModelShape("tiny-moe-long", 64, 96, 2, 4, 2, 16, 256, 150000.0, 1e-5,
+                                200, 10, untied=True, experts=8, experts_per_tok=2,
+                                model_type="stras_moe", std=0.25),
 }
 
 

@@ -243,12 +243,15 @@ def test_logits_window_and_chunking(model_dir):
     np.testing.assert_allclose(gl2[0], ol[-1], rtol=RTOL, atol=ATOL)
 
 
-def test_moe_tiny_against_oracle(model_dir):
+@pytest.mark.parametrize("name", ["tiny-moe", "tiny-moe-long"])
+def test_moe_tiny_against_oracle(name, model_dir):
     """MXFP4 MoE decoder: tokens identical to the oracle (the build's own
-    restatement; no reference counterpart exists)."""
+    restatement; no reference counterpart exists). The long prompt runs the
+    grouped prefill GEMMs with several 32-slot tiles per expert."""
     rt = runtime()
-    d = model_dir("tiny-moe")
-    prompt = synth.prompt_tokens(256, 8, PROMPT_SEED)
+    d = model_dir(name)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(256, shp.prompt_len, PROMPT_SEED)
     om = oracle_model(d, 4)
     ol = om.predict(prompt)
     om.reset()
