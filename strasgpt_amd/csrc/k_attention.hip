@@ -29,8 +29,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 constexpr int kDecThreads = 256;
 constexpr int kDecTile = 32;
 constexpr int kDecMaxG = 8;
-constexpr int kDecMaxChunks = 32;
-constexpr int kDecMinChunk = 16;  // keys per chunk, at least
+constexpr int kDecMaxChunks = 64;
+constexpr int kDecCombineGroup = 32;  // chunk partials loaded per round of the combine
+constexpr int kDecMinChunk = 32;  // keys per chunk, at least
 
 // Split of `total` keys into nch chunks of len keys (the last may be
 // shorter, none is empty): as many chunks as allowed, each of at least
@@ -478,8 +479,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(AttnParams p) 
   if (!flag[0]) return;
 
   // Last block of kv head g: combine the nch chunks of its G heads, two
-  // outputs per thread at a time (one round for G * HD <= 512). The
-  // statistics and the first round's partials are loaded before any use.
+  // outputs per thread at a time (one round for G * HD <= 512), the chunk
+  // partials in groups of 32 loaded before any is used.
   float m[MAXV], l[MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; j++) {
@@ -489,41 +490,45 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(AttnParams p) 
     m[j] = ok ? cload(pb) : -INFINITY;
     l[j] = ok ? cload(pb + 1) : 0.0f;
   }
+  constexpr int CG = kDecCombineGroup;
   for (int o0 = 0; o0 < G * HD; o0 += 2 * kDecThreads) {
-    float x[2][kDecMaxChunks];
+    float a[2] = {0.0f, 0.0f};
+    for (int c0 = 0; c0 < nch; c0 += CG) {
+      float x[2][CG];
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
-      const int o = o0 + tid + r * kDecThreads, h = o / HD, dd = o % HD;
-      const float* pb = p.partial + (size_t)(g * G + h) * p.splits * (HD + 2) + 2 + dd;
+      for (int r = 0; r < 2; r++) {
+        const int o = min(o0 + tid + r * kDecThreads, G * HD - 1), h = o / HD, dd = o % HD;
+        const float* pb = p.partial + (size_t)(g * G + h) * p.splits * (HD + 2) + 2 + dd;
 #pragma unroll
-      for (int i = 0; i < kDecMaxChunks; i++)
-        x[r][i] = o < G * HD && i < nch ? cload(pb + (size_t)i * (HD + 2)) : 0.0f;
-    }
-    if (o0 == 0) {
+        for (int i = 0; i < CG; i++) x[r][i] = cload(pb + (size_t)min(c0 + i, nch - 1) * (HD + 2));
+      }
+      if (o0 == 0 && c0 == 0) {
 #pragma unroll
-      for (int j = 0; j < MAXV; j++) {
-        const int h = wave + j * NW;
-        if (h < G) {
-          const float M = wave_max(m[j]);
-          const float w = lane < nch ? expf(m[j] - M) : 0.0f;
-          if (lane < kDecMaxChunks) wts[h * (kDecMaxChunks + 1) + lane] = w;
-          const float wl = wave_sum(w * l[j]);
-          if (lane == 0) wts[h * (kDecMaxChunks + 1) + kDecMaxChunks] = wl;
+        for (int j = 0; j < MAXV; j++) {
+          const int h = wave + j * NW;
+          if (h < G) {
+            const float M = wave_max(m[j]);
+            const float w = lane < nch ? expf(m[j] - M) : 0.0f;
+            if (lane < kDecMaxChunks) wts[h * (kDecMaxChunks + 1) + lane] = w;
+            const float wl = wave_sum(w * l[j]);
+            if (lane == 0) wts[h * (kDecMaxChunks + 1) + kDecMaxChunks] = wl;
+          }
         }
+        __syncthreads();
       }
-      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        const int h = min(o0 + tid + r * kDecThreads, G * HD - 1) / HD;
+        const float* w = wts + h * (kDecMaxChunks + 1) + c0;
+#pragma unroll
+        for (int i = 0; i < CG; i++)
+          if (c0 + i < nch) a[r] = fmaf(w[i], x[r][i], a[r]);
+      }
     }
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       const int o = o0 + tid + r * kDecThreads, h = o / HD, dd = o % HD;
-      if (o < G * HD) {
-        const float* w = wts + h * (kDecMaxChunks + 1);
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kDecMaxChunks; i++)
-          if (i < nch) a = fmaf(w[i], x[r][i], a);
-        p.out[(size_t)(g * G + h) * HD + dd] = a / w[kDecMaxChunks];
-      }
+      if (o < G * HD) p.out[(size_t)(g * G + h) * HD + dd] = a[r] / wts[h * (kDecMaxChunks + 1) + kDecMaxChunks];
     }
   }
   if (tid == 0) __hip_atomic_store(p.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
