@@ -167,7 +167,8 @@ def main():
 
     decode_kernels = ["qkv_gemv", "attention_decode", "o_gemv", "gate_up_gemv", "down_gemv",
                       "logits_gemv", "argmax", "moe_route", "moe_gate_up", "moe_down"]
-    prefill_kernels = ["qkv_gemm", "o_gemm", "gate_up_gemm", "down_gemm"]
+    prefill_kernels = ["qkv_gemm", "o_gemm", "gate_up_gemm", "down_gemm", "moe_gate_up_prefill",
+                       "moe_down_prefill"]
     kernels = {}
     for k, v in stats.items():
         avg_ms = v["total_ms"] / v["launches"]

@@ -28,7 +28,9 @@ int strasgpt_kbench_gemv_variants(void);
  *   bit 1: before each timed launch, an untimed kernel reads one word per
  *          64 KiB of that launch's weights (warms address translation);
  *   bit 2: time all launches back to back between two events instead of
- *          one event pair per launch. */
+ *          one event pair per launch;
+ *   bit 3: one weight copy re-read by every launch (Infinity Cache hits
+ *          when it fits). */
 int strasgpt_kbench_gemv2(int n, int k, int dual, int flags, int variant, int iters,
                           double* avg_us, double* rel_err);
 

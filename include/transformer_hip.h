@@ -123,7 +123,12 @@ enum transformer_kernel_class {
   TRANSFORMER_K_ARGMAX, TRANSFORMER_K_MOE_ROUTE, TRANSFORMER_K_MOE_GATE_UP,
   TRANSFORMER_K_MOE_DOWN, TRANSFORMER_K_QKV_GEMM, TRANSFORMER_K_ATTENTION_PREFILL,
   TRANSFORMER_K_O_GEMM, TRANSFORMER_K_GATE_UP_GEMM, TRANSFORMER_K_DOWN_GEMM,
-  TRANSFORMER_K_ELEMENTWISE, TRANSFORMER_K_CLASS_COUNT
+  TRANSFORMER_K_ELEMENTWISE,
+  /* MoE FFN of prompt chunks (more than one token): router, expert
+   * gate/up + SwiGLU and down projections (grouped MFMA GEMMs from 8
+   * tokens on); the MOE classes above count single-token decode steps. */
+  TRANSFORMER_K_MOE_ROUTE_PREFILL, TRANSFORMER_K_MOE_GATE_UP_PREFILL,
+  TRANSFORMER_K_MOE_DOWN_PREFILL, TRANSFORMER_K_CLASS_COUNT
 };
 
 typedef struct transformer_kernel_stat {

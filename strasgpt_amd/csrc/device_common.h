@@ -40,10 +40,12 @@ __device__ __forceinline__ float e2m1_value(uint32_t code) {
   return (code & 8u) ? -v : v;
 }
 __device__ __forceinline__ float e8m0_scale(uint32_t s) {
-  // 2^(s-127) as an fp32 bit pattern; s = 0 gives 2^-127 (subnormal) and
-  // s = 255 is NaN.
-  if (s == 255u) return __uint_as_float(0x7FC00000u);
-  return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+  // 2^(s-127) as an fp32 bit pattern: s << 23 for 1 <= s <= 254; s = 0
+  // gives 2^-127 (subnormal, 0x00400000) and s = 255 NaN (0x7FC00000).
+  // Integer arithmetic only (s <= 255): (s - 1) >> 31 is 1 only for s = 0,
+  // (s + 1) >> 8 only for s = 255, so the compiler emits no branch (a
+  // branch right after the byte load would wait for it).
+  return __uint_as_float((s << 23) | (((s - 1u) >> 31) << 22) | (((s + 1u) >> 8) << 22));
 }
 
 // 16-byte streaming load of weights that are read once per step.

@@ -30,7 +30,7 @@ constexpr int kWaves = kThreads / WAVE;
 constexpr int kHalves = 2 * kWaves;  // half-waves per block
 constexpr int kSteps = 3;            // blocks of 32 values per lane per pass (96 per row)
 constexpr int kGuRows = 2;           // rows per half-wave (gate/up)
-constexpr int kDownRows = 2;         // rows per half-wave (down)
+constexpr int kDownRows = 1;         // rows per half-wave (down)
 
 // Two values of byte `B` of `w` times `sc` (low nibble first).
 template <int B>
@@ -38,25 +38,49 @@ __device__ __forceinline__ float2v fp4_pair(uint32_t w, float sc) {
   return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, B);
 }
 
-// acc + (block of 32 MXFP4 values, scale sc) . xb[0, 32), in element order.
-__device__ __forceinline__ float mx_block_dot(uint4 q, float sc, const float* xb, float acc) {
-  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+// Activation rows in LDS: rows of K values back to back, each 32-value
+// block (8 chunks of 16 bytes) with chunk c stored at position c ^ (b & 7)
+// of block b. Lanes that take consecutive blocks then read the same
+// logical chunk from 8 different bank groups (without the swizzle every
+// lane of a half-wave would hit the same four banks). The rows are copied
+// by the global-to-LDS DMA (16 bytes per lane, no registers held): LDS slot
+// u of the copy fetches the global chunk that belongs there. A block of
+// zeros follows the rows: lanes past a row's last block read it, with a
+// zero scale, and add exact zeros.
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+__device__ __forceinline__ void dma_slot(const float* src, int u0, int u, float* dst) {
+  const int blk = u >> 3, c = (u & 7) ^ (blk & 7);
+  __builtin_amdgcn_global_load_lds((const void*)(src + blk * 32 + c * 4), (lds_ptr)(dst + u0 * 4), 16, 0, 0);
+}
+
+// n floats (n % 32 == 0): the first NI * NT / 4 ... slots by NI unrolled
+// instructions per wave (a loop would leave the compiler unable to count
+// the loads issued after it), the rest, with LOOP only, by a loop.
+template <int NT, int NI, bool LOOP>
+__device__ __forceinline__ void dma_rows(const float* src, int n, float* dst) {
+  const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const int slots = n / 4;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float4 xa = *(const float4*)(xb + 8 * i);
-    const float4 xc = *(const float4*)(xb + 8 * i + 4);
-    const float2v v0 = fp4_pair<0>(w[i], sc), v1 = fp4_pair<1>(w[i], sc);
-    const float2v v2 = fp4_pair<2>(w[i], sc), v3 = fp4_pair<3>(w[i], sc);
-    acc = fmaf(v0.x, xa.x, acc);
-    acc = fmaf(v0.y, xa.y, acc);
-    acc = fmaf(v1.x, xa.z, acc);
-    acc = fmaf(v1.y, xa.w, acc);
-    acc = fmaf(v2.x, xc.x, acc);
-    acc = fmaf(v2.y, xc.y, acc);
-    acc = fmaf(v3.x, xc.z, acc);
-    acc = fmaf(v3.y, xc.w, acc);
+  for (int i = 0; i < NI; i++) {
+    const int u0 = wave * WAVE + i * NT, u = u0 + lane;
+    if (u < slots) dma_slot(src, u0, u, dst);  // inactive lanes write nothing
   }
-  return acc;
+  if (LOOP) {
+    for (int u0 = wave * WAVE + NI * NT; u0 < slots; u0 += NT) {
+      const int u = u0 + lane;
+      if (u < slots) dma_slot(src, u0, u, dst);
+    }
+  }
+}
+
+// Block b of the row at `row` (or the zero block for b >= nb): base and
+// chunk swizzle. The swizzle follows the block's index in the whole DMA
+// copy: row_blocks = the blocks of the rows before this one.
+__device__ __forceinline__ const float* xblock(const float* row, const float* zero, int b, int nb,
+                                               int row_blocks, int& bm) {
+  bm = b < nb ? ((row_blocks + b) & 7) : 0;
+  return b < nb ? row + b * 32 : zero;
 }
 
 // Sum over the 32 lanes of a half-wave, the same in each of them.
@@ -66,11 +90,14 @@ __device__ __forceinline__ float half_sum(float v) {
   return v;
 }
 
-// One pass of a half-wave over blocks [b0 + hl, b0 + hl + 32 * kSteps) of
-// row `row` (blocks past nb are not loaded): codes and scales into registers.
+// One pass of a half-wave over blocks b0 + hl + 32 i (i < kSteps) of a row:
+// codes and scale bytes in registers. Blocks past the row load the row's
+// last block; the dot product gives them scale 0 and the zero block of the
+// activation row. Nothing here uses a loaded value (code between these
+// loads and the block barrier must not wait for them).
 struct RowLoad {
   uint4 q[kSteps];
-  float sc[kSteps];
+  uint8_t sc[kSteps];  // E8M0 byte (used only where the block lies in the row)
 };
 
 __device__ __forceinline__ void row_load(const uint8_t* blocks, const uint8_t* scales, size_t row,
@@ -79,30 +106,99 @@ __device__ __forceinline__ void row_load(const uint8_t* blocks, const uint8_t* s
   const uint8_t* bs = scales + row * (size_t)nb;
 #pragma unroll
   for (int i = 0; i < kSteps; i++) {
-    const int b = min(b0 + hl + 32 * i, nb - 1);  // past the row: a loaded block, never used
-    r.q[i] = load_nt_u4(bq + (size_t)b * 16);
-    r.sc[i] = e8m0_scale(bs[b]);
+    const int b = b0 + hl + 32 * i, bc = min(b, nb - 1);
+    r.q[i] = load_nt_u4(bq + (size_t)bc * 16);
+    r.sc[i] = bs[bc];
   }
 }
 
-__device__ __forceinline__ float row_dot(const RowLoad& r, const float* xs, int nb, int b0, int hl,
-                                         float acc) {
+// Materialises v[] in registers here: the products of a step cannot be
+// deferred to the end of the kernel (the compiler would otherwise sink them
+// and keep every activation read of the pass live at once).
+template <int N>
+__device__ __forceinline__ void pin_values(float (&v)[N]) {
 #pragma unroll
-  for (int i = 0; i < kSteps; i++) {
-    const int b = b0 + hl + 32 * i;
-    if (b < nb) acc = mx_block_dot(r.q[i], r.sc[i], xs + b * 32, acc);
-  }
-  return acc;
+  for (int i = 0; i < N; i++) asm volatile("" : "+v"(v[i]));
 }
 
-// Router + top-k + softmax, one block of kRouteThreads per token: each
-// wave takes experts w, w + 8, ..., kRouteE at a time with every 128-bit
-// weight load of those experts in flight before the first is used; wave 0
-// then selects.
+// acc[r] += block `st` of rows r < NR (codes q, scale sc) . the activation
+// block at xb (chunk swizzle bm); each 8-value slice is read from LDS once
+// for all rows.
+// Per row the products are accumulated in element order.
+template <int NR>
+__device__ __forceinline__ void rows_block_dot(const RowLoad* rl, int st, const float* xb, int bm, bool in_row,
+                                               float* acc) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float4 xa = *(const float4*)(xb + (((2 * i) ^ bm) << 2));
+    const float4 xc = *(const float4*)(xb + (((2 * i + 1) ^ bm) << 2));
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const uint4 q = rl[r].q[st];
+      const uint32_t w = i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+      // scale 0 past the row, without a branch
+      const float sc = __uint_as_float(__float_as_uint(e8m0_scale(rl[r].sc[st])) & (0u - (uint32_t)in_row));
+      const float2v v0 = fp4_pair<0>(w, sc), v1 = fp4_pair<1>(w, sc);
+      const float2v v2 = fp4_pair<2>(w, sc), v3 = fp4_pair<3>(w, sc);
+      float a = acc[r];
+      a = fmaf(v0.x, xa.x, a);
+      a = fmaf(v0.y, xa.y, a);
+      a = fmaf(v1.x, xa.z, a);
+      a = fmaf(v1.y, xa.w, a);
+      a = fmaf(v2.x, xc.x, a);
+      a = fmaf(v2.y, xc.y, a);
+      a = fmaf(v3.x, xc.z, a);
+      a = fmaf(v3.y, xc.w, a);
+      acc[r] = a;
+    }
+  }
+}
+
+// Waits until at most LOADS vector-memory operations are in flight (63 at
+// most, the counter's range): with the activation DMA issued before LOADS
+// weight loads (one code and one scale load per step and row), that
+// completes the DMA.
+template <int LOADS>
+__device__ __forceinline__ void wait_dma_behind() {
+  constexpr int N = LOADS < 63 ? LOADS : 63;
+  __builtin_amdgcn_sched_barrier(0);  // no use of a weight load may be scheduled above this wait
+  // s_waitcnt encoding (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Router + top-k + softmax, one block of kRouteThreads per token: the
+// activation row goes to LDS by DMA, then each wave issues every 128-bit
+// weight load of its first kRouteE experts before any is used (further
+// experts, for E > kRouteWaves * kRouteE, follow in a loop); wave 0 then
+// selects.
 constexpr int kRouteThreads = 512;
 constexpr int kRouteWaves = kRouteThreads / WAVE;
 constexpr int kRouteE = 4;     // experts per wave per pass
 constexpr int kRouteLd = 6;    // 8-value chunks per lane per expert per pass
+constexpr int kRouteDma = 4;   // unrolled DMA instructions per wave: d <= 8192
+
+__device__ __forceinline__ void route_load(const uint16_t* router, int E, int d, int e0, int c0, int lane,
+                                           uint4 (&w)[kRouteE][kRouteLd]) {
+  const int chunks = d / 8;
+#pragma unroll
+  for (int i = 0; i < kRouteE; i++) {
+    const uint16_t* wr = router + (size_t)min(e0 + i, E - 1) * d;
+#pragma unroll
+    for (int u = 0; u < kRouteLd; u++) w[i][u] = load_nt_u4(wr + min(c0 + u * WAVE + lane, chunks - 1) * 8);
+  }
+}
+
+__device__ __forceinline__ void route_dot(const uint4 (&w)[kRouteE][kRouteLd], const float* xs, int chunks,
+                                          int c0, int lane, float (&acc)[kRouteE]) {
+#pragma unroll
+  for (int i = 0; i < kRouteE; i++)
+#pragma unroll
+    for (int u = 0; u < kRouteLd; u++) {
+      const int c = c0 + u * WAVE + lane;
+      if (c < chunks)
+        acc[i] = dot8(w[i][u], *(const float4*)(xs + c * 8), *(const float4*)(xs + c * 8 + 4), acc[i]);
+    }
+}
 
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, const uint16_t* router,
                                                               int E, int d, int k, int* sel,
@@ -111,30 +207,27 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, c
   float* xs = sm;        // [d]
   float* lg = sm + d;    // [E]
   const int t = blockIdx.x, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  for (int i = threadIdx.x * 4; i < d; i += kRouteThreads * 4)
-    *(float4*)(xs + i) = *(const float4*)(xn + (size_t)t * d + i);
-  __syncthreads();
+  {
+    const float* xrow = xn + (size_t)t * d;
+#pragma unroll
+    for (int i = 0; i < kRouteDma; i++) {
+      const int u0 = wave * WAVE + i * kRouteThreads, u = u0 + lane;
+      if (u < d / 4)  // inactive lanes write nothing
+        __builtin_amdgcn_global_load_lds((const void*)(xrow + u * 4), (lds_ptr)(xs + u0 * 4), 16, 0, 0);
+    }
+  }
   const int chunks = d / 8;
+  uint4 w[kRouteE][kRouteLd];
+  route_load(router, E, d, wave * kRouteE, 0, lane, w);  // (clamped rows for a wave without experts)
+  wait_dma_behind<kRouteE * kRouteLd>();
+  __syncthreads();
   for (int e0 = wave * kRouteE; e0 < E; e0 += kRouteWaves * kRouteE) {
     float acc[kRouteE];
 #pragma unroll
     for (int i = 0; i < kRouteE; i++) acc[i] = 0.0f;
     for (int c0 = 0; c0 < chunks; c0 += kRouteLd * WAVE) {
-      uint4 w[kRouteE][kRouteLd];
-#pragma unroll
-      for (int i = 0; i < kRouteE; i++) {
-        const uint16_t* wr = router + (size_t)min(e0 + i, E - 1) * d;
-#pragma unroll
-        for (int u = 0; u < kRouteLd; u++) w[i][u] = load_nt_u4(wr + min(c0 + u * WAVE + lane, chunks - 1) * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < kRouteE; i++)
-#pragma unroll
-        for (int u = 0; u < kRouteLd; u++) {
-          const int c = c0 + u * WAVE + lane;
-          if (c < chunks)
-            acc[i] = dot8(w[i][u], *(const float4*)(xs + c * 8), *(const float4*)(xs + c * 8 + 4), acc[i]);
-        }
+      if (e0 != wave * kRouteE || c0 != 0) route_load(router, E, d, e0, c0, lane, w);
+      route_dot(w, xs, chunks, c0, lane, acc);
     }
 #pragma unroll
     for (int i = 0; i < kRouteE; i++) {
@@ -147,10 +240,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, c
     // k rounds of a wave-wide selection with the semantics of a sequential
     // scan over the experts not yet taken: start from the first, replace
     // on strictly greater (ties keep the lower id; a NaN first candidate
-    // stays, later NaNs never win). Lane l holds experts l + 64 m.
+    // stays, later NaNs never win). Lane l holds experts l + 64 m; lane j
+    // keeps the j-th pick.
     constexpr int kMaxPer = 1024 / WAVE;
     unsigned taken = 0;  // bit m: expert lane + 64 m taken
-    int idx[64];
+    int mine = 0, top = 0;
     for (int j = 0; j < k; j++) {
       int first = 0x7fffffff, bi = 0x7fffffff;
       float bv = -INFINITY;
@@ -178,93 +272,155 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, c
       }
       const float fv = lg[first];
       const int pick = (fv != fv || bi == 0x7fffffff) ? first : bi;
-      idx[j] = pick;
+      if (j == 0) top = pick;
+      if (lane == j) mine = pick;
       if (pick % WAVE == lane) taken |= 1u << (pick / WAVE);
     }
-    if (lane == 0) {
-      float val[64];
-      float sum = 0.0f;
-      for (int j = 0; j < k; j++) {
-        val[j] = expf(lg[idx[j]] - lg[idx[0]]);
-        sum += val[j];
-      }
-      for (int j = 0; j < k; j++) {
-        sel[t * k + j] = idx[j];
-        sel_w[t * k + j] = val[j] / sum;
-      }
+    // softmax over the k picks: e^(l_j - l_0), summed in pick order
+    const float v = lane < k ? expf(lg[mine] - lg[top]) : 0.0f;
+    float sum = 0.0f;
+    for (int j = 0; j < k; j++) sum += __shfl(v, j, WAVE);
+    if (lane < k) {
+      sel[t * k + lane] = mine;
+      sel_w[t * k + lane] = v / sum;
     }
   }
 }
 
 // act[s][h] = silu(gate_e[h] . x_s) * (up_e[h] . x_s), slot s = (token, j):
 // block (row group, slot); each half-wave takes kGuRows rows of both
-// matrices, all their loads of a pass in flight at once.
+// matrices. Order: expert id and activation loads, then every weight load
+// of the first pass, then the activation row into LDS.
+__device__ __forceinline__ void gu_load(const MoeGemvParams& p, int e, int r0, int nb, int b0, int hl,
+                                        RowLoad (&ld)[2 * kGuRows]) {
+#pragma unroll
+  for (int r = 0; r < kGuRows; r++) {
+    const size_t row = (size_t)e * p.N + min(r0 + r, p.N - 1);
+    row_load(p.blocks, p.scales, row, nb, b0, hl, ld[r]);
+    row_load(p.blocks2, p.scales2, row, nb, b0, hl, ld[kGuRows + r]);
+  }
+}
+
+__device__ __forceinline__ void gu_dot(const RowLoad (&ld)[2 * kGuRows], const float* xs, const float* zero,
+                                       int nb, int b0, int hl, float (&acc)[2 * kGuRows]) {
+#pragma unroll
+  for (int st = 0; st < kSteps; st++) {
+    int bm;
+    const int b = b0 + hl + 32 * st;
+    const float* xb = xblock(xs, zero, b, nb, 0, bm);
+    rows_block_dot<2 * kGuRows>(ld, st, xb, bm, b < nb, acc);
+    pin_values<2 * kGuRows>(acc);
+  }
+}
+
+
+// LOOP: rows longer than one pass (K > 32 * 32 * kSteps) take more passes
+// (kept out of the one-pass kernel, whose registers it would share).
+constexpr int kGuDma = 4;    // unrolled DMA instructions per wave: K <= 4096 without LOOP
+constexpr int kDownDma = 12; // k * K <= 12288 without LOOP
+template <bool LOOP>
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(MoeGemvParams p) {
-  extern __shared__ __attribute__((aligned(16))) float xs[];
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [K] swizzled, then 32 zeros
   const int slot = blockIdx.y, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const int half = wave * 2 + lane / 32, hl = lane % 32;
-  const float* xr = p.x + (size_t)(slot / p.topk) * p.K;
-  for (int i = threadIdx.x * 4; i < p.K; i += kThreads * 4) *(float4*)(xs + i) = *(const float4*)(xr + i);
-  __syncthreads();
   const int e = p.expert[slot];
+  dma_rows<kThreads, kGuDma, LOOP>(p.x + (size_t)(slot / p.topk) * p.K, p.K, xs);
   const int nb = p.K / 32;
   const int r0 = (blockIdx.x * kHalves + half) * kGuRows;
-  float g[kGuRows], u[kGuRows];
+  float acc[2 * kGuRows];  // gate rows, then up rows
 #pragma unroll
-  for (int r = 0; r < kGuRows; r++) g[r] = u[r] = 0.0f;
-  for (int b0 = 0; b0 < nb; b0 += 32 * kSteps) {
-    RowLoad lg[kGuRows], lu[kGuRows];
-#pragma unroll
-    for (int r = 0; r < kGuRows; r++) {
-      const size_t row = (size_t)e * p.N + min(r0 + r, p.N - 1);
-      row_load(p.blocks, p.scales, row, nb, b0, hl, lg[r]);
-      row_load(p.blocks2, p.scales2, row, nb, b0, hl, lu[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < kGuRows; r++) {
-      g[r] = row_dot(lg[r], xs, nb, b0, hl, g[r]);
-      u[r] = row_dot(lu[r], xs, nb, b0, hl, u[r]);
+  for (int r = 0; r < 2 * kGuRows; r++) acc[r] = 0.0f;
+  RowLoad ld[2 * kGuRows];
+  gu_load(p, e, r0, nb, 0, hl, ld);
+  float* zero = xs + p.K;
+  if (threadIdx.x < 32) zero[threadIdx.x] = 0.0f;
+  wait_dma_behind<2 * 2 * kGuRows * kSteps>();
+  __syncthreads();
+  gu_dot(ld, xs, zero, nb, 0, hl, acc);
+  if (LOOP) {
+    for (int b0 = 32 * kSteps; b0 < nb; b0 += 32 * kSteps) {
+      RowLoad ln[2 * kGuRows];
+      gu_load(p, e, r0, nb, b0, hl, ln);
+      gu_dot(ln, xs, zero, nb, b0, hl, acc);
     }
   }
 #pragma unroll
   for (int r = 0; r < kGuRows; r++) {
-    const float gs = half_sum(g[r]), us = half_sum(u[r]);
+    const float gs = half_sum(acc[r]), us = half_sum(acc[kGuRows + r]);
     if (hl == 0 && r0 + r < p.N) p.y[(size_t)slot * p.N + r0 + r] = silu_mul(gs, us);
   }
 }
 
 // y[t][n] += sum_j fmaf order of w_j * (down_e_j[n] . act[t*k + j]):
-// block (row group, token); each half-wave takes kDownRows rows in turn, for
-// every slot of the token, all of a row's loads of a pass in flight at once.
+// block (row group, token); each half-wave takes kDownRows rows, for every
+// slot of the token, all their loads of a pass in flight at once (the
+// activation DMA goes first).
 template <int KMAX>
+__device__ __forceinline__ void down_load(const MoeGemvParams& p, const int (&e)[KMAX], int n0, int nb, int b0,
+                                          int hl, RowLoad (&ld)[kDownRows * KMAX]) {
+#pragma unroll
+  for (int r = 0; r < kDownRows; r++)
+#pragma unroll
+    for (int j = 0; j < KMAX; j++)
+      row_load(p.blocks, p.scales, (size_t)e[j] * p.N + min(n0 + r, p.N - 1), nb, b0, hl, ld[r * KMAX + j]);
+}
+
+// Slots past k (KMAX > k) repeat slot k - 1; their sums are dropped.
+template <int KMAX>
+__device__ __forceinline__ void down_dot(const RowLoad (&ld)[kDownRows * KMAX], const float* as, const float* zero,
+                                         int k, int K, int nb, int b0, int hl, float (&dot)[kDownRows * KMAX]) {
+#pragma unroll
+  for (int st = 0; st < kSteps; st++) {
+#pragma unroll
+    for (int j = 0; j < KMAX; j++) {
+      int bm;
+      const int b = b0 + hl + 32 * st;
+      const int row = min(j, k - 1);
+      const float* xb = xblock(as + row * K, zero, b, nb, row * nb, bm);
+#pragma unroll
+      for (int r = 0; r < kDownRows; r++)
+        rows_block_dot<1>(&ld[r * KMAX + j], st, xb, bm, b < nb, &dot[r * KMAX + j]);
+    }
+    pin_values<kDownRows * KMAX>(dot);
+  }
+}
+
+template <int KMAX, bool LOOP>
 __global__ __launch_bounds__(kThreads) void down_kernel(MoeGemvParams p) {
-  extern __shared__ __attribute__((aligned(16))) float as[];  // [k][K]
+  extern __shared__ __attribute__((aligned(16))) float as[];  // [k][K] swizzled, then 32 zeros
   const int k = p.topk;
   const int t = blockIdx.y, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const int half = wave * 2 + lane / 32, hl = lane % 32;
-  for (int i = threadIdx.x * 4; i < k * p.K; i += kThreads * 4)
-    *(float4*)(as + i) = *(const float4*)(p.x + (size_t)t * k * p.K + i);
-  __syncthreads();
+  int e[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; j++) e[j] = p.expert[t * k + min(j, k - 1)];
+  dma_rows<kThreads, kDownDma, LOOP>(p.x + (size_t)t * k * p.K, k * p.K, as);
   const int nb = p.K / 32;
-  for (int n = (blockIdx.x * kHalves + half) * kDownRows, n1 = n + kDownRows; n < n1; n++) {
-    float dot[KMAX];
+  const int n0 = (blockIdx.x * kHalves + half) * kDownRows;
+  float dot[kDownRows * KMAX];
 #pragma unroll
-    for (int j = 0; j < KMAX; j++) dot[j] = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += 32 * kSteps) {
-      RowLoad ld[KMAX];
-#pragma unroll
-      for (int j = 0; j < KMAX; j++) {
-        const int e = p.expert[t * k + min(j, k - 1)];
-        row_load(p.blocks, p.scales, (size_t)e * p.N + min(n, p.N - 1), nb, b0, hl, ld[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < KMAX; j++)
-        if (j < k) dot[j] = row_dot(ld[j], as + j * p.K, nb, b0, hl, dot[j]);
+  for (int i = 0; i < kDownRows * KMAX; i++) dot[i] = 0.0f;
+  RowLoad ld[kDownRows * KMAX];  // row r, slot j at r * KMAX + j
+  down_load<KMAX>(p, e, n0, nb, 0, hl, ld);
+  float* zero = as + k * p.K;
+  if (threadIdx.x < 32) zero[threadIdx.x] = 0.0f;
+  wait_dma_behind<2 * kDownRows * KMAX * kSteps>();
+  __syncthreads();
+  down_dot<KMAX>(ld, as, zero, k, p.K, nb, 0, hl, dot);
+  if (LOOP) {
+    for (int b0 = 32 * kSteps; b0 < nb; b0 += 32 * kSteps) {
+      RowLoad ln[kDownRows * KMAX];
+      down_load<KMAX>(p, e, n0, nb, b0, hl, ln);
+      down_dot<KMAX>(ln, as, zero, k, p.K, nb, b0, hl, dot);
     }
+  }
+#pragma unroll
+  for (int r = 0; r < kDownRows; r++) {
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < KMAX; j++)
-      if (j < k) acc = fmaf(p.weight[t * k + j], half_sum(dot[j]), acc);
+      if (j < k) acc = fmaf(p.weight[t * k + j], half_sum(dot[r * KMAX + j]), acc);
+    const int n = n0 + r;
     if (hl == 0 && n < p.N) p.y[(size_t)t * p.N + n] += acc;
   }
 }
@@ -497,6 +653,7 @@ void moe_route(const float* xn, int T, const uint16_t* router, int E, int d, int
                float* sel_w, hipStream_t s) {
   if (k > 64 || k > E || E > 1024) ST_DIE("MoE top-k must satisfy k <= 64, k <= E <= 1024");
   if (d % 8 || (uintptr_t)router % 16 || (uintptr_t)xn % 16) ST_DIE("MoE router rows must be 16-byte aligned");
+  if (d > kRouteDma * kRouteThreads * 4) ST_DIE("MoE router supports embedding_dim <= 8192");
   const size_t shm = (size_t)(d + E) * sizeof(float);
   set_lds(route_kernel, shm);
   hipLaunchKernelGGL(route_kernel, dim3(T), dim3(kRouteThreads), shm, s, xn, router, E, d, k, sel, sel_w);
@@ -506,11 +663,16 @@ void moe_route(const float* xn, int T, const uint16_t* router, int E, int d, int
 void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s) {
   if (p.K % 32 || ((uintptr_t)p.blocks | (uintptr_t)p.blocks2) % 16) ST_DIE("MXFP4 rows must be 32-value aligned");
   if (p.topk <= 0 || p.tokens <= 0) ST_DIE("MoE GEMV needs tokens and topk");
-  const size_t shm = (size_t)p.K * sizeof(float);
-  set_lds(swiglu_kernel, shm);
+  const size_t shm = ((size_t)p.K + 32) * sizeof(float);  // row, then a zero block
   const int rows_per_block = kHalves * kGuRows;
   dim3 grid((p.N + rows_per_block - 1) / rows_per_block, p.tokens * p.topk);
-  hipLaunchKernelGGL(swiglu_kernel, grid, dim3(kThreads), shm, s, p);
+  if (p.K <= 32 * 32 * kSteps && p.K <= kGuDma * kThreads * 4) {
+    set_lds(swiglu_kernel<false>, shm);
+    hipLaunchKernelGGL(swiglu_kernel<false>, grid, dim3(kThreads), shm, s, p);
+  } else {
+    set_lds(swiglu_kernel<true>, shm);
+    hipLaunchKernelGGL(swiglu_kernel<true>, grid, dim3(kThreads), shm, s, p);
+  }
   HIP_CHECK(hipGetLastError());
 }
 
@@ -525,15 +687,22 @@ void moe_gemv_down(const MoeGemvParams& p, hipStream_t s) {
   if (p.K % 32 || (uintptr_t)p.blocks % 16) ST_DIE("MXFP4 rows must be 32-value aligned");
   if (p.topk <= 0 || p.tokens <= 0) ST_DIE("MoE GEMV needs tokens and topk");
   if (p.topk > 8) ST_DIE("MoE down projection supports top-k up to 8");
-  const size_t shm = (size_t)p.topk * p.K * sizeof(float);
+  const size_t shm = ((size_t)p.topk * p.K + 32) * sizeof(float);
   dim3 grid((p.N + kHalves * kDownRows - 1) / (kHalves * kDownRows), p.tokens);
+  const bool loop = p.K > 32 * 32 * kSteps || p.topk * p.K > kDownDma * kThreads * 4;
+#define DOWN_CASE(KM, LP)                                                      \
+  do {                                                                         \
+    set_lds(down_kernel<KM, LP>, shm);                                         \
+    hipLaunchKernelGGL((down_kernel<KM, LP>), grid, dim3(kThreads), shm, s, p); \
+  } while (0)
   if (p.topk <= 4) {
-    set_lds(down_kernel<4>, shm);
-    hipLaunchKernelGGL(down_kernel<4>, grid, dim3(kThreads), shm, s, p);
+    if (loop) DOWN_CASE(4, true);
+    else DOWN_CASE(4, false);
   } else {
-    set_lds(down_kernel<8>, shm);
-    hipLaunchKernelGGL(down_kernel<8>, grid, dim3(kThreads), shm, s, p);
+    if (loop) DOWN_CASE(8, true);
+    else DOWN_CASE(8, false);
   }
+#undef DOWN_CASE
   HIP_CHECK(hipGetLastError());
 }
 

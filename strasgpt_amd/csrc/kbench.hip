@@ -270,16 +270,18 @@ extern "C" int strasgpt_kbench_gemv(int n, int k, int dual, int variant, int ite
 
 extern "C" int strasgpt_kbench_gemv2(int n, int k, int dual, int flags, int variant, int iters,
                                      double* avg_us, double* rel_err) {
-  const bool norm = flags & 1, touch = flags & 2, batch = flags & 4;
+  const bool norm = flags & 1, touch = flags & 2, batch = flags & 4, reuse = flags & 8;
   if (n <= 0 || k <= 0 || k % 8 || k > 16384 || iters <= 0 || variant < 0 ||
       variant >= sg::gemv_variant_count())
     return -1;
   hipStream_t s;
   HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   // Enough distinct weight copies to exceed the 256 MiB Infinity Cache
-  // twice over, used round-robin so that every launch streams from HBM.
+  // twice over, used round-robin so that every launch streams from HBM
+  // (flag 8: one copy, re-read by every launch).
   const size_t bytes = (size_t)n * k * 2 * (dual ? 2 : 1);
-  const int copies = (int)std::min<size_t>(64, std::max<size_t>(2, (size_t)(1u << 30) / bytes + 1));
+  const int copies =
+      reuse ? 1 : (int)std::min<size_t>(64, std::max<size_t>(2, (size_t)(1u << 30) / bytes + 1));
   std::vector<uint16_t*> w(copies), w2(copies, nullptr);
   uint16_t* nw = nullptr;
   float *x, *y, *yr, *xn;

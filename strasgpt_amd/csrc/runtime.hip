@@ -330,7 +330,9 @@ enum {
   K_MOE_GU = TRANSFORMER_K_MOE_GATE_UP, K_MOE_DOWN = TRANSFORMER_K_MOE_DOWN,
   K_QKV_GEMM = TRANSFORMER_K_QKV_GEMM, K_ATT_PRE = TRANSFORMER_K_ATTENTION_PREFILL,
   K_O_GEMM = TRANSFORMER_K_O_GEMM, K_GU_GEMM = TRANSFORMER_K_GATE_UP_GEMM,
-  K_DOWN_GEMM = TRANSFORMER_K_DOWN_GEMM, K_ELEM = TRANSFORMER_K_ELEMENTWISE
+  K_DOWN_GEMM = TRANSFORMER_K_DOWN_GEMM, K_ELEM = TRANSFORMER_K_ELEMENTWISE,
+  K_ROUTE_PRE = TRANSFORMER_K_MOE_ROUTE_PREFILL, K_MOE_GU_PRE = TRANSFORMER_K_MOE_GATE_UP_PREFILL,
+  K_MOE_DOWN_PRE = TRANSFORMER_K_MOE_DOWN_PREFILL
 };
 
 double mxfp4_bytes(double values) { return values * (0.5 + 1.0 / 32.0); }
@@ -349,7 +351,7 @@ void ffn_moe(Dev* D, int l, int T) {
     sg::rmsnorm_rows(D->x, W16(D, W_FFN_NORM, l), D->xn, T, D->d, D->eps, s);
   }
   {
-    Prof pr(D, K_ROUTE, (double)D->E * d * 2, 2.0 * T * D->E * d);
+    Prof pr(D, T == 1 ? K_ROUTE : K_ROUTE_PRE, (double)D->E * d * 2, 2.0 * T * D->E * d);
     sg::moe_route(D->xn, T, W16(D, W_ROUTER, l), D->E, D->d, D->topk, D->moe_sel, D->moe_w, s);
   }
   if (T >= kMoeGroupedMinTokens) {
@@ -374,7 +376,7 @@ void ffn_moe(Dev* D, int l, int T) {
     g.K = D->d;
     g.y = D->moe_act;
     {
-      Prof pr(D, K_MOE_GU, used * mxfp4_bytes(2 * H * d), 4.0 * n * H * d);
+      Prof pr(D, K_MOE_GU_PRE, used * mxfp4_bytes(2 * H * d), 4.0 * n * H * d);
       sg::moe_group_gemm(g, s);
     }
     sg::MoeGemmParams dn{};
@@ -391,7 +393,7 @@ void ffn_moe(Dev* D, int l, int T) {
     dn.K = D->H;
     dn.y = D->moe_out;
     {
-      Prof pr(D, K_MOE_DOWN, used * mxfp4_bytes(H * d), 2.0 * n * H * d);
+      Prof pr(D, K_MOE_DOWN_PRE, used * mxfp4_bytes(H * d), 2.0 * n * H * d);
       sg::moe_group_gemm(dn, s);
       sg::moe_combine(D->moe_out, D->moe_w, T, D->topk, D->d, D->x, s);
     }
@@ -410,7 +412,7 @@ void ffn_moe(Dev* D, int l, int T) {
   g.K = D->d;
   g.y = D->moe_act;
   {
-    Prof pr(D, K_MOE_GU, T * k * mxfp4_bytes(2 * H * d), 4.0 * T * k * H * d);
+    Prof pr(D, T == 1 ? K_MOE_GU : K_MOE_GU_PRE, T * k * mxfp4_bytes(2 * H * d), 4.0 * T * k * H * d);
     sg::moe_gemv_swiglu(g, s);
   }
   sg::MoeGemvParams dn{};
@@ -425,7 +427,7 @@ void ffn_moe(Dev* D, int l, int T) {
   dn.K = D->H;
   dn.y = D->x;
   {
-    Prof pr(D, K_MOE_DOWN, T * k * mxfp4_bytes(H * d), 2.0 * T * k * H * d);
+    Prof pr(D, T == 1 ? K_MOE_DOWN : K_MOE_DOWN_PRE, T * k * mxfp4_bytes(H * d), 2.0 * T * k * H * d);
     sg::moe_gemv_down(dn, s);
   }
 }

@@ -124,7 +124,7 @@ DECODE_PERSISTENT, DECODE_GRAPH, DECODE_EAGER = 0, 1, 2
 PROFILE_KERNELS = ["qkv_gemv", "attention_decode", "o_gemv", "gate_up_gemv", "down_gemv",
                    "logits_gemv", "argmax", "moe_route", "moe_gate_up", "moe_down",
                    "qkv_gemm", "attention_prefill", "o_gemm", "gate_up_gemm", "down_gemm",
-                   "elementwise"]
+                   "elementwise", "moe_route_prefill", "moe_gate_up_prefill", "moe_down_prefill"]
 
 
 class Transformer:

@@ -102,6 +102,13 @@ TINY: Dict[str, ModelShape] = {
     "tiny-moe-long": ModelShape("tiny-moe-long", 64, 96, 2, 4, 2, 16, 256, 150000.0, 1e-5,
                                 200, 10, untied=True, experts=8, experts_per_tok=2,
                                 model_type="stras_moe", std=0.25),
+    # The MXFP4 MoE benchmark's expert shape (embedding and expert width
+    # 2880, top-4) on two layers: decode kernels with full-length rows.
+    # Weight std 0.02 as in the benchmark (at 0.25 and this width the
+    # attention scores reach the hundreds and amplify rounding noise).
+    "mid-moe": ModelShape("mid-moe", 2880, 2880, 2, 8, 2, 64, 512, 150000.0, 1e-5, 6, 10,
+                          untied=True, experts=8, experts_per_tok=4, model_type="stras_moe",
+                          std=0.02),
 }
 
 
