@@ -30,7 +30,6 @@ constexpr int kDecThreads = 256;
 constexpr int kDecTile = 32;
 constexpr int kDecMaxG = 8;
 constexpr int kDecMaxChunks = 64;
-constexpr int kDecCombineGroup = 32;  // chunk partials loaded per round of the combine
 constexpr int kDecMinChunk = 32;  // keys per chunk, at least
 
 // Split of `total` keys into nch chunks of len keys (the last may be
@@ -204,62 +203,45 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnParams p) {
   }
 }
 
-// LDS layout of the decode kernel (floats).
+// LDS layout of the decode kernel (floats). K rows are padded to HD + 4
+// floats: the lanes of a wave read one key row each, and with the padding
+// eight consecutive rows start in eight different bank groups.
 template <int HD>
 struct DecLds {
-  static constexpr int KG = kDecThreads / HD;  // key groups for P.V
-  static constexpr int qs = 0;                                 // [kDecMaxG][HD]
-  static constexpr int kn = qs + kDecMaxG * HD;                // [HD] new key
-  static constexpr int sc = kn + HD;                           // [kDecMaxG][kDecTile]
-  static constexpr int st = sc + kDecMaxG * kDecTile;          // [3][kDecMaxG] m, l, rescale
-  static constexpr int flag = st + 4 * kDecMaxG;               // [4]
-  static constexpr int tiles = flag + 4;                       // [2][K|V][kDecTile][HD]
-  // After the last tile, over the tile buffers:
-  static constexpr int red = tiles;                            // [KG][kDecMaxG][HD]
-  static constexpr int wts = red + KG * kDecMaxG * HD;         // [kDecMaxG][kDecMaxChunks + 1]
-  static constexpr int total = std::max(tiles + 4 * kDecTile * HD, wts + kDecMaxG * (kDecMaxChunks + 1));
+  static constexpr int KROW = HD + 4;
+  static constexpr int KT = kDecTile * KROW;       // K tile
+  static constexpr int VT = kDecTile * HD;         // V tile
+  static constexpr int qs = 0;                     // [kDecMaxG][HD] normalised, rotated queries
+  static constexpr int kn = qs + kDecMaxG * HD;    // [HD] this step's processed key
+  static constexpr int flag = kn + HD;             // [4]
+  static constexpr int tiles = flag + 4;           // [2][K tile | V tile]
+  static constexpr int total = tiles + 2 * (KT + VT);
+  static_assert(tiles % 4 == 0 && KT % 4 == 0, "tiles are 16-byte aligned");
 };
 
-// Keys [t0, t0 + n) of a kv head (rows of HD floats, contiguous) into the
-// LDS tiles kt / vt by the global-to-LDS DMA: 16 bytes per lane, each wave
-// filling 1 KiB of LDS per instruction. No registers are held; the caller
-// waits for vector memory operations and syncs the block before reading.
+// Keys [t0, t0 + n) of a kv head into LDS by the global-to-LDS DMA (16
+// bytes per lane): V rows back to back (each wave instruction fills 1 KiB),
+// K rows one instruction per row (its first HD / 4 lanes) into the padded
+// layout. No registers are held; the caller waits for vector memory
+// operations and syncs the block.
 template <int HD>
 __device__ __forceinline__ void dma_kv(const float* kb, const float* vb, int t0, int n, float* kt,
                                        float* vt) {
-  const int units = n * HD / 4;
+  constexpr int CPR = HD / 4;  // 16-byte chunks per row
+  constexpr int NWAVE = kDecThreads / WAVE;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const float* ks = kb + (size_t)t0 * HD;
   const float* vs = vb + (size_t)t0 * HD;
+  const int units = n * CPR;
   for (int u0 = wave * WAVE; u0 < units; u0 += kDecThreads) {
     const int u = u0 + lane;
-    if (u < units) {
-      __builtin_amdgcn_global_load_lds((const void*)(ks + u * 4), (lds_ptr)(kt + u0 * 4), 16, 0, 0);
+    if (u < units)
       __builtin_amdgcn_global_load_lds((const void*)(vs + u * 4), (lds_ptr)(vt + u0 * 4), 16, 0, 0);
-    }
   }
-}
-
-// N consecutive floats of LDS into registers, in 16-byte (8-byte for N == 2)
-// reads.
-template <int N>
-__device__ __forceinline__ void lds_read(const float* src, float* dst) {
-  if constexpr (N % 4 == 0) {
-#pragma unroll
-    for (int i = 0; i < N; i += 4) {
-      const float4 f = *(const float4*)(src + i);
-      dst[i] = f.x;
-      dst[i + 1] = f.y;
-      dst[i + 2] = f.z;
-      dst[i + 3] = f.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < N; i += 2) {
-      const float2 f = *(const float2*)(src + i);
-      dst[i] = f.x;
-      dst[i + 1] = f.y;
-    }
+  for (int r = wave; r < n; r += NWAVE) {
+    if (lane < CPR)
+      __builtin_amdgcn_global_load_lds((const void*)(ks + r * HD + lane * 4), (lds_ptr)(kt + r * (HD + 4)), 16,
+                                       0, 0);
   }
 }
 
@@ -278,7 +260,7 @@ __device__ __forceinline__ void norm_rope_regs(const float* xv, const float* wv,
 #pragma unroll
   for (int i = 0; i < PER; i++)
     if (lane + i * WAVE < HD) ss = fmaf(xv[i], xv[i], ss);
-  ss = wave_sum(ss);
+  ss = wave_total(ss);
   const float s = norm ? rms_scale(ss, HD, eps) : 1.0f;
 #pragma unroll
   for (int i = 0; i < PER; i++)
@@ -303,34 +285,37 @@ __device__ __forceinline__ void norm_rope_regs(const float* xv, const float* wv,
 // [c*len, min(P+1, (c+1)*len)) for the G query heads of kv head g (the K/V
 // rows are read once for the group), in tiles of kDecTile keys brought to
 // LDS by DMA, double-buffered: tile t+1 is in flight while tile t is used.
-// Per tile: scores (8 lanes per key), an online softmax per head (running
-// max m, sum l, rescale of the accumulators), P.V (thread = output dim x
-// key group). The block stores (m, l, unnormalised output) per head with
-// agent-coherent stores, then counts itself done on the kv head's counter;
-// the last block of the head reads all chunks' partials and writes
+// Wave w owns query heads w*GW .. w*GW+GW-1 and keeps their online softmax
+// state (running max m, sum l) and unnormalised output in registers; per
+// tile, lane (key kl = lane % 32, half = lane / 32) forms the score of its
+// key over half of the head dimension (the halves meet by one cross-lane
+// add), the wave updates m and l, and P.V runs with DPL output dimensions
+// per lane, the probabilities broadcast lane by lane. One block barrier per
+// tile. The block stores (m, l, output) per head with agent-coherent
+// stores, then counts itself done on the kv head's counter; the last block
+// of the head combines the chunks (one wave per head, the chunk weights in
+// lanes):
 //   att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c,  M = max_c m_c,
 // and resets the counter for the next launch. The block holding position
-// P also normalises and rotates this step's key and writes it to the
-// cache (the value row was written by the QKV projection). Each stage
-// issues all its global loads before using any (one memory round trip per
-// stage: inputs, partial stores, counter, partial loads).
-template <int HD>
-__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(AttnParams p) {
+// P also normalises and rotates this step's key (the lane whose key is P
+// reads it from LDS rather than from the tile) and writes it to the cache
+// (the value row was written by the QKV projection).
+// Two blocks fit per CU (LDS), so at most 2 waves per SIMD: the register
+// budget that lets every K read of a tile be in flight at once.
+template <int HD, int GW>
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_decode_kernel(
+    AttnParams p) {
   using L = DecLds<HD>;
-  constexpr int KP = HD / 8;  // dims per lane for scores; keys per group for P.V
-  constexpr int KG = L::KG;
   constexpr int NW = kDecThreads / WAVE;
   constexpr int PER = (HD + WAVE - 1) / WAVE;
-  constexpr int MAXV = (kDecMaxG + 1 + NW - 1) / NW;  // head vectors per wave
-  static_assert(kDecTile * 8 == kDecThreads && KG * KP == kDecTile, "tile shape");
+  constexpr int MAXV = (kDecMaxG + 1 + NW - 1) / NW;  // head vectors per wave in the staging
+  constexpr int HALF = HD / 2;                        // dims per lane in a score
+  constexpr int DPL = HD >= WAVE ? HD / WAVE : 1;     // output dims per lane
+  static_assert(kDecTile == 32 && NW * GW >= 1, "one key per lane pair");
   static_assert(kDecMaxChunks <= WAVE, "one lane per chunk in the combine");
   extern __shared__ __attribute__((aligned(16))) float lds[];
   float* qs = lds + L::qs;
   float* kn = lds + L::kn;
-  float* sc = lds + L::sc;
-  float* st = lds + L::st;
-  float* wts = lds + L::wts;
-  float* red = lds + L::red;
   int* flag = (int*)(lds + L::flag);
   float* tiles = lds + L::tiles;
 
@@ -348,7 +333,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(AttnParams p) 
 
   // Stage 1 loads: the first K/V tile, the raw q (and new k) vectors, their
   // norm weights and the rotation of position P.
-  dma_kv<HD>(kb, vb, s0, min(kDecTile, s1 - s0), tiles, tiles + kDecTile * HD);
+  dma_kv<HD>(kb, vb, s0, min(kDecTile, s1 - s0), tiles, tiles + L::KT);
   const float* cs = p.rope + (size_t)P * HD;
   const int nvec = G + (has_new ? 1 : 0);
   const int hp = lane * p.pair_stride;
@@ -379,89 +364,122 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(AttnParams p) 
       norm_rope_regs<HD>(xv[j], wv[j], (v == G ? p.kn : p.qn) != nullptr, p.eps, fr[j], fi[j],
                          p.pair_bound, p.pair_offset, p.pair_stride, v == G ? kn : qs + v * HD);
   }
-  if (tid < kDecMaxG) {
-    st[tid] = -INFINITY;
-    st[kDecMaxG + tid] = 0.0f;
-  }
+
   const float scale = sqrtf((float)HD);
-  const int d = tid % HD, kg = tid / HD, kk = tid / 8, pp = tid % 8;
-  float acc[kDecMaxG];
+  const int kl = lane % 32, half = lane / 32;
+  const bool active = wave * GW < G;  // waves past the group idle (G < 4)
+  float q[GW][HALF], m[GW], l[GW], acc[GW][DPL];
 #pragma unroll
-  for (int h = 0; h < kDecMaxG; h++) acc[h] = 0.0f;
+  for (int j = 0; j < GW; j++) {
+    m[j] = -INFINITY;
+    l[j] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DPL; d++) acc[j][d] = 0.0f;
+  }
 
   for (int t0 = s0, buf = 0; t0 < s1; t0 += kDecTile, buf ^= 1) {
     const int n = min(kDecTile, s1 - t0);
-    float* kt = tiles + buf * 2 * kDecTile * HD;
-    float* vt = kt + kDecTile * HD;
+    const float* kt = tiles + buf * (L::KT + L::VT);
+    const float* vt = kt + L::KT;
     __builtin_amdgcn_s_waitcnt(0);  // this tile (and the q/k loads) landed
     __syncthreads();                // ... for every wave; previous tile consumed
     if (t0 + kDecTile < s1) {
-      float* nk = tiles + (buf ^ 1) * 2 * kDecTile * HD;
-      dma_kv<HD>(kb, vb, t0 + kDecTile, min(kDecTile, s1 - t0 - kDecTile), nk, nk + kDecTile * HD);
+      float* nk = tiles + (buf ^ 1) * (L::KT + L::VT);
+      dma_kv<HD>(kb, vb, t0 + kDecTile, min(kDecTile, s1 - t0 - kDecTile), nk, nk + L::KT);
     }
-    if (has_new && P >= t0 && P < t0 + n) {  // row P: this step's processed key
-      for (int e = tid; e < HD; e += kDecThreads) kt[(P - t0) * HD + e] = kn[e];
-      __syncthreads();
-    }
-    float kv[KP];
-    lds_read<KP>(kt + kk * HD + pp * KP, kv);
+    if (!active) continue;
+    if (t0 == s0) {  // this wave's queries, the lane's half of each
 #pragma unroll
-    for (int h = 0; h < kDecMaxG; h++) {
-      if (h < G) {
-        float q[KP];
-        lds_read<KP>(qs + h * HD + pp * KP, q);
-        float a = 0.0f;
+      for (int j = 0; j < GW; j++) {
+        const int h = min(wave * GW + j, G - 1);
 #pragma unroll
-        for (int i = 0; i < KP; i++) a = fmaf(q[i], kv[i], a);
-        a = group_sum<8>(a);
-        if (pp == 0) sc[h * kDecTile + kk] = a / scale;
+        for (int i = 0; i < HALF; i += 4) {
+          const float4 f = *(const float4*)(qs + h * HD + half * HALF + i);
+          q[j][i] = f.x;
+          q[j][i + 1] = f.y;
+          q[j][i + 2] = f.z;
+          q[j][i + 3] = f.w;
+        }
       }
     }
-    __syncthreads();
-    for (int h = wave; h < G; h += kDecThreads / WAVE) {  // online softmax of head h
-      const float s = lane < n ? sc[h * kDecTile + lane] : -INFINITY;
-      const float mo = st[h], mn = fmaxf(mo, wave_max(s));
-      const float e = lane < n ? expf(s - mn) : 0.0f;
-      if (lane < kDecTile) sc[h * kDecTile + lane] = e;  // 0 past the tile's keys
-      const float sum = wave_sum(e);
-      if (lane == 0) {
-        const float f = expf(mo - mn);
-        st[2 * kDecMaxG + h] = f;
-        st[kDecMaxG + h] = st[kDecMaxG + h] * f + sum;
-        st[h] = mn;
+    // scores: key t0 + kl, dims [half * HALF, (half + 1) * HALF)
+    const bool valid = kl < n;
+    const bool is_new = has_new && t0 + kl == P;
+    const float* krow = (is_new ? kn : kt + kl * L::KROW) + half * HALF;
+    float s[GW];
+#pragma unroll
+    for (int j = 0; j < GW; j++) s[j] = 0.0f;
+    float4 kv[HALF / 4];  // every read of the row issued before the first product
+#pragma unroll
+    for (int i = 0; i < HALF / 4; i++) kv[i] = *(const float4*)(krow + 4 * i);
+#pragma unroll
+    for (int i = 0; i < HALF / 4; i++) {
+#pragma unroll
+      for (int j = 0; j < GW; j++) {
+        s[j] = fmaf(q[j][4 * i], kv[i].x, s[j]);
+        s[j] = fmaf(q[j][4 * i + 1], kv[i].y, s[j]);
+        s[j] = fmaf(q[j][4 * i + 2], kv[i].z, s[j]);
+        s[j] = fmaf(q[j][4 * i + 3], kv[i].w, s[j]);
       }
     }
-    __syncthreads();
-    float v[KP];
+    float pr[GW];
 #pragma unroll
-    for (int i = 0; i < KP; i++) v[i] = kg * KP + i < n ? vt[(kg * KP + i) * HD + d] : 0.0f;
+    for (int j = 0; j < GW; j++) {
+      const float full = s[j] + __shfl_xor(s[j], 32, WAVE);  // the same sum in both halves
+      const float sc = valid ? full / scale : -INFINITY;
+      const float mn = fmaxf(m[j], wave_peak(sc));
+      const float e = valid ? expf(sc - mn) : 0.0f;
+      const float f = expf(m[j] - mn);
+      l[j] = l[j] * f + wave_total(half == 0 ? e : 0.0f);
+      m[j] = mn;
 #pragma unroll
-    for (int h = 0; h < kDecMaxG; h++) {
-      if (h < G) {
-        float w[KP];
-        lds_read<KP>(sc + h * kDecTile + kg * KP, w);
-        float a = acc[h] * st[2 * kDecMaxG + h];
+      for (int d = 0; d < DPL; d++) acc[j][d] *= f;
+      pr[j] = e;
+    }
+    // P.V: dims lane * DPL .. + DPL (lanes past HD use the last dims and
+    // never store), 8 keys per batch with all their reads in flight; keys
+    // past n read row n - 1 (finite data) with probability 0.
+    const int dd = min(lane * DPL, HD - DPL);
+    for (int k0 = 0; k0 < n; k0 += 8) {
+      float v[8][DPL];
 #pragma unroll
-        for (int i = 0; i < KP; i++) a = fmaf(w[i], v[i], a);
-        acc[h] = a;
+      for (int kk = 0; kk < 8; kk++) {
+        const float* vr = vt + min(k0 + kk, n - 1) * HD + dd;
+        if constexpr (DPL == 2) {
+          const float2 f = *(const float2*)vr;
+          v[kk][0] = f.x;
+          v[kk][1] = f.y;
+        } else {
+#pragma unroll
+          for (int d = 0; d < DPL; d++) v[kk][d] = vr[d];
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < 8; kk++) {
+#pragma unroll
+        for (int j = 0; j < GW; j++) {
+          const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[j]), k0 + kk));
+#pragma unroll
+          for (int d = 0; d < DPL; d++) acc[j][d] = fmaf(pk, v[kk][d], acc[j][d]);
+        }
       }
     }
   }
-  __syncthreads();  // last tile consumed (red overlaps the tiles)
+  if (active) {
 #pragma unroll
-  for (int h = 0; h < kDecMaxG; h++)
-    if (h < G) red[(kg * kDecMaxG + h) * HD + d] = acc[h];
-  __syncthreads();
-  for (int o = tid; o < G * HD; o += kDecThreads) {
-    const int h = o / HD, dd = o % HD;
-    float a = 0.0f;
+    for (int j = 0; j < GW; j++) {
+      const int h = wave * GW + j;
+      if (h < G) {
+        float* part = p.partial + ((size_t)(g * G + h) * p.splits + c) * (HD + 2);
+        if (lane * DPL < HD) {
 #pragma unroll
-    for (int k = 0; k < KG; k++) a += red[(k * kDecMaxG + h) * HD + dd];
-    float* part = p.partial + ((size_t)(g * G + h) * p.splits + c) * (HD + 2);
-    cstore(part + 2 + dd, a);
-    if (dd == 0) {
-      cstore(part, st[h]);
-      cstore(part + 1, st[kDecMaxG + h]);
+          for (int d = 0; d < DPL; d++) cstore(part + 2 + lane * DPL + d, acc[j][d]);
+        }
+        if (lane == 0) {
+          cstore(part, m[j]);
+          cstore(part + 1, l[j]);
+        }
+      }
     }
   }
   if (has_new) {  // cache row P of kv head g, read by later steps
@@ -478,57 +496,70 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(AttnParams p) 
   __syncthreads();
   if (!flag[0]) return;
 
-  // Last block of kv head g: combine the nch chunks of its G heads, two
-  // outputs per thread at a time (one round for G * HD <= 512), the chunk
-  // partials in groups of 32 loaded before any is used.
-  float m[MAXV], l[MAXV];
+  // Last block of kv head g: wave w combines heads w*GW.., lane c holding
+  // chunk c's weight. Every chunk partial of the lane's output dims (of all
+  // the wave's heads when they fit in registers) is loaded before the first
+  // is used, 8 chunks per batch up to nch, then summed in chunk order.
+  constexpr int CB = 8;                          // chunks per load batch
+  constexpr int HB = GW * DPL <= 2 ? GW : 1;     // heads loaded together
+  const int dd = min(lane * DPL, HD - DPL);
+  const bool ok = lane < nch;
 #pragma unroll
-  for (int j = 0; j < MAXV; j++) {
-    const int h = wave + j * NW;
-    const float* pb = p.partial + (size_t)(g * G + h) * p.splits * (HD + 2) + (size_t)lane * (HD + 2);
-    const bool ok = h < G && lane < nch;
-    m[j] = ok ? cload(pb) : -INFINITY;
-    l[j] = ok ? cload(pb + 1) : 0.0f;
-  }
-  constexpr int CG = kDecCombineGroup;
-  for (int o0 = 0; o0 < G * HD; o0 += 2 * kDecThreads) {
-    float a[2] = {0.0f, 0.0f};
-    for (int c0 = 0; c0 < nch; c0 += CG) {
-      float x[2][CG];
+  for (int j0 = 0; j0 < GW; j0 += HB) {
+    if (wave * GW + j0 >= G) break;
+    float mc[HB], lc[HB], x[HB][kDecMaxChunks][DPL];
 #pragma unroll
-      for (int r = 0; r < 2; r++) {
-        const int o = min(o0 + tid + r * kDecThreads, G * HD - 1), h = o / HD, dd = o % HD;
-        const float* pb = p.partial + (size_t)(g * G + h) * p.splits * (HD + 2) + 2 + dd;
+    for (int j = 0; j < HB; j++) {
+      const float* base = p.partial + (size_t)(g * G + min(wave * GW + j0 + j, G - 1)) * p.splits * (HD + 2);
+      mc[j] = ok ? cload(base + (size_t)lane * (HD + 2)) : -INFINITY;
+      lc[j] = ok ? cload(base + (size_t)lane * (HD + 2) + 1) : 0.0f;
+    }
 #pragma unroll
-        for (int i = 0; i < CG; i++) x[r][i] = cload(pb + (size_t)min(c0 + i, nch - 1) * (HD + 2));
-      }
-      if (o0 == 0 && c0 == 0) {
+    for (int j = 0; j < HB; j++) {
+      const float* base = p.partial + (size_t)(g * G + min(wave * GW + j0 + j, G - 1)) * p.splits * (HD + 2);
 #pragma unroll
-        for (int j = 0; j < MAXV; j++) {
-          const int h = wave + j * NW;
-          if (h < G) {
-            const float M = wave_max(m[j]);
-            const float w = lane < nch ? expf(m[j] - M) : 0.0f;
-            if (lane < kDecMaxChunks) wts[h * (kDecMaxChunks + 1) + lane] = w;
-            const float wl = wave_sum(w * l[j]);
-            if (lane == 0) wts[h * (kDecMaxChunks + 1) + kDecMaxChunks] = wl;
+      for (int b = 0; b < kDecMaxChunks / CB; b++) {
+        if (b * CB < nch) {
+#pragma unroll
+          for (int i = 0; i < CB; i++) {
+            const float* src = base + (size_t)min(b * CB + i, nch - 1) * (HD + 2) + 2 + dd;
+            if constexpr (DPL == 2) {
+              const float2 f = cload2(src);  // 8-byte aligned: HD + 2 and dd are even
+              x[j][b * CB + i][0] = f.x;
+              x[j][b * CB + i][1] = f.y;
+            } else {
+#pragma unroll
+              for (int d = 0; d < DPL; d++) x[j][b * CB + i][d] = cload(src + d);
+            }
           }
         }
-        __syncthreads();
-      }
-#pragma unroll
-      for (int r = 0; r < 2; r++) {
-        const int h = min(o0 + tid + r * kDecThreads, G * HD - 1) / HD;
-        const float* w = wts + h * (kDecMaxChunks + 1) + c0;
-#pragma unroll
-        for (int i = 0; i < CG; i++)
-          if (c0 + i < nch) a[r] = fmaf(w[i], x[r][i], a[r]);
       }
     }
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
-      const int o = o0 + tid + r * kDecThreads, h = o / HD, dd = o % HD;
-      if (o < G * HD) p.out[(size_t)(g * G + h) * HD + dd] = a[r] / wts[h * (kDecMaxChunks + 1) + kDecMaxChunks];
+    for (int j = 0; j < HB; j++) {
+      const int h = wave * GW + j0 + j;
+      if (h >= G) break;
+      const float M = wave_peak(mc[j]);
+      const float w = ok ? expf(mc[j] - M) : 0.0f;
+      const float W = wave_total(w * lc[j]);
+      float o[DPL];
+#pragma unroll
+      for (int d = 0; d < DPL; d++) o[d] = 0.0f;
+#pragma unroll
+      for (int b = 0; b < kDecMaxChunks / CB; b++) {
+        if (b * CB < nch) {
+#pragma unroll
+          for (int i = 0; i < CB; i++) {
+            const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b * CB + i));  // 0 past nch
+#pragma unroll
+            for (int d = 0; d < DPL; d++) o[d] = fmaf(wc, x[j][b * CB + i][d], o[d]);
+          }
+        }
+      }
+      if (lane * DPL < HD) {
+#pragma unroll
+        for (int d = 0; d < DPL; d++) p.out[(size_t)(g * G + h) * HD + lane * DPL + d] = o[d] / W;
+      }
     }
   }
   if (tid == 0) __hip_atomic_store(p.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -550,14 +581,19 @@ void attention_init() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 64 * (int)sizeof(float)));
   HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_mfma_kernel<128>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 128 * (int)sizeof(float)));
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(DecLds<16>::total * sizeof(float))));
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<32>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(DecLds<32>::total * sizeof(float))));
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(DecLds<64>::total * sizeof(float))));
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(DecLds<128>::total * sizeof(float))));
+#define DECODE_ATTR(HD, GW)                                                                     \
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<HD, GW>,                        \
+                                hipFuncAttributeMaxDynamicSharedMemorySize,                     \
+                                (int)(DecLds<HD>::total * sizeof(float))));
+  DECODE_ATTR(16, 1)
+  DECODE_ATTR(16, 2)
+  DECODE_ATTR(32, 1)
+  DECODE_ATTR(32, 2)
+  DECODE_ATTR(64, 1)
+  DECODE_ATTR(64, 2)
+  DECODE_ATTR(128, 1)
+  DECODE_ATTR(128, 2)
+#undef DECODE_ATTR
 }
 
 size_t attention_decode_lds_bytes(int hd) {
@@ -600,10 +636,12 @@ void attention_decode(const AttnParams& p, hipStream_t s) {
     ST_DIE("decode attention: RoPE pairs must fit one per lane within the head");
   const dim3 grid(p.splits, p.kv_heads);
   const size_t shm = attention_decode_lds_bytes(p.hd);
+  const bool two = G > kDecThreads / WAVE;  // two query heads per wave
   switch (p.hd) {
-#define DECODE_CASE(HD)                                                              \
-  case HD:                                                                           \
-    hipLaunchKernelGGL(attn_decode_kernel<HD>, grid, dim3(kDecThreads), shm, s, p); \
+#define DECODE_CASE(HD)                                                                        \
+  case HD:                                                                                     \
+    if (two) hipLaunchKernelGGL((attn_decode_kernel<HD, 2>), grid, dim3(kDecThreads), shm, s, p); \
+    else hipLaunchKernelGGL((attn_decode_kernel<HD, 1>), grid, dim3(kDecThreads), shm, s, p);     \
     break;
     DECODE_CASE(16)
     DECODE_CASE(32)

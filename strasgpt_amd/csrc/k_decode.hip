@@ -198,25 +198,6 @@ __device__ __forceinline__ int job_batches(const Job& j) {
   return (j.items + per - 1) / per;
 }
 
-// Sum over the 64 lanes of a wave (all lanes active), the same in every
-// lane: sums within each row of 16 lanes by DPP moves (no LDS traffic),
-// then the four row sums read as scalars.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float wave_total(float v) {
-  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_mov<0x141>(v);  // row_half_mirror
-  v += dpp_mov<0x140>(v);  // row_mirror
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return (r0 + r1) + (r2 + r3);
-}
 
 // Position in a wave's item sequence: item n is iteration i (of it) of the
 // wave's slice sl (block slice wave + 8 sl).
