@@ -165,6 +165,159 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   }
 }
 
+// Second form: one row per wavefront at a time and a flat stream of
+// (row, step) items per wavefront, PD steps in flight in a ring of
+// registers whose slots are fixed by unrolling (no register copies, so no
+// wait is forced before a slot is consumed), running across row
+// boundaries. The input row (and the RMSNorm weights) are loaded into
+// registers before any weight load, so staging them waits for those loads
+// alone while the first PD weight loads are in flight; the RMSNorm sum of
+// squares is formed from the registers in the same partition and order as
+// stage_row. Per row the products are accumulated in step order as in
+// gemv_kernel; the row sum is a DPP reduction. Used when the staged row fits
+// kV2Lds bytes and XF float4 per thread.
+constexpr int kV2Lds = 64 * 1024;
+
+template <int EPI>
+__device__ __forceinline__ void gemv_store(const GemvParams& p, int n, float a, float a2) {
+  if (EPI == GEMV_STORE) {
+    p.y[n] = a;
+  } else if (EPI == GEMV_RESIDUAL) {
+    p.y[n] += a;
+  } else if (EPI == GEMV_SWIGLU) {
+    p.y[n] = silu_mul(a, a2);
+  } else {  // GEMV_QKV
+    if (n < p.q_dim) {
+      p.q[n] = a;
+    } else if (n < p.q_dim + p.kv_dim) {
+      p.kraw[n - p.q_dim] = a;
+    } else {
+      const int j = n - p.q_dim - p.kv_dim;
+      const int head = j / p.head_dim, h = j % p.head_dim;
+      p.vcache[((size_t)head * p.ctx + *p.pos) * p.head_dim + h] = a;
+    }
+  }
+}
+
+template <int EPI, bool NORM, int XF, bool EXACT, int kPD>
+__global__ __launch_bounds__(kThreads) void gemv2_kernel(GemvParams p) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [S * kStep], zero past K
+  __shared__ float red[kWaves];
+  constexpr bool DUAL = EPI == GEMV_SWIGLU;
+  const int lane = threadIdx.x % WAVE;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);  // wave-uniform from here
+  const int K = p.K, N = p.N;
+  const int S = (K + kStep - 1) / kStep;  // steps per row
+  const int groups = (N + kWaves - 1) / kWaves;
+  const int G = gridDim.x, per = (groups + G - 1) / G;
+  const int v = (G % kXcds == 0) ? (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds : blockIdx.x;
+  const int g0 = v * per;
+  // rows of this wavefront: (g0 + i) * 4 + wave, i < nrows
+  const int glast = N - 1 - wave >= 0 ? (N - 1 - wave) / kWaves : -1;  // last group with a row here
+  const int nrows = max(0, min(min(groups, g0 + per), glast + 1) - g0);
+  const int T = nrows * S;
+
+  // input row elements tid*4 + i*1024 (and their norm weights), clamped
+  float4 xv[XF];
+  uint2 nv[NORM ? XF : 1];
+#pragma unroll
+  for (int i = 0; i < XF; i++) {
+    const int k = min((int)threadIdx.x * 4 + i * kThreads * 4, K - 4);
+    xv[i] = *(const float4*)(p.x + k);
+    if (NORM) nv[i] = *(const uint2*)(p.norm_w + k);
+  }
+
+  // The ring. The refill cursor (rrow, rstep) walks the items in order.
+  // Refills past the last item are issued all the same (so that every
+  // consumption waits for an exact count of newer loads) but read the
+  // first 1 KiB of the input row, which is in cache, instead of weights.
+  uint4 w[kPD], w2[DUAL ? kPD : 1];
+  const int lk = lane * 8;
+  int rrow = 0, rstep = 0;
+  auto load = [&](uint4& a, uint4& b) {
+    const bool past = rrow >= nrows;  // wave-uniform
+    const size_t row = (size_t)min((g0 + rrow) * kWaves + wave, N - 1);
+    const int k = EXACT ? rstep * kStep + lk : min(rstep * kStep + lk, K - 8);
+    const uint16_t* wa = past ? (const uint16_t*)p.x + lk : p.w + row * K + k;
+    a = load_nt_u4(wa);
+    if (DUAL) b = load_nt_u4(past ? wa : p.w2 + row * K + k);
+    if (++rstep == S) {
+      rstep = 0;
+      rrow++;
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kPD; j++) load(w[j], w2[DUAL ? j : 0]);
+  __builtin_amdgcn_sched_barrier(0);  // the weight loads go out before the staging waits
+
+  float s = 1.0f;
+  if (NORM) {  // same partition and order as stage_row
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XF; i++) {
+      if ((int)threadIdx.x * 4 + i * kThreads * 4 < K) {
+        ss = fmaf(xv[i].x, xv[i].x, ss);
+        ss = fmaf(xv[i].y, xv[i].y, ss);
+        ss = fmaf(xv[i].z, xv[i].z, ss);
+        ss = fmaf(xv[i].w, xv[i].w, ss);
+      }
+    }
+    s = rms_scale(block_sum<kThreads>(ss, red), K, p.eps);
+  }
+#pragma unroll
+  for (int i = 0; i < XF; i++) {
+    const int k = (int)threadIdx.x * 4 + i * kThreads * 4;
+    if (k < K) {
+      float4 o = xv[i];
+      if (NORM) {
+        o.x = (o.x * s) * bf16_to_f32((uint16_t)(nv[i].x & 0xffffu));
+        o.y = (o.y * s) * bf16_to_f32((uint16_t)(nv[i].x >> 16));
+        o.z = (o.z * s) * bf16_to_f32((uint16_t)(nv[i].y & 0xffffu));
+        o.w = (o.w * s) * bf16_to_f32((uint16_t)(nv[i].y >> 16));
+      }
+      *(float4*)(xs + k) = o;
+    }
+  }
+  for (int k = K + threadIdx.x; k < S * kStep; k += kThreads) xs[k] = 0.0f;
+  __syncthreads();
+
+  float acc = 0.0f, acc2 = 0.0f;
+  int step = 0, rowi = 0;
+  for (int t0 = 0; t0 < T; t0 += kPD) {
+#pragma unroll
+    for (int j = 0; j < kPD; j++) {
+      if (t0 + j < T) {
+        const int k = step * kStep + lk;
+        uint4 a = w[j], b = w2[DUAL ? j : 0];
+        if (!EXACT) {  // past K: zero weights (x is zero there too)
+          const bool in = k < K;
+          a.x = in ? a.x : 0u;
+          a.y = in ? a.y : 0u;
+          a.z = in ? a.z : 0u;
+          a.w = in ? a.w : 0u;
+          b.x = in ? b.x : 0u;
+          b.y = in ? b.y : 0u;
+          b.z = in ? b.z : 0u;
+          b.w = in ? b.w : 0u;
+        }
+        const float4 xa = *(const float4*)(xs + k);
+        const float4 xb = *(const float4*)(xs + k + 4);
+        acc = dot8(a, xa, xb, acc);
+        if (DUAL) acc2 = dot8(b, xa, xb, acc2);
+        if (++step == S) {
+          const float r1 = wave_total(acc), r2 = DUAL ? wave_total(acc2) : 0.0f;
+          if (lane == 0) gemv_store<EPI>(p, (g0 + rowi) * kWaves + wave, r1, r2);
+          acc = acc2 = 0.0f;
+          step = 0;
+          rowi++;
+        }
+      }
+      load(w[j], w2[DUAL ? j : 0]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load left in flight at exit
+}
+
 // Blocks: at most `cap`, the same number of row groups for each block, and
 // a multiple of the XCD count when there are enough groups.
 int balanced_blocks(int groups, int cap) {
@@ -172,6 +325,48 @@ int balanced_blocks(int groups, int cap) {
   int blocks = (groups + per - 1) / per;
   if (blocks >= kXcds * 4) blocks = (blocks + kXcds - 1) / kXcds * kXcds;
   return blocks;
+}
+
+// PD: weight steps in flight per wavefront (8 KiB; the SwiGLU pair reads
+// two matrices per step, so half as many steps).
+template <int EPI, int PD = EPI == GEMV_SWIGLU ? 4 : 8>
+bool launch_v2(const GemvParams& p, hipStream_t s, int cap) {
+  const int S = (p.K + kStep - 1) / kStep;
+  const size_t shm = (size_t)S * kStep * sizeof(float);
+  if (shm > kV2Lds || p.K < 256 || p.K > 16 * kThreads * 4) return false;  // K >= 256: 1 KiB of x
+  const int groups = (p.N + kWaves - 1) / kWaves;
+  const int blocks = balanced_blocks(groups, cap);
+  static bool attr = false;
+  if (!attr) {
+#define V2_ATTR(NORM, XF, EX)                                                                   \
+  HIP_CHECK(hipFuncSetAttribute((const void*)gemv2_kernel<EPI, NORM, XF, EX, PD>,               \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kV2Lds));
+    V2_ATTR(true, 4, true)
+    V2_ATTR(false, 4, true)
+    V2_ATTR(true, 16, true)
+    V2_ATTR(false, 16, true)
+    V2_ATTR(true, 4, false)
+    V2_ATTR(false, 4, false)
+    V2_ATTR(true, 16, false)
+    V2_ATTR(false, 16, false)
+#undef V2_ATTR
+    attr = true;
+  }
+  const bool small = p.K <= 4 * kThreads * 4, exact = p.K % kStep == 0;
+#define V2_GO(NORM, XF, EX) \
+  hipLaunchKernelGGL((gemv2_kernel<EPI, NORM, XF, EX, PD>), dim3(blocks), dim3(kThreads), shm, s, p)
+#define V2_GO2(NORM, XF) \
+  if (exact) V2_GO(NORM, XF, true); else V2_GO(NORM, XF, false);
+  if (p.norm_w) {
+    if (small) { V2_GO2(true, 4) }
+    else { V2_GO2(true, 16) }
+  } else {
+    if (small) { V2_GO2(false, 4) }
+    else { V2_GO2(false, 16) }
+  }
+#undef V2_GO2
+#undef V2_GO
+  return true;
 }
 
 template <int R, int U, int EPI>
@@ -203,10 +398,20 @@ void check(const GemvParams& p, int epi) {
 void gemv(const GemvParams& p, int epi, hipStream_t s) {
   check(p, epi);
   switch (epi) {
-    case GEMV_STORE: launch<1, 2, GEMV_STORE>(p, s, 2048); break;
-    case GEMV_RESIDUAL: launch<1, 4, GEMV_RESIDUAL>(p, s, 4096); break;
-    case GEMV_QKV: launch<1, 2, GEMV_QKV>(p, s, 2048); break;
-    case GEMV_SWIGLU: launch<1, 2, GEMV_SWIGLU>(p, s, 2048); break;
+    // Flat-stream form where the row fits (steps in flight, block cap from
+    // sweeps of the decode shapes on MI355X), else the chunked form.
+    case GEMV_STORE:
+      if (!launch_v2<GEMV_STORE, 8>(p, s, 2048)) launch<1, 2, GEMV_STORE>(p, s, 2048);
+      break;
+    case GEMV_RESIDUAL:
+      if (!launch_v2<GEMV_RESIDUAL, 8>(p, s, 256)) launch<1, 4, GEMV_RESIDUAL>(p, s, 4096);
+      break;
+    case GEMV_QKV:
+      if (!launch_v2<GEMV_QKV, 4>(p, s, 1024)) launch<1, 2, GEMV_QKV>(p, s, 2048);
+      break;
+    case GEMV_SWIGLU:
+      if (!launch_v2<GEMV_SWIGLU, 2>(p, s, 2048)) launch<1, 2, GEMV_SWIGLU>(p, s, 2048);
+      break;
     default: ST_DIE("unknown GEMV epilogue");
   }
   HIP_CHECK(hipGetLastError());
@@ -214,7 +419,7 @@ void gemv(const GemvParams& p, int epi, hipStream_t s) {
 
 // Launch-shape variants for the micro-benchmark (STORE epilogue, or
 // SwiGLU when `dual`): rows per wavefront R, steps per chunk U, block cap.
-int gemv_variant_count() { return 12; }
+int gemv_variant_count() { return 18; }
 
 void gemv_variant(const GemvParams& p, bool dual, int v, hipStream_t s) {
   check(p, dual ? GEMV_SWIGLU : GEMV_STORE);
@@ -235,6 +440,28 @@ void gemv_variant(const GemvParams& p, bool dual, int v, hipStream_t s) {
     case 9: V(2, 2, 512)
     case 10: V(4, 4, 1024)
     case 11: V(1, 4, 4096)
+    case 12:  // the flat-stream form, block caps 2048 .. 256 (falls back to variant 1 when the row does not fit)
+    case 13:
+    case 14:
+    case 15: {
+      const int cap = 2048 >> (v - 12);
+      if (dual) {
+        if (!launch_v2<GEMV_SWIGLU>(p, s, cap)) launch<1, 4, GEMV_SWIGLU>(p, s, 2048);
+      } else {
+        if (!launch_v2<GEMV_STORE>(p, s, cap)) launch<1, 4, GEMV_STORE>(p, s, 2048);
+      }
+      break;
+    }
+    case 16:  // the flat-stream form, 2 (SwiGLU) or 4 steps in flight, caps 2048 and 1024
+    case 17: {
+      const int cap = 2048 >> (v - 16);
+      if (dual) {
+        if (!launch_v2<GEMV_SWIGLU, 2>(p, s, cap)) launch<1, 4, GEMV_SWIGLU>(p, s, 2048);
+      } else {
+        if (!launch_v2<GEMV_STORE, 4>(p, s, cap)) launch<1, 4, GEMV_STORE>(p, s, 2048);
+      }
+      break;
+    }
     default: ST_DIE("unknown GEMV variant");
   }
 #undef V
