@@ -287,6 +287,107 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, c
   }
 }
 
+// Decode router (one token): block b computes the logits of experts
+// 4b .. 4b+3, one per wavefront, each from the RMSNorm of the residual row
+// formed in the block (the row and the norm weights are loaded before the
+// router rows, which are all in flight before the first is used); block 0
+// also writes the normalised row for the expert kernels. Logit e is the
+// dot product in the lane order of route_kernel, summed across the wave by
+// DPP.
+constexpr int kRlXF = 8;   // float4 of the row per thread: d <= 8192
+constexpr int kRlLd = 16;  // 8-value router chunks per lane: d <= 8192
+
+__global__ __launch_bounds__(256) void route_logits_kernel(const float* x, const uint16_t* nw, float eps,
+                                                           const uint16_t* router, int E, int d, float* logits,
+                                                           float* xn) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [d]
+  __shared__ float red[4];
+  const int lane = threadIdx.x % WAVE, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int e = blockIdx.x * 4 + wave;
+  const int chunks = d / 8;
+  float4 xv[kRlXF];
+  uint2 nv[kRlXF];
+#pragma unroll
+  for (int i = 0; i < kRlXF; i++) {
+    const int k = min((int)threadIdx.x * 4 + i * 1024, d - 4);
+    xv[i] = *(const float4*)(x + k);
+    nv[i] = *(const uint2*)(nw + k);
+  }
+  uint4 w[kRlLd];
+  const uint16_t* wr = router + (size_t)min(e, E - 1) * d;
+#pragma unroll
+  for (int u = 0; u < kRlLd; u++) w[u] = load_nt_u4(wr + min(u * WAVE + lane, chunks - 1) * 8);
+  __builtin_amdgcn_sched_barrier(0);  // the router loads go out before the staging waits
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kRlXF; i++) {
+    if ((int)threadIdx.x * 4 + i * 1024 < d) {
+      ss = fmaf(xv[i].x, xv[i].x, ss);
+      ss = fmaf(xv[i].y, xv[i].y, ss);
+      ss = fmaf(xv[i].z, xv[i].z, ss);
+      ss = fmaf(xv[i].w, xv[i].w, ss);
+    }
+  }
+  const float s = rms_scale(block_sum<256>(ss, red), d, eps);
+#pragma unroll
+  for (int i = 0; i < kRlXF; i++) {
+    const int k = (int)threadIdx.x * 4 + i * 1024;
+    if (k < d) {
+      float4 o;
+      o.x = (xv[i].x * s) * bf16_to_f32((uint16_t)(nv[i].x & 0xffffu));
+      o.y = (xv[i].y * s) * bf16_to_f32((uint16_t)(nv[i].x >> 16));
+      o.z = (xv[i].z * s) * bf16_to_f32((uint16_t)(nv[i].y & 0xffffu));
+      o.w = (xv[i].w * s) * bf16_to_f32((uint16_t)(nv[i].y >> 16));
+      *(float4*)(xs + k) = o;
+      if (blockIdx.x == 0) *(float4*)(xn + k) = o;
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kRlLd; u++) {
+    const int c = u * WAVE + lane;
+    if (c < chunks) acc = dot8(w[u], *(const float4*)(xs + c * 8), *(const float4*)(xs + c * 8 + 4), acc);
+  }
+  acc = wave_total(acc);
+  if (lane == 0 && e < E) logits[e] = acc;
+}
+
+// Top-k of one token's router logits (E <= 64, one per lane) with the
+// semantics of route_kernel's selection: each round takes the largest
+// untaken logit, ties to the lowest expert id, NaN never selected unless it
+// is the first untaken expert (a sequential scan starting from it would
+// keep it); -inf only when nothing larger is left (the first untaken).
+// Lane j < k ends with the j-th pick and its weight e^(l_j - l_0) / sum,
+// the sum over the picks in pick order. Whole wave, uniform control flow.
+__device__ __forceinline__ void topk_lanes(const float* lg, int E, int k, int& mine, float& wmine) {
+  const int lane = threadIdx.x % WAVE;
+  const float v = lane < E ? lg[lane] : -INFINITY;
+  bool taken = false;
+  int top = 0;
+  mine = 0;
+  for (int j = 0; j < k; j++) {
+    const int first = __ffsll((unsigned long long)__ballot(lane < E && !taken)) - 1;  // k <= E: one is left
+    const bool cand = lane < E && !taken && v > -INFINITY;
+    int pick = first;
+    if (__ballot(cand)) {
+      const float M = wave_peak(cand ? v : -INFINITY);
+      pick = __ffsll((unsigned long long)__ballot(cand && v == M)) - 1;
+    }
+    const float fv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), first));
+    if (fv != fv) pick = first;
+    if (j == 0) top = pick;
+    if (lane == j) mine = pick;
+    if (lane == pick) taken = true;
+  }
+  const float lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
+  const float lm = __shfl(v, mine, WAVE);
+  const float ev = lane < k ? expf(lm - lt) : 0.0f;
+  float sum = 0.0f;
+  for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
+  wmine = ev / sum;
+}
+
 // act[s][h] = silu(gate_e[h] . x_s) * (up_e[h] . x_s), slot s = (token, j):
 // block (row group, slot); each half-wave takes kGuRows rows of both
 // matrices. Order: expert id and activation loads, then every weight load
@@ -323,8 +424,16 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(MoeGemvParams p) {
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [K] swizzled, then 32 zeros
   const int slot = blockIdx.y, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const int half = wave * 2 + lane / 32, hl = lane % 32;
-  const int e = p.expert[slot];
   dma_rows<kThreads, kGuDma, LOOP>(p.x + (size_t)(slot / p.topk) * p.K, p.K, xs);
+  int e;
+  if (p.logits) {  // decode: this slot's expert from the router logits
+    int mine;
+    float wm;
+    topk_lanes(p.logits + (size_t)(slot / p.topk) * p.E, p.E, p.topk, mine, wm);
+    e = __builtin_amdgcn_readlane(mine, slot % p.topk);
+  } else {
+    e = p.expert[slot];
+  }
   const int nb = p.K / 32;
   const int r0 = (blockIdx.x * kHalves + half) * kGuRows;
   float acc[2 * kGuRows];  // gate rows, then up rows
@@ -391,10 +500,25 @@ __global__ __launch_bounds__(kThreads) void down_kernel(MoeGemvParams p) {
   const int k = p.topk;
   const int t = blockIdx.y, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const int half = wave * 2 + lane / 32, hl = lane % 32;
-  int e[KMAX];
-#pragma unroll
-  for (int j = 0; j < KMAX; j++) e[j] = p.expert[t * k + min(j, k - 1)];
   dma_rows<kThreads, kDownDma, LOOP>(p.x + (size_t)t * k * p.K, k * p.K, as);
+  int e[KMAX];
+  float wt[KMAX];
+  if (p.logits) {  // decode: the token's experts and weights from the router logits
+    int mine;
+    float wm;
+    topk_lanes(p.logits + (size_t)t * p.E, p.E, k, mine, wm);
+#pragma unroll
+    for (int j = 0; j < KMAX; j++) {
+      e[j] = __builtin_amdgcn_readlane(mine, min(j, k - 1));
+      wt[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wm), min(j, k - 1)));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KMAX; j++) {
+      e[j] = p.expert[t * k + min(j, k - 1)];
+      wt[j] = p.weight[t * k + min(j, k - 1)];
+    }
+  }
   const int nb = p.K / 32;
   const int n0 = (blockIdx.x * kHalves + half) * kDownRows;
   float dot[kDownRows * KMAX];
@@ -419,7 +543,7 @@ __global__ __launch_bounds__(kThreads) void down_kernel(MoeGemvParams p) {
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < KMAX; j++)
-      if (j < k) acc = fmaf(p.weight[t * k + j], half_sum(dot[r * KMAX + j]), acc);
+      if (j < k) acc = fmaf(wt[j], half_sum(dot[r * KMAX + j]), acc);
     const int n = n0 + r;
     if (hl == 0 && n < p.N) p.y[(size_t)t * p.N + n] += acc;
   }
@@ -657,6 +781,23 @@ void moe_route(const float* xn, int T, const uint16_t* router, int E, int d, int
   const size_t shm = (size_t)(d + E) * sizeof(float);
   set_lds(route_kernel, shm);
   hipLaunchKernelGGL(route_kernel, dim3(T), dim3(kRouteThreads), shm, s, xn, router, E, d, k, sel, sel_w);
+  HIP_CHECK(hipGetLastError());
+}
+
+bool moe_route_logits_supported(int E, int topk, int d) {
+  return E >= 1 && E <= WAVE && topk >= 1 && topk <= E && topk <= 8 && d % 8 == 0 && d >= 8 &&
+         d <= kRlXF * 1024 && d <= kRlLd * WAVE * 8;
+}
+
+void moe_route_logits(const float* x, const uint16_t* norm_w, float eps, const uint16_t* router, int E, int d,
+                      float* logits, float* xn, hipStream_t s) {
+  if (!moe_route_logits_supported(E, 1, d)) ST_DIE("decode MoE router shape out of range");
+  if (((uintptr_t)router | (uintptr_t)x | (uintptr_t)xn) % 16 || (uintptr_t)norm_w % 8)
+    ST_DIE("decode MoE router operands must be aligned");
+  const size_t shm = (size_t)d * sizeof(float);
+  set_lds(route_logits_kernel, shm);
+  hipLaunchKernelGGL(route_logits_kernel, dim3((E + 3) / 4), dim3(256), shm, s, x, norm_w, eps, router, E, d,
+                     logits, xn);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -50,7 +50,16 @@ struct MoeGemvParams {
   const float* weight;     // [tokens][topk] routing weights (down-proj only)
   int tokens, topk, N, K;
   float* y;                // SWIGLU: [tokens*topk][N]; DOWN: y[t][n] += routed sum
+  // Decode (one token, E <= 64): router logits [E] instead of expert /
+  // weight; each block selects the top-k itself.
+  const float* logits;
+  int E;
 };
+// Decode router: logits[e] = W_r[e] . RMSNorm(x) for one token, and the
+// normalised row into xn (read by the expert kernels). E <= 64, d <= 8192.
+void moe_route_logits(const float* x, const uint16_t* norm_w, float eps, const uint16_t* router, int E, int d,
+                      float* logits, float* xn, hipStream_t s);
+bool moe_route_logits_supported(int E, int topk, int d);
 void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s);
 void moe_gemv_down(const MoeGemvParams& p, hipStream_t s);
 // Prefill MoE: slots grouped by expert, then grouped MXFP4 GEMMs.

@@ -171,6 +171,7 @@ struct transformer_device {
   int* moe_sel = nullptr;
   float* moe_w = nullptr;
   float* moe_act = nullptr;
+  float* moe_logits = nullptr;  // [E] router logits of a decode step
   int* moe_offs = nullptr;   // [E + 1] grouped prefill: slot ranges per expert
   int* moe_order = nullptr;  // [T * topk] slots sorted by expert
   float* moe_out = nullptr;  // [T * topk][d] per-slot down projections
@@ -346,13 +347,22 @@ constexpr int kMoeGroupedMinTokens = 8;
 void ffn_moe(Dev* D, int l, int T) {
   hipStream_t s = D->stream;
   const double d = D->d, H = D->H, k = D->topk;
-  {
-    Prof pr(D, K_ELEM, 2.0 * T * d * 4, 0);
-    sg::rmsnorm_rows(D->x, W16(D, W_FFN_NORM, l), D->xn, T, D->d, D->eps, s);
-  }
-  {
-    Prof pr(D, T == 1 ? K_ROUTE : K_ROUTE_PRE, (double)D->E * d * 2, 2.0 * T * D->E * d);
-    sg::moe_route(D->xn, T, W16(D, W_ROUTER, l), D->E, D->d, D->topk, D->moe_sel, D->moe_w, s);
+  const bool fused = T == 1 && sg::moe_route_logits_supported(D->E, D->topk, D->d);
+  if (fused) {
+    // decode: RMSNorm + router logits in one launch; the expert kernels
+    // select the top-k from the logits themselves
+    Prof pr(D, K_ROUTE, (double)D->E * d * 2, 2.0 * D->E * d);
+    sg::moe_route_logits(D->x, W16(D, W_FFN_NORM, l), D->eps, W16(D, W_ROUTER, l), D->E, D->d, D->moe_logits,
+                         D->xn, s);
+  } else {
+    {
+      Prof pr(D, K_ELEM, 2.0 * T * d * 4, 0);
+      sg::rmsnorm_rows(D->x, W16(D, W_FFN_NORM, l), D->xn, T, D->d, D->eps, s);
+    }
+    {
+      Prof pr(D, T == 1 ? K_ROUTE : K_ROUTE_PRE, (double)D->E * d * 2, 2.0 * T * D->E * d);
+      sg::moe_route(D->xn, T, W16(D, W_ROUTER, l), D->E, D->d, D->topk, D->moe_sel, D->moe_w, s);
+    }
   }
   if (T >= kMoeGroupedMinTokens) {
     // prefill: slots grouped by expert, each expert's weights read once per
@@ -406,6 +416,8 @@ void ffn_moe(Dev* D, int l, int T) {
   g.scales2 = W8(D, W_US, l);
   g.x = D->xn;
   g.expert = D->moe_sel;
+  g.logits = fused ? D->moe_logits : nullptr;
+  g.E = D->E;
   g.tokens = T;
   g.topk = D->topk;
   g.N = D->H;
@@ -421,6 +433,8 @@ void ffn_moe(Dev* D, int l, int T) {
   dn.x = D->moe_act;
   dn.expert = D->moe_sel;
   dn.weight = D->moe_w;
+  dn.logits = fused ? D->moe_logits : nullptr;
+  dn.E = D->E;
   dn.tokens = T;
   dn.topk = D->topk;
   dn.N = D->d;
@@ -1176,6 +1190,7 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
     D->moe_sel = dalloc<int>(T * D->topk);
     D->moe_w = dalloc<float>(T * D->topk);
     D->moe_act = dalloc<float>(T * D->topk * H);
+    D->moe_logits = dalloc<float>(D->E);
     D->moe_offs = dalloc<int>(D->E + 1);
     D->moe_order = dalloc<int>(T * D->topk);
     D->moe_out = dalloc<float>(T * D->topk * d);
@@ -1213,7 +1228,7 @@ extern "C" void sg_free(transformer_t* t) {
     void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
                     D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part, D->attn_cnt,
                     D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
-                    D->moe_sel, D->moe_w, D->moe_act, D->moe_offs, D->moe_order, D->moe_out,
+                    D->moe_sel, D->moe_w, D->moe_act, D->moe_logits, D->moe_offs, D->moe_order, D->moe_out,
                     D->xn_hi, D->xn_lo,
                     D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws,
                     D->dec_layers, D->dec_buf, D->dec_am_i, D->dec_sync, D->dec_trace,
