@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnParams p) {
   const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
   const int head = blockIdx.y;
   const int G = p.q_heads / p.kv_heads, kvh = head / G;
-  const int P = *p.pos, T = p.T;
+  const int P = *p.pos + p.q0, T = p.T;
   const int qd = p.q_heads * HD;
   const int t = qb * PQ + wave * 16 + c;  // this lane's query (column)
   const float* kb = p.kcache + (size_t)kvh * p.ctx * HD;

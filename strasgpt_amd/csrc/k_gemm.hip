@@ -21,6 +21,9 @@
 // next kernel (RMSNorm with residual, k_elementwise.hip) sums in order.
 //
 // Algorithmic FLOP per launch: 2 * M * N * K (x2 for the SwiGLU pair).
+#include <cstdlib>
+#include <cstring>
+
 #include "device_common.h"
 #include "hip_check.h"
 #include "kernels.h"
@@ -306,17 +309,38 @@ void launch(const GemmParams& p, int splits, hipStream_t s) {
                      shm, s, p);
 }
 
+// Tile shape forced by STRASGPT_GEMM_TILE ("128x256", "128x128", "64x128",
+// "64x64"), for tests that run every shape on small models; 0 = by size.
+int forced_tile() {
+  const char* v = getenv("STRASGPT_GEMM_TILE");
+  if (!v || !*v) return 0;
+  if (!strcmp(v, "128x256")) return 4;
+  if (!strcmp(v, "128x128")) return 3;
+  if (!strcmp(v, "64x128")) return 2;
+  if (!strcmp(v, "64x64")) return 1;
+  ST_DIE("STRASGPT_GEMM_TILE must be 128x256, 128x128, 64x128 or 64x64");
+}
+
 template <int EPI, int PREC>
 void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
-  // Measured on MI355X (prefill shapes, M = 512): with two blocks of tiles
-  // per CU or more, 128 x 128 tiles with a 2-stage ring (48 KiB of LDS:
-  // three blocks per CU) beat deeper rings; from about one block per CU,
-  // 64 x 128 tiles with 4 stages; below that 64 x 64.
+  // Measured on MI355X: with two blocks of 128 x 256 tiles per CU or more
+  // (M >= 2048 prefill shapes), those tiles (wavefront tile 64 x 128: fewer
+  // LDS bytes per MFMA; 64 KiB of LDS, two blocks per CU) reach ~45% of the
+  // MFMA rate against ~30% for 128 x 128; with two blocks of 128 x 128 per
+  // CU, 128 x 128 with a 2-stage ring (48 KiB: three blocks per CU) beats
+  // deeper rings; from about one block per CU, 64 x 128 with 4 stages;
+  // below that 64 x 64.
   const int cols = EPI == GEMM_SWIGLU ? 64 : 128;
   const long big = (long)((p.N + cols - 1) / cols) * ((p.M + 127) / 128) * splits;
-  if (big >= 512) launch<128, 128, 2, EPI, PREC>(p, splits, s);
-  else if (big >= 192) launch<64, 128, 4, EPI, PREC>(p, splits, s);
-  else launch<64, 64, 4, EPI, PREC>(p, splits, s);
+  const long wide = (long)((p.N + 2 * cols - 1) / (2 * cols)) * ((p.M + 127) / 128) * splits;
+  int shape = forced_tile();
+  if (!shape) shape = wide >= 512 ? 4 : big >= 512 ? 3 : big >= 192 ? 2 : 1;
+  switch (shape) {
+    case 4: launch<128, 256, 2, EPI, PREC>(p, splits, s); break;
+    case 3: launch<128, 128, 2, EPI, PREC>(p, splits, s); break;
+    case 2: launch<64, 128, 4, EPI, PREC>(p, splits, s); break;
+    default: launch<64, 64, 4, EPI, PREC>(p, splits, s); break;
+  }
 }
 
 template <int PREC>
@@ -347,10 +371,13 @@ void check(const GemmParams& p, int epi, int prec, int splits) {
 }  // namespace
 
 int gemm_splits(int M, int N, int K) {
-  // Enough blocks for the 256 CUs on the N = embedding_dim projections.
+  // Enough blocks for the 256 CUs on the N = embedding_dim projections;
+  // long reductions (K >= 16384: a 1024-step K loop and more) split until
+  // there are about four 128 x 128 tiles per CU.
   const long tiles = (long)((N + 127) / 128) * ((M + 127) / 128);
-  if (tiles >= 192) return 1;
-  int s = (int)((256 + tiles - 1) / tiles);
+  const long want = K >= 16384 ? 1024 : 192;
+  if (tiles >= want) return 1;
+  int s = (int)((K >= 16384 ? want : 256) + tiles - 1) / (int)tiles;
   while (s > 1 && (K + BK - 1) / BK < 4 * s) s--;  // keep at least 4 K tiles per split
   return s < 1 ? 1 : s;
 }

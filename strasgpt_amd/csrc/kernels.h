@@ -151,6 +151,7 @@ struct AttnParams {
   uint16_t* out_lo;      //   (out_lo may be null)
   const int* pos;        // device: position of the first query (cached count)
   int T, q_heads, kv_heads, hd, ctx;
+  int q0;                // prefill: the first query is at position *pos + q0
   // decode only: raw key of this step and QK-norm/RoPE inputs
   const float* kraw;     // [kv_heads*hd] or null
   float* kcache_w;       // k-cache (writable) for the processed key

@@ -126,13 +126,15 @@ struct transformer_device {
   int pb = 0, po = 0, pst = 0;
   size_t per_layer[W_COUNT] = {0};  // bytes per layer (or total for globals)
   void* w[W_COUNT] = {nullptr};
-  // activations [512][...]
+  // activations [chunk][...]
   float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *act = nullptr;
   // prefill GEMM inputs as bf16 hi/lo planes, split-K partial sums
   uint16_t *xn_hi = nullptr, *xn_lo = nullptr, *att_hi = nullptr, *att_lo = nullptr;
   uint16_t *act_hi = nullptr, *act_lo = nullptr;
   float* ws = nullptr;
   int ws_splits = 0;
+  size_t ws_rows = 0;   // split-K workspace: ws_splits x ws_rows rows of d
+  size_t chunk = 0;     // prefill rows per forward_chunk (>= the API's 512)
   float *kraw = nullptr, *logits = nullptr;
   int logits_rows = 0;
   size_t host_pos = 0;  // host mirror of *pos (profiling byte counts)
@@ -577,6 +579,8 @@ int residual_gemm(Dev* D, const uint16_t* a_hi, const uint16_t* a_lo, int lda,
   g.ldc = N;
   int splits = sg::gemm_splits(T, N, K);
   if (splits > D->ws_splits) splits = D->ws_splits;
+  if (splits > 1 && (size_t)splits * T > (size_t)D->ws_splits * D->ws_rows)
+    splits = (int)std::max<size_t>(1, (size_t)D->ws_splits * D->ws_rows / T);
   Prof pr(D, cls, (double)N * K * 2, 2.0 * T * N * K);
   if (splits > 1) {
     g.c = D->ws;
@@ -587,6 +591,8 @@ int residual_gemm(Dev* D, const uint16_t* a_hi, const uint16_t* a_lo, int lda,
   }
   return splits;
 }
+
+constexpr int kAttnRows = 512;  // queries per prefill attention launch
 
 // One layer over T > 1 rows. On entry D->xn_hi/lo hold the layer's input
 // RMSNorm; on exit x holds the layer output and, if next_norm is given, the
@@ -643,7 +649,17 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
     const double pairs = M * (double)D->host_pos + M * (M + 1) / 2;
     Prof pr(D, K_ATT_PRE, 2.0 * D->kvh * ((double)D->host_pos + M) * D->hd * 4,
             4.0 * D->qh * D->hd * pairs);
-    sg::attention_prefill(a, s);
+    // launches of at most kAttnRows queries (one launch over a long chunk
+    // balances its causal ranges less well)
+    for (int q0 = 0; q0 < T; q0 += kAttnRows) {
+      sg::AttnParams b = a;
+      b.q0 = q0;
+      b.T = std::min(kAttnRows, T - q0);
+      b.q = D->q + (size_t)q0 * D->qd;
+      b.out_hi = D->att_hi + (size_t)q0 * D->qd;
+      b.out_lo = split ? D->att_lo + (size_t)q0 * D->qd : nullptr;
+      sg::attention_prefill(b, s);
+    }
   }
   const int so = residual_gemm(D, D->att_hi, split ? D->att_lo : nullptr, D->qd, W16(D, W_O, l),
                                T, D->d, D->qd, K_O_GEMM);
@@ -690,7 +706,7 @@ void classifier(Dev* D, int T, int lc) {
   }
 }
 
-// One chunk of T <= 512 tokens whose ids are in device memory at `tok`,
+// One chunk of T <= D->chunk tokens whose ids are in device memory at `tok`,
 // at the device position *D->pos (mirrored on the host in D->host_pos).
 void forward_chunk(Dev* D, const int* tok, int T, int lc) {
   {
@@ -764,7 +780,11 @@ void predict_device(transformer_t* t, size_t T, const int* token, size_t lc,
   if (T + t->state->cached_count > (size_t)D->ctx) ST_DIE("context length exhausted");
   if (lc > T) lc = T;
   const size_t start = T - lc;
-  const size_t chunk_max = TRANSFORMER_CHUNK_MAX_LEN;
+  // The device runs prompts in chunks of D->chunk rows (the results do not
+  // depend on the chunk length: every row attends to the cache before its
+  // chunk and causally within it); hidden-state capture keeps the API's
+  // 512-token chunk.
+  const size_t chunk_max = D->cap_out ? (size_t)TRANSFORMER_CHUNK_MAX_LEN : D->chunk;
   if (D->cap_out && T > chunk_max) ST_DIE("hidden-state capture covers one chunk of at most 512 tokens");
   for (size_t c0 = 0; c0 < T; c0 += chunk_max) {
     const size_t n = T - c0 < chunk_max ? T - c0 : chunk_max;
@@ -1147,8 +1167,17 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
     }
   }
 
-  // State.
-  const size_t T = TRANSFORMER_CHUNK_MAX_LEN;
+  // State. Prefill chunk: STRASGPT_PREFILL_CHUNK rows (default 8192; at
+  // least the API's 512, at most the context): larger chunks give the
+  // prefill GEMMs larger M (wider tiles) and fewer launches.
+  {
+    size_t ch = 8192;
+    if (const char* v = getenv("STRASGPT_PREFILL_CHUNK")) ch = (size_t)strtoull(v, nullptr, 10);
+    if (ch < TRANSFORMER_CHUNK_MAX_LEN) ch = TRANSFORMER_CHUNK_MAX_LEN;
+    if (ch > (size_t)D->ctx) ch = std::max<size_t>(D->ctx, TRANSFORMER_CHUNK_MAX_LEN);
+    D->chunk = ch;
+  }
+  const size_t T = D->chunk;
   const size_t wide = H > d ? H : d;
   D->x = dalloc<float>(T * d);
   D->xn = dalloc<float>(T * wide);
@@ -1163,7 +1192,8 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->act_hi = dalloc<uint16_t>(T * H);
   D->act_lo = dalloc<uint16_t>(T * H);
   D->ws_splits = 8;
-  D->ws = dalloc<float>((size_t)D->ws_splits * T * d);
+  D->ws_rows = TRANSFORMER_CHUNK_MAX_LEN;  // split-K only pays on short chunks
+  D->ws = dalloc<float>((size_t)D->ws_splits * D->ws_rows * d);
   const size_t cache = (size_t)D->L * D->kvh * D->ctx * hd;
   D->kc = dalloc<float>(cache);
   D->vc = dalloc<float>(cache);

@@ -55,6 +55,47 @@ def test_tiny_golden(name, model_dir):
         assert tokens == [int(v) for v in g["generated"]]
 
 
+@pytest.mark.parametrize("tile", ["128x256", "128x128", "64x128", "64x64"])
+@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-chunk"])
+def test_gemm_tile_shapes(name, tile, model_dir, monkeypatch):
+    """Every prefill GEMM tile shape (forced with STRASGPT_GEMM_TILE; by
+    default the shape follows the grid size, so small models never reach
+    the large tiles) through every epilogue: fused QKV, residual, split-K
+    partial sums and SwiGLU. Logits and tokens as in test_tiny_golden."""
+    rt = runtime()
+    g = np.load(os.path.join(GOLDEN_DIR, f"{name}.npz"))
+    prompt = [int(v) for v in g["prompt"]]
+    monkeypatch.setenv("STRASGPT_GEMM_TILE", tile)
+    with rt.Transformer(model_dir(name)) as t:
+        logits = t.predict(prompt)
+        err = np.abs(logits[0] - g["logits"]).max()
+        log(f"{name} {tile}: max |logit error| {err:.3g}")
+        np.testing.assert_allclose(logits[0], g["logits"], rtol=RTOL, atol=ATOL)
+        assert err < 5e-4
+        t.reset()
+        tokens, _ = t.generate(prompt, len(g["generated"]))
+        assert tokens == [int(v) for v in g["generated"]]
+
+
+@pytest.mark.parametrize("chunk", ["512", "600"])
+def test_prefill_chunk_lengths(chunk, model_dir, monkeypatch):
+    """The 520-token prompt of tiny-chunk in device chunks of 512 (two
+    chunks, the API's chunk length) and of 600 rows (one chunk): tokens and
+    logits as in the reference run either way."""
+    rt = runtime()
+    g = np.load(os.path.join(GOLDEN_DIR, "tiny-chunk.npz"))
+    prompt = [int(v) for v in g["prompt"]]
+    monkeypatch.setenv("STRASGPT_PREFILL_CHUNK", chunk)
+    with rt.Transformer(model_dir("tiny-chunk")) as t:
+        logits = t.predict(prompt)
+        err = np.abs(logits[0] - g["logits"]).max()
+        log(f"tiny-chunk, chunk {chunk}: max |logit error| {err:.3g}")
+        assert err < 5e-4
+        t.reset()
+        tokens, _ = t.generate(prompt, len(g["generated"]))
+        assert tokens == [int(v) for v in g["generated"]]
+
+
 @pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen"])
 def test_tiny_hidden_states(name, model_dir):
     """Residual stream after every layer and the final-norm output against
