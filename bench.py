@@ -73,6 +73,7 @@ def cpu_baseline(d, shp, prompt, threads, decode_tokens):
 
 COPY_PROBE_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_decode_kernels_qwen3-4b.json")
+TRAFFIC_CONFIG = "qwen3-4b"  # the workload the counter summary was taken on
 
 
 def probe_traffic(t, prompt):
@@ -92,9 +93,12 @@ def probe_traffic(t, prompt):
     log("probe decode done")
 
 
-def traffic_for(kernel):
+def traffic_for(kernel, config):
     """HBM bytes per launch of a decode kernel class from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated on copy_probe_kernel), or None."""
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on copy_probe_kernel), or None.
+    The summary covers the Qwen3-4B-shaped workload only."""
+    if config != TRAFFIC_CONFIG:
+        return None
     try:
         with open(TRAFFIC_FILE) as f:
             table = json.load(f)
@@ -183,7 +187,7 @@ def main():
     kd = kernels[dom]
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(kd["gbs"], 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kd["gbs"] / HBM_PEAK_GBS, 4),
-                "traffic": traffic_for(dom), "avg_us": round(kd["avg_us"], 2),
+                "traffic": traffic_for(dom, shp.name), "avg_us": round(kd["avg_us"], 2),
                 "bytes_per_launch": kd["bytes_per_launch"]}
     pre = {k: stats[k] for k in prefill_kernels if k in stats}
     roofline_prefill = None
