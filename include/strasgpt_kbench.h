@@ -35,7 +35,8 @@ int strasgpt_kbench_gemv2(int n, int k, int dual, int flags, int variant, int it
                           double* avg_us, double* rel_err);
 
 /* Prefill GEMM C = A W^T, A fp32 [M][K], W bf16 [N][K]; precision 0 is
- * bf16x2 (split activations), 1 is bf16. */
+ * bf16x2 (split activations), 1 is bf16; adding 2 evicts the caches before
+ * each timed launch (operands come from HBM, as in a prefill pass). */
 int strasgpt_kbench_gemm(int m, int n, int k, int precision, int variant, int iters,
                          double* avg_us, double* rel_err);
 int strasgpt_kbench_gemm_variants(void);

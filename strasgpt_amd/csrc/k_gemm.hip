@@ -44,34 +44,36 @@ __device__ __forceinline__ void store_split(uint16_t* hi, uint16_t* lo, size_t i
 }
 
 // Block -> (m tile, n tile). Blocks are dispatched round-robin over the
-// XCDs; renumber so that each XCD receives a contiguous range of tiles, and
-// walk m fastest so that consecutive tiles share W columns.
+// XCDs; renumber so that each XCD receives a contiguous range of tiles.
+// Tiles are ordered in groups of kGroupM row tiles: within a group m runs
+// fastest, then n. The blocks resident on one XCD at a time then cover a
+// few row tiles x a few column tiles (about 8 x 4), so each A and W tile
+// fetched into that XCD's L2 serves several blocks; with every row tile in
+// flight at once (m fastest over all of M) each A tile would be fetched once
+// per block.
+constexpr int kGroupM = 8;
 __device__ __forceinline__ void tile_of(int mt, int nt, int& m_tile, int& n_tile) {
   const int b = blockIdx.x, total = mt * nt;
   int t = b;
   if (total % kXcds == 0) t = (b % kXcds) * (total / kXcds) + b / kXcds;
-  m_tile = t % mt;
-  n_tile = t / mt;
+  const int group = t / (kGroupM * nt), first = group * kGroupM;
+  const int rows = min(kGroupM, mt - first), in = t - group * kGroupM * nt;
+  m_tile = first + in % rows;
+  n_tile = in / rows;
 }
 
 // Waits until at most n vector-memory operations of this wavefront are in
-// flight (n is a multiple of the loads issued per stage, at most 31).
+// flight (n is a multiple of the loads issued per stage; counts that are not
+// listed wait for everything, which is correct but slower).
 __device__ __forceinline__ void wait_vmcnt(int n) {
   // s_waitcnt encoding (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
-#define SG_WAIT(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14))
+#define SG_WAIT(N) \
+  case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); break;
   switch (n) {
-    case 0: SG_WAIT(0); break;
-    case 2: SG_WAIT(2); break;
-    case 3: SG_WAIT(3); break;
-    case 4: SG_WAIT(4); break;
-    case 6: SG_WAIT(6); break;
-    case 8: SG_WAIT(8); break;
-    case 9: SG_WAIT(9); break;
-    case 12: SG_WAIT(12); break;
-    case 16: SG_WAIT(16); break;
-    case 18: SG_WAIT(18); break;
-    case 24: SG_WAIT(24); break;
-    default: SG_WAIT(0); break;
+    SG_WAIT(2) SG_WAIT(3) SG_WAIT(4) SG_WAIT(5) SG_WAIT(6) SG_WAIT(8) SG_WAIT(9) SG_WAIT(10)
+    SG_WAIT(12) SG_WAIT(15) SG_WAIT(16) SG_WAIT(18) SG_WAIT(20) SG_WAIT(24) SG_WAIT(30)
+    SG_WAIT(32) SG_WAIT(36) SG_WAIT(40) SG_WAIT(48)
+    default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break;
   }
 #undef SG_WAIT
 }
@@ -79,27 +81,63 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // One K step of 32 per stage. LDS rows are 64 bytes (32 bf16) with the four
-// 16-byte chunks of row r stored at chunk c ^ swz(r), swz(r) = ((r >> 1) & 3)
-// ^ ((r >> 3) & 1) (a function of r mod 16, so the 16-row load groups and
-// the fragment reads agree): the 16-byte fragment reads of 8 consecutive
-// lanes (rows r..r+7, one chunk) cover all 32 banks once, and those of 16
-// consecutive lanes cover 64 banks once. Stages are filled by global_load_lds_dwordx4: one
-// wavefront instruction writes 1 KiB = 16 rows, lane i landing at row i/4,
-// physical chunk i%4, so lane i fetches the logical chunk that belongs there.
-template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false>
-__global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams p) {
+// 16-byte chunks of row r stored at chunk c ^ swz(r), swz(r) = (-(r >> 2)) & 3
+// (a function of r mod 16, so the 16-row load groups and the fragment reads
+// agree). A fragment read is ds_read_b128 with lane l reading row l % 16,
+// logical chunk l / 16. gfx950 has 64 four-byte banks and serves a 128-bit
+// read in four phases of 16 lanes: within each half wavefront, the lane
+// quads (l >> 2) & 7 of even bit parity form one phase and those of odd
+// parity the other (measured with the bank-conflict counters). Rows r and
+// r + 4j share banks for a given chunk, so each phase's four quads must land
+// on four different physical chunks; this swizzle does that for both
+// parities (a conflict costs a second pass: 8 instead of 4 LDS cycles per
+// read). Stages are filled by global_load_lds_dwordx4: one wavefront
+// instruction writes 1 KiB = 16 rows, lane i landing at row i/4, physical
+// chunk i%4, so lane i fetches the logical chunk that belongs there.
+//
+// K steps of 64 per stage use 128-byte rows (eight chunks; rows r and r + 2j
+// share banks): swz(r) = (r >> 1) & 7 spreads each phase's rows over the
+// eight chunks of both bank halves. A 128-byte row segment per DMA lane
+// group moves about 1.8x the bytes per cycle of a 64-byte one through the
+// CU's texture path (L2-resident microbenchmark), which is what limits the
+// 32-deep stages.
+template <int KS>
+__device__ __forceinline__ int lds_swz(int r) {
+  return KS == 32 ? (0 - (r >> 2)) & 3 : (r >> 1) & 7;
+}
+
+// OCC: blocks per CU the register allocation must allow (0: two with
+// fragment pipelining, else one).
+// WD = 1: the W tiles get a ring one stage deeper than the A tiles (A is
+// re-read by every column block and stays in cache; W streams from HBM once
+// per XCD), loads issued so that W has one more K step of latency cover.
+template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false, int OCC = 0, int KS = 32,
+          int WD = 0>
+__global__ __launch_bounds__(kThreads, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_kernel(GemmParams p) {
   constexpr bool SPLIT = PREC == GEMM_SPLIT2;
   constexpr bool DUAL = EPI == GEMM_SWIGLU;
-  constexpr int KS = 32;                       // K per stage
+  static_assert(KS == 32 || KS == 64, "K per stage");
+  static_assert(!PIPE || KS == 32, "fragment pipelining uses 32-deep stages");
+  constexpr int ROWB = KS * 2;                 // bytes per LDS row
+  constexpr int CPR = ROWB / 16;               // 16-byte chunks per row
+  constexpr int RPI = 1024 / ROWB;             // rows per 1 KiB load instruction
+  constexpr int KSUB = KS / 32;                // MFMA k-steps per stage
   constexpr int WM = BM / 2, WN = BN / 2;      // wavefront tile
   constexpr int MT = WM / 16, NT = WN / 16;    // 16x16 MFMA tiles per wavefront
   constexpr int A_ROWS = BM * (SPLIT ? 2 : 1);
-  constexpr int ROWS = A_ROWS + BN;            // 64-byte rows per stage
-  constexpr int GROUPS = ROWS / 16;            // 1 KiB load instructions per stage
+  constexpr int ROWS = A_ROWS + BN;            // rows per stage
+  constexpr int GROUPS = ROWS / RPI;           // 1 KiB load instructions per stage
   constexpr int PER_WAVE = GROUPS / (kThreads / WAVE);
   static_assert(GROUPS % (kThreads / WAVE) == 0, "stage loads must split evenly over waves");
   static_assert(!DUAL || NT % 2 == 0, "SwiGLU tiles pair gate and up sub-tiles");
-  constexpr int STAGE = ROWS * 64;             // bytes
+  constexpr int STAGE = ROWS * ROWB;           // bytes
+  static_assert(!WD || !PIPE, "deep W ring without fragment pipelining");
+  constexpr int NSW = NS + WD;                 // W ring depth
+  constexpr int A_BYTES = A_ROWS * ROWB, W_BYTES = BN * ROWB;
+  constexpr int GA = A_ROWS / RPI, GW = BN / RPI;
+  constexpr int PWA = GA / (kThreads / WAVE), PWW = GW / (kThreads / WAVE);
+  static_assert(!WD || (GA % (kThreads / WAVE) == 0 && GW % (kThreads / WAVE) == 0),
+                "deep W ring: A and W loads must split evenly over waves");
 
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
 
@@ -115,27 +153,34 @@ __global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams
   const int kbeg = blockIdx.z * kper, kend = min(K, kbeg + kper);
   const int nk = kend > kbeg ? (kend - kbeg) / KS : 0;
 
-  // Per-lane global source of each load group this wavefront issues.
-  const uint16_t* src[PER_WAVE];
-  {
-    const int r16 = lane / 4, phys = lane % 4;
-#pragma unroll
-    for (int i = 0; i < PER_WAVE; i++) {
-      const int g = wave * PER_WAVE + i;
-      const int row = g * 16 + r16;  // row in the stage
-      const int c = phys ^ (((r16 >> 1) & 3) ^ ((r16 >> 3) & 1));
-      if (row < A_ROWS) {
-        const int r = row % BM;
-        const int m = min(m0 + r, M - 1);  // rows past M load row M-1, never stored
-        const uint16_t* base = (SPLIT && row >= BM) ? p.a_lo : p.a_hi;
-        src[i] = base + (size_t)m * p.lda + c * 8;
-      } else {
-        const int r = row - A_ROWS;
-        const int nn = min(DUAL ? n0 + (r % (BN / 2)) : n0 + r, N - 1);
-        const uint16_t* base = (DUAL && r >= BN / 2) ? p.w2 : p.w;
-        src[i] = base + (size_t)nn * K + c * 8;
-      }
+  // Per-lane global source of load group g (rows g * RPI .. of the stage:
+  // A rows first, then W rows).
+  auto group_src = [&](int g) -> const uint16_t* {
+    const int rr = lane / CPR, phys = lane % CPR;
+    const int row = g * RPI + rr;  // row in the stage
+    const int c = phys ^ lds_swz<KS>(row);
+    if (row < A_ROWS) {
+      const int r = row % BM;
+      const int m = min(m0 + r, M - 1);  // rows past M load row M-1, never stored
+      const uint16_t* base = (SPLIT && row >= BM) ? p.a_lo : p.a_hi;
+      return base + (size_t)m * p.lda + c * 8;
     }
+    const int r = row - A_ROWS;
+    const int nn = min(DUAL ? n0 + (r % (BN / 2)) : n0 + r, N - 1);
+    const uint16_t* base = (DUAL && r >= BN / 2) ? p.w2 : p.w;
+    return base + (size_t)nn * K + c * 8;
+  };
+  const uint16_t* src[WD ? 1 : PER_WAVE];
+  const uint16_t* srca[WD ? PWA : 1];
+  const uint16_t* srcw[WD ? PWW : 1];
+  if constexpr (WD) {
+#pragma unroll
+    for (int i = 0; i < PWA; i++) srca[i] = group_src(wave * PWA + i);
+#pragma unroll
+    for (int i = 0; i < PWW; i++) srcw[i] = group_src(GA + wave * PWW + i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; i++) src[i] = group_src(wave * PER_WAVE + i);
   }
   auto issue = [&](int t) {
     unsigned char* st = smem + (t % NS) * STAGE;
@@ -146,9 +191,25 @@ __global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams
       __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0), (lds_ptr)(st + g * 1024), 16, 0, 0);
     }
   };
-  auto frag = [&](const unsigned char* base, int r) -> bf16x8 {
-    const int c = lane / 16;
-    return *(const bf16x8*)(base + r * 64 + ((c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1))) << 4));
+  auto issue_a = [&](int t) {
+    unsigned char* st = smem + (t % NS) * A_BYTES;
+    const int k0 = kbeg + t * KS;
+#pragma unroll
+    for (int i = 0; i < PWA; i++)
+      __builtin_amdgcn_global_load_lds((const void*)(srca[i] + k0),
+                                       (lds_ptr)(st + (wave * PWA + i) * 1024), 16, 0, 0);
+  };
+  auto issue_w = [&](int t) {
+    unsigned char* st = smem + NS * A_BYTES + (t % NSW) * W_BYTES;
+    const int k0 = kbeg + t * KS;
+#pragma unroll
+    for (int i = 0; i < PWW; i++)
+      __builtin_amdgcn_global_load_lds((const void*)(srcw[i] + k0),
+                                       (lds_ptr)(st + (wave * PWW + i) * 1024), 16, 0, 0);
+  };
+  auto frag = [&](const unsigned char* base, int r, int j = 0) -> bf16x8 {
+    const int c = 4 * j + lane / 16;  // logical chunk of MFMA k-step j
+    return *(const bf16x8*)(base + r * ROWB + ((c ^ lds_swz<KS>(r)) << 4));
   };
   auto b_tile_row = [&](int j) -> int {
     if (!DUAL) return wn * WN + j * 16;
@@ -162,10 +223,55 @@ __global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams
 #pragma unroll
     for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const int fr = lane % 16;
+  // One K step: fragments from A stage sa and W stage sw, MFMAs.
+  auto mma_step = [&](const unsigned char* sa, const unsigned char* sw) {
+#pragma unroll
+    for (int ks = 0; ks < KSUB; ks++) {
+      bf16x8 bfrag[NT];
+#pragma unroll
+      for (int j = 0; j < NT; j++) bfrag[j] = frag(sw, b_tile_row(j) + fr, ks);
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        const int r = wm * WM + i * 16 + fr;
+        const bf16x8 ahi = frag(sa, r, ks);
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bfrag[j], acc[i][j], 0, 0, 0);
+        if (SPLIT) {
+          const bf16x8 alo = frag(sa + BM * ROWB, r, ks);
+#pragma unroll
+          for (int j = 0; j < NT; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bfrag[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+  };
+  if constexpr (WD) {
+    // Issue order W0 A0 W1 A1 .. W(NS-2) A(NS-2) W(NS-1), then per step kt
+    // A(kt+NS-1) W(kt+NS). Loads complete in issue order, so at step kt the
+    // ones issued after A(kt) may stay in flight: W(kt+1 .. kt+NS-1) and
+    // A(kt+1 .. kt+NS-2). Slots rewritten at step kt were last read at step
+    // kt-1, which every wave has finished at the barrier.
+#pragma unroll
+    for (int t = 0; t < NS - 1; t++)
+      if (t < nk) {
+        issue_w(t);
+        issue_a(t);
+      }
+    if (NS - 1 < nk) issue_w(NS - 1);
+    for (int kt = 0; kt < nk; kt++) {
+      const int aw = max(0, min(kt + NS - 1, nk - 1) - kt), aa = max(0, min(kt + NS - 2, nk - 1) - kt);
+      wait_vmcnt(aw * PWW + aa * PWA);
+      __builtin_amdgcn_s_barrier();
+      if (kt + NS - 1 < nk) issue_a(kt + NS - 1);
+      if (kt + NS < nk) issue_w(kt + NS);
+      mma_step(smem + (kt % NS) * A_BYTES, smem + NS * A_BYTES + (kt % NSW) * W_BYTES);
+    }
+  } else {
 #pragma unroll
   for (int t = 0; t < NS - 1; t++)
     if (t < nk) issue(t);
-  const int fr = lane % 16;
   if constexpr (PIPE) {
     // Fragments of K step kt+1 are read from LDS while the MFMAs of step kt
     // run (two register sets, alternating without copies). At step kt:
@@ -181,12 +287,12 @@ __global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams
     auto read_frags = [&](int kt, Frags& F) {
       const unsigned char* st = smem + (kt % NS) * STAGE;
 #pragma unroll
-      for (int j = 0; j < NT; j++) F.b[j] = frag(st + A_ROWS * 64, b_tile_row(j) + fr);
+      for (int j = 0; j < NT; j++) F.b[j] = frag(st + A_ROWS * ROWB, b_tile_row(j) + fr);
 #pragma unroll
       for (int i = 0; i < MT; i++) {
         const int r = wm * WM + i * 16 + fr;
         F.ahi[i] = frag(st, r);
-        if (SPLIT) F.alo[i] = frag(st + BM * 64, r);
+        if (SPLIT) F.alo[i] = frag(st + BM * ROWB, r);
       }
     };
     auto mma = [&](const Frags& F) {
@@ -232,23 +338,8 @@ __global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams
     __builtin_amdgcn_s_barrier();
     if (kt + NS - 1 < nk) issue(kt + NS - 1);
     const unsigned char* st = smem + (kt % NS) * STAGE;
-    bf16x8 bfrag[NT];
-#pragma unroll
-    for (int j = 0; j < NT; j++) bfrag[j] = frag(st + A_ROWS * 64, b_tile_row(j) + fr);
-#pragma unroll
-    for (int i = 0; i < MT; i++) {
-      const int r = wm * WM + i * 16 + fr;
-      const bf16x8 ahi = frag(st, r);
-#pragma unroll
-      for (int j = 0; j < NT; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bfrag[j], acc[i][j], 0, 0, 0);
-      if (SPLIT) {
-        const bf16x8 alo = frag(st + BM * 64, r);
-#pragma unroll
-        for (int j = 0; j < NT; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bfrag[j], acc[i][j], 0, 0, 0);
-      }
-    }
+    mma_step(st, st + A_ROWS * ROWB);
+  }
   }
 
   // Epilogue: lane holds C[4*(lane/16) + e][lane % 16] of each 16x16 tile.
@@ -292,51 +383,70 @@ __global__ __launch_bounds__(kThreads, PIPE ? 2 : 1) void gemm_kernel(GemmParams
   }
 }
 
-template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false>
+template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false, int OCC = 0, int KS = 32,
+          int WD = 0>
 void launch(const GemmParams& p, int splits, hipStream_t s) {
   const int cols = EPI == GEMM_SWIGLU ? BN / 2 : BN;
   const int tiles = ((p.N + cols - 1) / cols) * ((p.M + BM - 1) / BM);
   constexpr int rows = BM * (PREC == GEMM_SPLIT2 ? 2 : 1) + BN;
-  constexpr size_t shm = (size_t)NS * rows * 64;
+  constexpr size_t shm = ((size_t)NS * rows + (size_t)WD * BN) * KS * 2;
   static_assert(shm <= 160 * 1024, "GEMM stages exceed LDS");
   static bool attr = false;
   if (!attr) {
-    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC, PIPE>,
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
     attr = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC, PIPE>), dim3(tiles, 1, splits), dim3(kThreads),
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD>), dim3(tiles, 1, splits), dim3(kThreads),
                      shm, s, p);
 }
 
-// Tile shape forced by STRASGPT_GEMM_TILE ("128x256", "128x128", "64x128",
-// "64x64"), for tests that run every shape on small models; 0 = by size.
+// Tile shape forced by STRASGPT_GEMM_TILE ("128x256", "128x128",
+// "64x128x64", "64x128x64s4", "64x128", "64x64"), for tests that run every
+// shape on small models; 0 = by size.
 int forced_tile() {
   const char* v = getenv("STRASGPT_GEMM_TILE");
   if (!v || !*v) return 0;
   if (!strcmp(v, "128x256")) return 4;
   if (!strcmp(v, "128x128")) return 3;
+  if (!strcmp(v, "64x128x64")) return 5;
+  if (!strcmp(v, "64x128x64s4")) return 6;
   if (!strcmp(v, "64x128")) return 2;
   if (!strcmp(v, "64x64")) return 1;
-  ST_DIE("STRASGPT_GEMM_TILE must be 128x256, 128x128, 64x128 or 64x64");
+  ST_DIE("STRASGPT_GEMM_TILE must be 128x256, 128x128, 64x128x64, 64x128x64s4, 64x128 or 64x64");
 }
 
 template <int EPI, int PREC>
 void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
-  // Measured on MI355X: with two blocks of 128 x 256 tiles per CU or more
-  // (M >= 2048 prefill shapes), those tiles (wavefront tile 64 x 128: fewer
-  // LDS bytes per MFMA; 64 KiB of LDS, two blocks per CU) reach ~45% of the
-  // MFMA rate against ~30% for 128 x 128; with two blocks of 128 x 128 per
-  // CU, 128 x 128 with a 2-stage ring (48 KiB: three blocks per CU) beats
-  // deeper rings; from about one block per CU, 64 x 128 with 4 stages;
-  // below that 64 x 64.
+  // Measured on MI355X, bf16x2, with the weights coming from HBM (caches
+  // evicted before each launch, as in a prefill pass):
+  // * from about 4 blocks of 128 x 256 per CU (M >= 2048 prefill shapes),
+  //   128 x 256 with 32-deep stages and two blocks per CU reaches ~50% of
+  //   the MFMA rate (fewest stage bytes per MFMA);
+  // * below that, 64 x 128 tiles with 64-deep stages: 128-byte row segments
+  //   per DMA lane group move ~1.8x the bytes per cycle of 64-byte ones.
+  //   With more than one block per CU: two blocks per CU, a 2-stage A ring
+  //   and a 3-stage W ring (80 KiB; the blocks sharing a W tile request it
+  //   together, so W needs the longer cover); with at most one block per
+  //   CU: one block with a 4-stage ring. 1.2-2.3x over the 32-deep shapes
+  //   on the M = 256 and 512 projections;
+  // * K not a multiple of 64 and tiny grids keep the 32-deep shapes.
   const int cols = EPI == GEMM_SWIGLU ? 64 : 128;
   const long big = (long)((p.N + cols - 1) / cols) * ((p.M + 127) / 128) * splits;
   const long wide = (long)((p.N + 2 * cols - 1) / (2 * cols)) * ((p.M + 127) / 128) * splits;
+  const long small = (long)((p.N + cols - 1) / cols) * ((p.M + 63) / 64) * splits;
   int shape = forced_tile();
-  if (!shape) shape = wide >= 512 ? 4 : big >= 512 ? 3 : big >= 192 ? 2 : 1;
+  if ((shape == 5 || shape == 6) && p.K % 64) shape = 2;
+  if (!shape) {
+    if (wide >= 1024) shape = 4;
+    else if (p.K % 64 == 0 && small > 256) shape = 5;
+    else if (p.K % 64 == 0 && small >= 64) shape = 6;
+    else shape = big >= 512 ? 3 : big >= 192 ? 2 : 1;
+  }
   switch (shape) {
-    case 4: launch<128, 256, 2, EPI, PREC>(p, splits, s); break;
+    case 4: launch<128, 256, 2, EPI, PREC, false, 2>(p, splits, s); break;
+    case 5: launch<64, 128, 2, EPI, PREC, false, 2, 64, 1>(p, splits, s); break;
+    case 6: launch<64, 128, 4, EPI, PREC, false, 1, 64>(p, splits, s); break;
     case 3: launch<128, 128, 2, EPI, PREC>(p, splits, s); break;
     case 2: launch<64, 128, 4, EPI, PREC>(p, splits, s); break;
     default: launch<64, 64, 4, EPI, PREC>(p, splits, s); break;
@@ -390,13 +500,27 @@ void gemm(const GemmParams& p, int epi, int prec, int splits, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
-int gemm_variant_count() { return 14; }
+int gemm_variant_count() { return 30; }
 
 void gemm_variant(const GemmParams& p, int prec, int v, hipStream_t s) {
   check(p, GEMM_STORE, prec, 1);
 #define GP(BM, BN, NS)                                                                \
   if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, true>(p, 1, s); \
   else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, true>(p, 1, s);                      \
+  break;
+#define GO(BM, BN, NS, PIPE, OCC)                                                          \
+  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, PIPE, OCC>(p, 1, s); \
+  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, PIPE, OCC>(p, 1, s);                      \
+  break;
+#define GK(BM, BN, NS, OCC)                                                                \
+  if (p.K % 64) ST_DIE("64-deep GEMM stages need K to be a multiple of 64");               \
+  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, false, OCC, 64>(p, 1, s); \
+  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, false, OCC, 64>(p, 1, s);                      \
+  break;
+#define GW(BM, BN, NS, OCC, KS)                                                                \
+  if (p.K % KS) ST_DIE("GEMM stages need K to be a multiple of the stage depth");                \
+  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, false, OCC, KS, 1>(p, 1, s); \
+  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, false, OCC, KS, 1>(p, 1, s);                      \
   break;
 #define G(BM, BN, NS)                                                        \
   if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2>(p, 1, s); \
@@ -417,10 +541,29 @@ void gemm_variant(const GemmParams& p, int prec, int v, hipStream_t s) {
     case 11: GP(64, 128, 4)
     case 12: GP(128, 256, 3)
     case 13: GP(64, 128, 3)
+    case 14: GO(128, 256, 2, false, 2)
+    case 15: GO(128, 128, 2, false, 3)
+    case 16: GO(128, 256, 3, true, 1)
+    case 17: GO(128, 128, 3, false, 2)
+    case 18: GO(256, 128, 2, false, 2)
+    case 19: GO(128, 256, 4, true, 1)
+    case 20: GK(128, 128, 3, 1)
+    case 21: GK(128, 128, 2, 1)
+    case 22: GK(128, 256, 2, 1)
+    case 23: GK(64, 128, 4, 1)
+    case 24: GK(64, 128, 2, 2)
+    case 25: GK(256, 128, 2, 1)
+    case 26: GW(64, 128, 2, 2, 64)
+    case 27: GW(64, 128, 3, 1, 64)
+    case 28: GW(128, 128, 2, 1, 64)
+    case 29: GW(64, 128, 3, 2, 32)
     default: ST_DIE("unknown GEMM variant");
   }
 #undef G
 #undef GP
+#undef GO
+#undef GK
+#undef GW
   HIP_CHECK(hipGetLastError());
 }
 

@@ -55,13 +55,16 @@ def test_tiny_golden(name, model_dir):
         assert tokens == [int(v) for v in g["generated"]]
 
 
-@pytest.mark.parametrize("tile", ["128x256", "128x128", "64x128", "64x64"])
+@pytest.mark.parametrize("tile", ["128x256", "128x128", "64x128x64", "64x128x64s4", "64x128", "64x64"])
 @pytest.mark.parametrize("name", ["tiny-qwen", "tiny-chunk"])
 def test_gemm_tile_shapes(name, tile, model_dir, monkeypatch):
     """Every prefill GEMM tile shape (forced with STRASGPT_GEMM_TILE; by
     default the shape follows the grid size, so small models never reach
     the large tiles) through every epilogue: fused QKV, residual, split-K
-    partial sums and SwiGLU. Logits and tokens as in test_tiny_golden."""
+    partial sums and SwiGLU. The 64x128x64 shapes (64-deep K stages; a
+    deeper ring for W, or a 4-stage ring) need K to be a multiple of 64: the
+    two models reach them with every epilogue between them (tiny-chunk: QKV,
+    O, gate/up; tiny-qwen: O, down) and fall back to 64x128 elsewhere. Logits and tokens as in test_tiny_golden."""
     rt = runtime()
     g = np.load(os.path.join(GOLDEN_DIR, f"{name}.npz"))
     prompt = [int(v) for v in g["prompt"]]
