@@ -61,6 +61,12 @@ int strasgpt_kbench_copy(size_t bytes, int iters, double* avg_us);
 int strasgpt_kbench_barrier(int blocks, int rounds, int fence, int words,
                             double* us_per_round, int* bad_reads, int* timed_out);
 
+/* Causal prefill attention over T queries after P cached positions
+ * (synthetic fp32 queries and cache); variant 0 is the split-bf16
+ * matrix-core kernel, 1 the fp32 matrix-core kernel. */
+int strasgpt_kbench_attn_prefill(int T, int P, int q_heads, int kv_heads, int hd, int variant,
+                                 int iters, double* avg_us);
+
 #ifdef __cplusplus
 }
 #endif

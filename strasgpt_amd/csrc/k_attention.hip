@@ -13,6 +13,8 @@
 // projection); the block holding the newest position writes the processed
 // key into the cache.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 #include "device_common.h"
 #include "hip_check.h"
@@ -55,6 +57,7 @@ __host__ __device__ inline void attention_decode_split(int total, int max_chunks
 // rows are stored with their 16-byte chunks XOR-swizzled by the row index
 // so that the 16 rows read by one instruction hit distinct banks.
 constexpr int PQ = 64, PK = 64;
+constexpr int kX3Keys = 32;  // key tile of the split-bf16 kernel
 
 template <int HD>
 __device__ __forceinline__ int pre_swz(int row) {
@@ -71,10 +74,10 @@ __device__ __forceinline__ int pre_off(int row, int d) {
 // rows past it are masked) into swizzled LDS tiles by DMA, 1 KiB per wave
 // instruction; lane i of instruction n lands at tile float n*256 + 4i and
 // fetches the chunk that belongs there.
-template <int HD>
+template <int HD, int ROWS = PK>
 __device__ __forceinline__ void pre_dma(const float* kb, const float* vb, int kv0, int last, float* kt,
                                         float* vt) {
-  constexpr int CH = HD / 4, RPK = 256 / HD, NI = PK * HD / 256;
+  constexpr int CH = HD / 4, RPK = 256 / HD, NI = ROWS * HD / 256;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   for (int n = wave; n < NI; n += 4) {
     const int row = n * RPK + lane / CH, phys = lane % CH;
@@ -185,6 +188,280 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnParams p) {
         }
   }
   // lane (g, c) holds O^T[16j + 4g + e][t]: out[t][head*HD + 16j + 4g + e]
+  if (t < T) {
+#pragma unroll
+    for (int j = 0; j < DJ; j++) {
+      const size_t idx = (size_t)t * qd + head * HD + 16 * j + 4 * g;
+      uint16_t hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float v = o[j][e] / l;
+        hi[e] = f32_to_bf16_rne(v);
+        lo[e] = f32_to_bf16_rne(v - bf16_to_f32(hi[e]));
+      }
+      *(uint2*)(p.out_hi + idx) = make_uint2(hi[0] | ((unsigned)hi[1] << 16), hi[2] | ((unsigned)hi[3] << 16));
+      if (p.out_lo)
+        *(uint2*)(p.out_lo + idx) = make_uint2(lo[0] | ((unsigned)lo[1] << 16), lo[2] | ((unsigned)lo[3] << 16));
+    }
+  }
+}
+
+// Prefill attention on the bf16 matrix cores with split operands
+// (v_mfma_f32_16x16x32_bf16). Every fp32 operand x is split into
+// hi = bf16(x) and lo = bf16(x - hi) (x - hi is exact in fp32), and each
+// product is formed as hi*hi' + hi*lo' + lo*hi' in the fp32 accumulator:
+// the dropped lo*lo' term and the remainders of the split are below
+// 2^-16 of the product, against the 2^-24 of an fp32 product, at 3 bf16
+// MFMAs (16 cycles each for 16x16x32) where the fp32 matrix cores take 32
+// cycles per 16x16x4. The causal structure, the online softmax and the
+// summation per query follow the fp32 kernel above.
+//
+// Block = 64 queries of one head (4 waves x 16), key tiles of 32. Each
+// thread loads its share of the next tile's fp32 K and V rows into
+// registers while the current tile is multiplied, splits them once for the
+// whole block and stores bf16 hi/lo planes to LDS: K as rows [key][HD]
+// (16-byte chunks XOR-swizzled by key), V transposed [HD][32 keys] (chunks
+// swizzled by d), double-buffered (64 KiB at head_dim 128: two blocks per
+// CU). Per tile and wave:
+// * S^T = K Q^T: A operand row c of key sub-tile s is key
+//   8 (c / 4) + 4 s + c % 4, so that the output lane (g, c) holds keys
+//   8 g .. 8 g + 7 of query c; B operand = the query's split values, kept
+//   in registers for the whole block.
+// * O^T += V^T P^T over the tile's 32 keys as one MFMA k-step: P^T is the
+//   B operand straight from the scores a lane holds; the A operand is one
+//   16-byte read of V^T (row 16 dj + c, keys 8 g ..) per plane.
+// head_dim 16 pads the 32-dim k-step of S with zeros (lanes g >= 2).
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+
+// (a, b) -> packed bf16 hi pair and lo pair: hi = bf16(x) (round to nearest
+// even, v_cvt_pk_bf16_f32), lo = bf16(x - hi) with x - hi exact in fp32.
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const bf16x2v h = __builtin_convertvector((f32x2v){a, b}, bf16x2v);
+  const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+  const float ra = a - __builtin_bit_cast(float, hb << 16);
+  const float rb = b - __builtin_bit_cast(float, hb & 0xffff0000u);
+  hi = hb;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){ra, rb}, bf16x2v));
+}
+
+template <int HD>
+struct X3Lds {
+  static constexpr int KP = kX3Keys * HD;  // bf16 elements per K plane
+  static constexpr int VP = HD * kX3Keys;  // per V^T plane
+  static constexpr int buf = 2 * KP + 2 * VP;  // one tile: K hi, K lo, V^T hi, V^T lo
+  static constexpr int bytes = 2 * buf * 2;    // two buffers of bf16
+};
+
+template <int HD>
+__device__ __forceinline__ int x3_kswz(int key) {
+  constexpr int CH = HD / 8;  // 16-byte chunks per K row
+  return CH >= 4 ? (key ^ (key >> 2)) & (CH - 1) : (key >> 2) & (CH - 1);
+}
+__device__ __forceinline__ int x3_vswz(int d) { return (0 - (d >> 2)) & 3; }
+
+template <int HD>
+__global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
+  constexpr int KT = kX3Keys;              // keys per tile
+  constexpr int NKK = (HD + 31) / 32;      // 32-dim k-steps of S
+  constexpr int DJ = HD / 16;              // 16-dim sub-tiles of O
+  constexpr int CH = HD / 8;               // 16-byte chunks per K row
+  constexpr int NL = (KT * HD / 4 + 255) / 256;  // K float4s / V key quads per thread
+  using L = X3Lds<HD>;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
+  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, g = lane / 16, c = lane % 16;
+  const int nqb = (p.T + PQ - 1) / PQ;
+  const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
+  const int head = blockIdx.y;
+  const int G = p.q_heads / p.kv_heads, kvh = head / G;
+  const int P = *p.pos + p.q0, T = p.T;
+  const int qd = p.q_heads * HD;
+  const int t = qb * PQ + wave * 16 + c;  // this lane's query
+  const float* kb = p.kcache + (size_t)kvh * p.ctx * HD;
+  const float* vb = p.vcache + (size_t)kvh * p.ctx * HD;
+  const int kv_end = P + min(qb * PQ + PQ, T);  // keys visible to the block's last query
+  const int ntiles = (kv_end + KT - 1) / KT;
+  // scores in the base-2 domain: s * log2(e) / sqrt(HD)
+  const float sl2 = 1.44269504088896341f / sqrtf((float)HD);
+  // last key visible to this lane's query, and to every query of the block
+  const int vis = min(P + t, kv_end - 1), vis_all = min(P + qb * PQ, kv_end - 1);
+
+  auto split8 = [](const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) split2(x[2 * e], x[2 * e + 1], h[e], l[e]);
+    hi = __builtin_bit_cast(bf16x8, (uint4){h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(bf16x8, (uint4){l[0], l[1], l[2], l[3]});
+  };
+  // Register staging of one tile: K float4 u (key u / (HD/4), dims 4 (u %
+  // (HD/4)) ..) and V key quad u (dim u % HD, keys 4 (u / HD) ..), for
+  // u = tid + 256 i < KT * HD / 4. Rows past the last visible key load that
+  // key (masked later).
+  float4 kr[NL];
+  float vr[NL][4];
+  auto load_tile = [&](int kv0) {
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int u = tid + 256 * i;
+      if (KT * HD / 4 % 256 == 0 || u < KT * HD / 4) {
+        const int key = min(kv0 + u / (HD / 4), kv_end - 1);
+        kr[i] = *(const float4*)(kb + (size_t)key * HD + 4 * (u % (HD / 4)));
+        const int d = u % HD, k4 = kv0 + 4 * (u / HD);
+        if (k4 + 3 < kv_end) {  // whole quad visible: one address, constant row offsets
+          const float* vp = vb + (size_t)k4 * HD + d;
+#pragma unroll
+          for (int e = 0; e < 4; e++) vr[i][e] = vp[e * HD];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) vr[i][e] = vb[(size_t)min(k4 + e, kv_end - 1) * HD + d];
+        }
+      }
+    }
+  };
+  auto store_tile = [&](uint16_t* buf) {
+    uint16_t* khi = buf;
+    uint16_t* klo = buf + L::KP;
+    uint16_t* vhi = buf + 2 * L::KP;
+    uint16_t* vlo = vhi + L::VP;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int u = tid + 256 * i;
+      if (KT * HD / 4 % 256 == 0 || u < KT * HD / 4) {
+        uint2 h, lo;
+        split2(kr[i].x, kr[i].y, h.x, lo.x);
+        split2(kr[i].z, kr[i].w, h.y, lo.y);
+        const int key = u / (HD / 4), d4 = u % (HD / 4);
+        const int off = key * HD + (((d4 >> 1) ^ x3_kswz<HD>(key)) << 3) + ((d4 & 1) << 2);
+        *(uint2*)(khi + off) = h;
+        *(uint2*)(klo + off) = lo;
+        split2(vr[i][0], vr[i][1], h.x, lo.x);
+        split2(vr[i][2], vr[i][3], h.y, lo.y);
+        const int d = u % HD, q4 = u / HD;  // key quad
+        const int voff = d * KT + (((q4 >> 1) ^ x3_vswz(d)) << 3) + ((q4 & 1) << 2);
+        *(uint2*)(vhi + voff) = h;
+        *(uint2*)(vlo + voff) = lo;
+      }
+    }
+  };
+
+  load_tile(0);
+  // Q^T operand: lane (g, c) holds q[t][32 kk + 8 g .. + 7], split.
+  bf16x8 qh[NKK], ql[NKK];
+  {
+    const float* qr = p.q + (size_t)min(t, T - 1) * qd + head * HD;
+#pragma unroll
+    for (int kk = 0; kk < NKK; kk++) {
+      float x[8];
+      const int d = 32 * kk + 8 * g;
+      if (d < HD) {
+        const float4 a = *(const float4*)(qr + d), b = *(const float4*)(qr + d + 4);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = 0.0f;
+      }
+      split8(x, qh[kk], ql[kk]);
+    }
+  }
+  store_tile(xl);
+  if (ntiles > 1) load_tile(KT);
+  __syncthreads();
+
+  f32x4 o[DJ];
+#pragma unroll
+  for (int j = 0; j < DJ; j++) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+  // Per-lane parts of the LDS addresses (elements).
+  int krow[2], kx[2];
+#pragma unroll
+  for (int s = 0; s < 2; s++) {
+    const int key = 8 * (c >> 2) + 4 * s + (c & 3);
+    krow[s] = key * HD;
+    kx[s] = x3_kswz<HD>(key);
+  }
+  const int vrow = c * KT + ((g ^ x3_vswz(c)) << 3);  // + 16 dj * KT
+
+  for (int it = 0; it < ntiles; it++) {
+    const uint16_t* buf = xl + (it & 1) * L::buf;
+    const uint16_t* khi = buf;
+    const uint16_t* klo = buf + L::KP;
+    const uint16_t* vhi = buf + 2 * L::KP;
+    const uint16_t* vlo = vhi + L::VP;
+    const int kv0 = it * KT;
+    f32x4 sc[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      sc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NKK; kk++) {
+        // dims past HD (head_dim 16: lane groups 2, 3) are zero in both
+        // operands; the MFMAs run on the whole wavefront
+        bf16x8 kh = {}, kl = {};
+        if (32 * kk + 8 * g < HD) {
+          const int off = krow[s] + (((4 * kk + g) ^ kx[s]) << 3);
+          kh = *(const bf16x8*)(khi + off);
+          kl = *(const bf16x8*)(klo + off);
+        }
+        sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[kk], sc[s], 0, 0, 0);
+        sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[kk], sc[s], 0, 0, 0);
+        sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[kk], sc[s], 0, 0, 0);
+      }
+    }
+    // Causal mask and online softmax of query t (base 2; lane groups g hold
+    // keys 8 g .. 8 g + 7 of the tile).
+    float pv[8];
+    float mx = -INFINITY;
+    if (kv0 + KT - 1 <= vis_all) {  // every key of the tile visible to every query of the block
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        pv[j] = sc[j >> 2][j & 3] * sl2;
+        mx = fmaxf(mx, pv[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float v = kv0 + 8 * g + j <= vis ? sc[j >> 2][j & 3] * sl2 : -INFINITY;
+        pv[j] = v;
+        mx = fmaxf(mx, v);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+    const float mn = fmaxf(m, mx);
+    const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float e = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pv[j] - mn);
+      pv[j] = e;
+      rs += e;
+    }
+    rs += __shfl_xor(rs, 16, WAVE);
+    rs += __shfl_xor(rs, 32, WAVE);
+    l = l * corr + rs;
+    m = mn;
+#pragma unroll
+    for (int j = 0; j < DJ; j++) o[j] *= corr;
+    bf16x8 ph, pl;
+    split8(pv, ph, pl);
+#pragma unroll
+    for (int dj = 0; dj < DJ; dj++) {
+      const bf16x8 vh = *(const bf16x8*)(vhi + vrow + 16 * dj * KT);
+      const bf16x8 vl = *(const bf16x8*)(vlo + vrow + 16 * dj * KT);
+      o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[dj], 0, 0, 0);
+      o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[dj], 0, 0, 0);
+      o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[dj], 0, 0, 0);
+    }
+    // Next tile: split the staged registers into the other buffer (last
+    // read in the previous iteration, before the barrier below it), then
+    // start loading the tile after it.
+    if (it + 1 < ntiles) {
+      store_tile(xl + ((it + 1) & 1) * L::buf);
+      if (it + 2 < ntiles) load_tile((it + 2) * KT);
+    }
+    __syncthreads();
+  }
+  // lane (g, c) holds O^T[16 dj + 4 g + e][t]: out[t][head*HD + 16 dj + 4 g + e]
   if (t < T) {
 #pragma unroll
     for (int j = 0; j < DJ; j++) {
@@ -581,6 +858,15 @@ void attention_init() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 64 * (int)sizeof(float)));
   HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_mfma_kernel<128>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 128 * (int)sizeof(float)));
+#define X3_ATTR(HD)                                                                  \
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_x3_kernel<HD>,             \
+                                hipFuncAttributeMaxDynamicSharedMemorySize,          \
+                                X3Lds<HD>::bytes));
+  X3_ATTR(16)
+  X3_ATTR(32)
+  X3_ATTR(64)
+  X3_ATTR(128)
+#undef X3_ATTR
 #define DECODE_ATTR(HD, GW)                                                                     \
   HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<HD, GW>,                        \
                                 hipFuncAttributeMaxDynamicSharedMemorySize,                     \
@@ -606,14 +892,32 @@ size_t attention_decode_lds_bytes(int hd) {
   }
 }
 
+// STRASGPT_PREFILL_ATTN=fp32 selects the fp32 matrix-core kernel; the
+// default is the split bf16 one (about 3x faster at long contexts).
+bool prefill_attn_fp32() {
+  const char* e = getenv("STRASGPT_PREFILL_ATTN");
+  if (!e || !*e || !strcmp(e, "x3")) return false;
+  if (!strcmp(e, "fp32")) return true;
+  ST_DIE("STRASGPT_PREFILL_ATTN must be x3 or fp32");
+}
+
 void attention_prefill(const AttnParams& p, hipStream_t s) {
+  attention_prefill_variant(p, prefill_attn_fp32() ? 1 : 0, s);
+}
+
+void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s) {
   if (p.T <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
   if (!p.out_hi) ST_DIE("prefill attention writes bf16 planes");
+  if (variant != 0 && variant != 1) ST_DIE("prefill attention variant is 0 (split bf16) or 1 (fp32)");
   dim3 grid((p.T + PQ - 1) / PQ, p.q_heads);
+  const bool fp32 = variant == 1;
   switch (p.hd) {
 #define PREFILL_CASE(HD)                                                                         \
   case HD:                                                                                       \
-    hipLaunchKernelGGL(attn_prefill_mfma_kernel<HD>, grid, dim3(256), 4 * PK * HD * sizeof(float), s, p); \
+    if (fp32)                                                                                    \
+      hipLaunchKernelGGL(attn_prefill_mfma_kernel<HD>, grid, dim3(256), 4 * PK * HD * sizeof(float), s, p); \
+    else                                                                                         \
+      hipLaunchKernelGGL(attn_prefill_x3_kernel<HD>, grid, dim3(256), X3Lds<HD>::bytes, s, p); \
     break;
     PREFILL_CASE(16)
     PREFILL_CASE(32)

@@ -412,3 +412,50 @@ extern "C" int strasgpt_kbench_gemm(int m, int n, int k, int precision, int vari
   HIP_CHECK(hipStreamDestroy(s));
   return 0;
 }
+
+extern "C" int strasgpt_kbench_attn_prefill(int T, int P, int q_heads, int kv_heads, int hd, int variant,
+                                            int iters, double* avg_us) {
+  if (T <= 0 || P < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || iters <= 0 ||
+      (hd != 16 && hd != 32 && hd != 64 && hd != 128) || (variant != 0 && variant != 1))
+    return -1;
+  hipStream_t s;
+  HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  const int ctx = P + T;
+  float *q, *kc, *vc;
+  uint16_t *hi, *lo;
+  int* pos;
+  const size_t nq = (size_t)T * q_heads * hd, nkv = (size_t)kv_heads * ctx * hd;
+  HIP_CHECK(hipMalloc(&q, nq * 4));
+  HIP_CHECK(hipMalloc(&kc, nkv * 4));
+  HIP_CHECK(hipMalloc(&vc, nkv * 4));
+  HIP_CHECK(hipMalloc(&hi, nq * 2));
+  HIP_CHECK(hipMalloc(&lo, nq * 2));
+  HIP_CHECK(hipMalloc(&pos, sizeof(int)));
+  hipLaunchKernelGGL(fill_f32, dim3(1024), dim3(256), 0, s, q, nq, 11u);
+  hipLaunchKernelGGL(fill_f32, dim3(1024), dim3(256), 0, s, kc, nkv, 12u);
+  hipLaunchKernelGGL(fill_f32, dim3(1024), dim3(256), 0, s, vc, nkv, 13u);
+  HIP_CHECK(hipMemcpyAsync(pos, &P, sizeof(int), hipMemcpyHostToDevice, s));
+  sg::AttnParams p{};
+  p.q = q;
+  p.kcache = kc;
+  p.vcache = vc;
+  p.out_hi = hi;
+  p.out_lo = lo;
+  p.pos = pos;
+  p.T = T;
+  p.q_heads = q_heads;
+  p.kv_heads = kv_heads;
+  p.hd = hd;
+  p.ctx = ctx;
+  p.q0 = 0;
+  *avg_us = time_launches(s, iters, [] {}, [&] { sg::attention_prefill_variant(p, variant, s); });
+  HIP_CHECK(hipStreamSynchronize(s));
+  HIP_CHECK(hipFree(q));
+  HIP_CHECK(hipFree(kc));
+  HIP_CHECK(hipFree(vc));
+  HIP_CHECK(hipFree(hi));
+  HIP_CHECK(hipFree(lo));
+  HIP_CHECK(hipFree(pos));
+  HIP_CHECK(hipStreamDestroy(s));
+  return 0;
+}

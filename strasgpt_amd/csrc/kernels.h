@@ -165,6 +165,8 @@ struct AttnParams {
   unsigned* counters;    // [kv_heads], zero between launches
 };
 void attention_prefill(const AttnParams& p, hipStream_t s);
+// variant 0: split-bf16 matrix cores, 1: fp32 matrix cores
+void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s);
 void attention_decode(const AttnParams& p, hipStream_t s);
 int attention_decode_chunks(int kv_heads);
 // Sets the decode kernels' LDS limits; called once per device before use.

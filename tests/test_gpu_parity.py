@@ -80,6 +80,29 @@ def test_gemm_tile_shapes(name, tile, model_dir, monkeypatch):
         assert tokens == [int(v) for v in g["generated"]]
 
 
+@pytest.mark.parametrize("kernel", ["x3", "fp32"])
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk"])
+def test_prefill_attention_kernels(name, kernel, model_dir, monkeypatch):
+    """Both prefill attention kernels (STRASGPT_PREFILL_ATTN): split-bf16
+    matrix-core products (x3, the default; head_dim 16 pads the 32-dim
+    k-step with zeros) and fp32 matrix-core products, over head_dim 16
+    (tiny-llama) and 32 (tiny-qwen; tiny-chunk: 520 queries, several
+    query blocks and key tiles). Logits and tokens as in test_tiny_golden."""
+    rt = runtime()
+    g = np.load(os.path.join(GOLDEN_DIR, f"{name}.npz"))
+    prompt = [int(v) for v in g["prompt"]]
+    monkeypatch.setenv("STRASGPT_PREFILL_ATTN", kernel)
+    with rt.Transformer(model_dir(name)) as t:
+        logits = t.predict(prompt)
+        err = np.abs(logits[0] - g["logits"]).max()
+        log(f"{name} {kernel}: max |logit error| {err:.3g}")
+        np.testing.assert_allclose(logits[0], g["logits"], rtol=RTOL, atol=ATOL)
+        assert err < 5e-4
+        t.reset()
+        tokens, _ = t.generate(prompt, len(g["generated"]))
+        assert tokens == [int(v) for v in g["generated"]]
+
+
 @pytest.mark.parametrize("chunk", ["512", "600"])
 def test_prefill_chunk_lengths(chunk, model_dir, monkeypatch):
     """The 520-token prompt of tiny-chunk in device chunks of 512 (two
