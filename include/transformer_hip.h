@@ -144,6 +144,19 @@ int transformer_profile_read(
     transformer_t* transformer, int kernel_class, transformer_kernel_stat_t* out
 );
 
+/* Sustained rate of one decode kernel class: `reps` passes of back-to-back
+ * launches over every layer's weights (same shapes and inputs as a decode
+ * step), bracketed by one pair of events on the library's stream. Writes
+ * the average duration per launch (one inter-kernel gap included, as in a
+ * decode step) and the algorithmic bytes per launch. Supported for the
+ * dense gate/up GEMV (TRANSFORMER_K_GATE_UP_GEMV), whose launches write
+ * only scratch activations; returns -1 for other classes. No reference
+ * counterpart (measurement hook). */
+int transformer_kernel_rate(
+    transformer_t* transformer, int kernel_class, int reps, double* avg_us,
+    double* bytes_per_launch
+);
+
 /* Library build identification (gfx target, kernel variants). */
 const char* transformer_hip_version(void);
 

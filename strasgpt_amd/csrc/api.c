@@ -108,3 +108,9 @@ int transformer_profile_read(transformer_t* transformer, int kernel_class,
   if (!transformer || !out) return -1;
   return sg_profile_read(transformer, kernel_class, out);
 }
+
+int transformer_kernel_rate(transformer_t* transformer, int kernel_class, int reps, double* avg_us,
+                            double* bytes_per_launch) {
+  if (!transformer || !avg_us || !bytes_per_launch) return -1;
+  return sg_kernel_rate(transformer, kernel_class, reps, avg_us, bytes_per_launch);
+}

@@ -35,6 +35,7 @@ void sg_decode_trace(transformer_t* t, int enable);
 int sg_decode_trace_read(transformer_t* t, double* us, int max_values);
 void sg_profile(transformer_t* t, int enable);
 int sg_profile_read(transformer_t* t, int kernel_class, transformer_kernel_stat_t* out);
+int sg_kernel_rate(transformer_t* t, int kernel_class, int reps, double* avg_us, double* bytes);
 
 #ifdef __cplusplus
 }

@@ -1480,6 +1480,42 @@ extern "C" void sg_profile(transformer_t* t, int enable) {
   D->prof = enable != 0;
 }
 
+extern "C" int sg_kernel_rate(transformer_t* t, int cls, int reps, double* avg_us, double* bytes) {
+  Dev* D = t->device;
+  if (cls != K_GU_GEMV || D->moe || reps <= 0) return -1;
+  hipStream_t s = D->stream;
+  const double d = D->d;
+  auto launch = [&](int l) {
+    sg::GemvParams f{};
+    f.w = W16(D, W_GATE, l);
+    f.w2 = W16(D, W_UP, l);
+    f.x = D->x;
+    f.norm_w = W16(D, W_FFN_NORM, l);
+    f.eps = D->eps;
+    f.N = D->H;
+    f.K = D->d;
+    f.y = D->act;  // scratch: the generation state is untouched
+    sg::gemv(f, sg::GEMV_SWIGLU, s);
+  };
+  HIP_CHECK(hipStreamSynchronize(s));
+  for (int l = 0; l < D->L; l++) launch(l);  // warm the code path
+  hipEvent_t a, b;
+  HIP_CHECK(hipEventCreate(&a));
+  HIP_CHECK(hipEventCreate(&b));
+  HIP_CHECK(hipEventRecord(a, s));
+  for (int r = 0; r < reps; r++)
+    for (int l = 0; l < D->L; l++) launch(l);
+  HIP_CHECK(hipEventRecord(b, s));
+  HIP_CHECK(hipEventSynchronize(b));
+  float ms = 0.f;
+  HIP_CHECK(hipEventElapsedTime(&ms, a, b));
+  HIP_CHECK(hipEventDestroy(a));
+  HIP_CHECK(hipEventDestroy(b));
+  *avg_us = ms * 1e3 / ((double)reps * D->L);
+  *bytes = 2.0 * D->H * d * 2;
+  return 0;
+}
+
 extern "C" int sg_profile_read(transformer_t* t, int cls, transformer_kernel_stat_t* out) {
   if (cls < 0 || cls >= TRANSFORMER_K_CLASS_COUNT) return -1;
   *out = t->device->stat[cls];

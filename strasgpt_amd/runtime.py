@@ -104,6 +104,8 @@ def lib():
     L.transformer_profile.argtypes = [TP, ctypes.c_int]
     L.transformer_profile_read.restype = ctypes.c_int
     L.transformer_profile_read.argtypes = [TP, ctypes.c_int, ctypes.POINTER(KernelStat)]
+    L.transformer_kernel_rate.restype = ctypes.c_int
+    L.transformer_kernel_rate.argtypes = [TP, ctypes.c_int, ctypes.c_int, dp, dp]
     _LIB = L
     return L
 
@@ -223,6 +225,15 @@ class Transformer:
 
     def profile(self, enable: bool):
         self._lib.transformer_profile(self._t, int(enable))
+
+    def kernel_rate(self, name: str, reps: int = 4):
+        """(avg_us, bytes_per_launch) of back-to-back launches of one decode
+        kernel class over every layer, or None where unsupported."""
+        us, by = ctypes.c_double(), ctypes.c_double()
+        cls = PROFILE_KERNELS.index(name)
+        if self._lib.transformer_kernel_rate(self._t, cls, reps, ctypes.byref(us), ctypes.byref(by)) != 0:
+            return None
+        return us.value, by.value
 
     def profile_read(self):
         out = {}
