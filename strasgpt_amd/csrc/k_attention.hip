@@ -260,16 +260,62 @@ __device__ __forceinline__ int x3_kswz(int key) {
 }
 __device__ __forceinline__ int x3_vswz(int d) { return (0 - (d >> 2)) & 3; }
 
+// Cache rows [r0, r1) of one kv head (blockIdx.y) into the bf16 planes:
+// 32 rows per block. K keeps its row layout; V goes through LDS and is
+// written transposed, 64 contiguous bytes (32 keys) per dim and plane.
+template <int HD>
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* kc, const float* vc, uint16_t* khi,
+                                                         uint16_t* klo, uint16_t* vthi, uint16_t* vtlo,
+                                                         int ctx, int ctx_pad, int r0, int r1) {
+  __shared__ float vs[32][HD + 1];
+  const int tid = threadIdx.x, h = blockIdx.y;
+  const int rb = r0 + blockIdx.x * 32;  // first row of the block
+  const size_t kbase = (size_t)h * ctx * HD;
+  for (int i = tid; i < 32 * HD / 2; i += 256) {
+    const int r = rb + (2 * i) / HD, dd = (2 * i) % HD;
+    if (r < r1) {
+      const float2 x = *(const float2*)(kc + kbase + (size_t)r * HD + dd);
+      uint32_t hi, lo;
+      split2(x.x, x.y, hi, lo);
+      *(uint32_t*)(khi + kbase + (size_t)r * HD + dd) = hi;
+      *(uint32_t*)(klo + kbase + (size_t)r * HD + dd) = lo;
+    }
+  }
+  for (int i = tid; i < 32 * HD; i += 256) {
+    const int r = rb + i / HD, dd = i % HD;
+    vs[i / HD][dd] = r < r1 ? vc[kbase + (size_t)r * HD + dd] : 0.0f;
+  }
+  __syncthreads();
+  const size_t vbase = (size_t)h * HD * ctx_pad;
+  for (int i = tid; i < HD * 16; i += 256) {
+    const int dd = i / 16, k2 = 2 * (i % 16);  // keys rb + k2, + 1
+    if (rb + k2 < r1) {  // r1 is even or the odd last key's partner is beyond r1 (zero)
+      uint32_t hi, lo;
+      split2(vs[k2][dd], vs[k2 + 1][dd], hi, lo);
+      if (rb + k2 + 1 >= r1) {  // keep the partner's stored value (not yet converted)
+        hi &= 0xFFFFu;
+        lo &= 0xFFFFu;
+        const size_t o = vbase + (size_t)dd * ctx_pad + rb + k2;
+        vthi[o] = (uint16_t)hi;
+        vtlo[o] = (uint16_t)lo;
+      } else {
+        *(uint32_t*)(vthi + vbase + (size_t)dd * ctx_pad + rb + k2) = hi;
+        *(uint32_t*)(vtlo + vbase + (size_t)dd * ctx_pad + rb + k2) = lo;
+      }
+    }
+  }
+}
+
 template <int HD>
 __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
   constexpr int KT = kX3Keys;              // keys per tile
   constexpr int NKK = (HD + 31) / 32;      // 32-dim k-steps of S
   constexpr int DJ = HD / 16;              // 16-dim sub-tiles of O
-  constexpr int CH = HD / 8;               // 16-byte chunks per K row
-  constexpr int NL = (KT * HD / 4 + 255) / 256;  // K float4s / V key quads per thread
   using L = X3Lds<HD>;
+  static_assert(L::KP % 512 == 0 && L::VP % 512 == 0, "planes split into 1 KiB DMA instructions");
+  constexpr int NKI = L::KP / 512, NVI = L::VP / 512;  // 1 KiB instructions per plane
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
-  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, g = lane / 16, c = lane % 16;
+  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, g = lane / 16, c = lane % 16;
   const int nqb = (p.T + PQ - 1) / PQ;
   const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
   const int head = blockIdx.y;
@@ -277,8 +323,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
   const int P = *p.pos + p.q0, T = p.T;
   const int qd = p.q_heads * HD;
   const int t = qb * PQ + wave * 16 + c;  // this lane's query
-  const float* kb = p.kcache + (size_t)kvh * p.ctx * HD;
-  const float* vb = p.vcache + (size_t)kvh * p.ctx * HD;
+  const uint16_t* khg = p.khi + (size_t)kvh * p.ctx * HD;
+  const uint16_t* klg = p.klo + (size_t)kvh * p.ctx * HD;
+  const uint16_t* vhg = p.vthi + (size_t)kvh * HD * p.ctx_pad;
+  const uint16_t* vlg = p.vtlo + (size_t)kvh * HD * p.ctx_pad;
   const int kv_end = P + min(qb * PQ + PQ, T);  // keys visible to the block's last query
   const int ntiles = (kv_end + KT - 1) / KT;
   // scores in the base-2 domain: s * log2(e) / sqrt(HD)
@@ -293,58 +341,31 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
     hi = __builtin_bit_cast(bf16x8, (uint4){h[0], h[1], h[2], h[3]});
     lo = __builtin_bit_cast(bf16x8, (uint4){l[0], l[1], l[2], l[3]});
   };
-  // Register staging of one tile: K float4 u (key u / (HD/4), dims 4 (u %
-  // (HD/4)) ..) and V key quad u (dim u % HD, keys 4 (u / HD) ..), for
-  // u = tid + 256 i < KT * HD / 4. Rows past the last visible key load that
-  // key (masked later).
-  float4 kr[NL];
-  float vr[NL][4];
-  auto load_tile = [&](int kv0) {
-#pragma unroll
-    for (int i = 0; i < NL; i++) {
-      const int u = tid + 256 * i;
-      if (KT * HD / 4 % 256 == 0 || u < KT * HD / 4) {
-        const int key = min(kv0 + u / (HD / 4), kv_end - 1);
-        kr[i] = *(const float4*)(kb + (size_t)key * HD + 4 * (u % (HD / 4)));
-        const int d = u % HD, k4 = kv0 + 4 * (u / HD);
-        if (k4 + 3 < kv_end) {  // whole quad visible: one address, constant row offsets
-          const float* vp = vb + (size_t)k4 * HD + d;
-#pragma unroll
-          for (int e = 0; e < 4; e++) vr[i][e] = vp[e * HD];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; e++) vr[i][e] = vb[(size_t)min(k4 + e, kv_end - 1) * HD + d];
-        }
-      }
+  // One tile's planes into LDS buffer buf by the global-to-LDS DMA: lane i
+  // of instruction n lands at plane element 512 n + 8 i and fetches the
+  // logical chunk that belongs there. K rows past the last visible key load
+  // that key (masked later); V^T rows cover keys kv0 .. kv0 + 31 < ctx_pad
+  // (entries never converted are zero, finite).
+  auto dma_tile = [&](int kv0, uint16_t* buf) {
+    for (int n = wave; n < NKI; n += 4) {
+      const int e = 512 * n + 8 * lane, row = e / HD, phys = (e % HD) / 8;
+      const int lc = phys ^ x3_kswz<HD>(row);
+      const size_t src = (size_t)min(kv0 + row, kv_end - 1) * HD + 8 * lc;
+      __builtin_amdgcn_global_load_lds((const void*)(khg + src), (lds_ptr)(buf + 512 * n), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(klg + src), (lds_ptr)(buf + L::KP + 512 * n), 16, 0, 0);
     }
-  };
-  auto store_tile = [&](uint16_t* buf) {
-    uint16_t* khi = buf;
-    uint16_t* klo = buf + L::KP;
-    uint16_t* vhi = buf + 2 * L::KP;
-    uint16_t* vlo = vhi + L::VP;
-#pragma unroll
-    for (int i = 0; i < NL; i++) {
-      const int u = tid + 256 * i;
-      if (KT * HD / 4 % 256 == 0 || u < KT * HD / 4) {
-        uint2 h, lo;
-        split2(kr[i].x, kr[i].y, h.x, lo.x);
-        split2(kr[i].z, kr[i].w, h.y, lo.y);
-        const int key = u / (HD / 4), d4 = u % (HD / 4);
-        const int off = key * HD + (((d4 >> 1) ^ x3_kswz<HD>(key)) << 3) + ((d4 & 1) << 2);
-        *(uint2*)(khi + off) = h;
-        *(uint2*)(klo + off) = lo;
-        split2(vr[i][0], vr[i][1], h.x, lo.x);
-        split2(vr[i][2], vr[i][3], h.y, lo.y);
-        const int d = u % HD, q4 = u / HD;  // key quad
-        const int voff = d * KT + (((q4 >> 1) ^ x3_vswz(d)) << 3) + ((q4 & 1) << 2);
-        *(uint2*)(vhi + voff) = h;
-        *(uint2*)(vlo + voff) = lo;
-      }
+    for (int n = wave; n < NVI; n += 4) {
+      const int e = 512 * n + 8 * lane, d = e / KT, phys = (e % KT) / 8;
+      const int lc = phys ^ x3_vswz(d);
+      const size_t src = (size_t)d * p.ctx_pad + kv0 + 8 * lc;
+      __builtin_amdgcn_global_load_lds((const void*)(vhg + src), (lds_ptr)(buf + 2 * L::KP + 512 * n), 16, 0,
+                                       0);
+      __builtin_amdgcn_global_load_lds((const void*)(vlg + src),
+                                       (lds_ptr)(buf + 2 * L::KP + L::VP + 512 * n), 16, 0, 0);
     }
   };
 
-  load_tile(0);
+  dma_tile(0, xl);
   // Q^T operand: lane (g, c) holds q[t][32 kk + 8 g .. + 7], split.
   bf16x8 qh[NKK], ql[NKK];
   {
@@ -363,9 +384,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
       split8(x, qh[kk], ql[kk]);
     }
   }
-  store_tile(xl);
-  if (ntiles > 1) load_tile(KT);
-  __syncthreads();
 
   f32x4 o[DJ];
 #pragma unroll
@@ -382,6 +400,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
   const int vrow = c * KT + ((g ^ x3_vswz(c)) << 3);  // + 16 dj * KT
 
   for (int it = 0; it < ntiles; it++) {
+    __builtin_amdgcn_s_waitcnt(0);  // this tile's DMA (and the q loads) landed
+    __syncthreads();                // for every wave; the other buffer is free
+    if (it + 1 < ntiles) dma_tile((it + 1) * KT, xl + ((it + 1) & 1) * L::buf);
     const uint16_t* buf = xl + (it & 1) * L::buf;
     const uint16_t* khi = buf;
     const uint16_t* klo = buf + L::KP;
@@ -452,14 +473,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
       o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[dj], 0, 0, 0);
       o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[dj], 0, 0, 0);
     }
-    // Next tile: split the staged registers into the other buffer (last
-    // read in the previous iteration, before the barrier below it), then
-    // start loading the tile after it.
-    if (it + 1 < ntiles) {
-      store_tile(xl + ((it + 1) & 1) * L::buf);
-      if (it + 2 < ntiles) load_tile((it + 2) * KT);
-    }
-    __syncthreads();
   }
   // lane (g, c) holds O^T[16 dj + 4 g + e][t]: out[t][head*HD + 16 dj + 4 g + e]
   if (t < T) {
@@ -905,9 +918,34 @@ void attention_prefill(const AttnParams& p, hipStream_t s) {
   attention_prefill_variant(p, prefill_attn_fp32() ? 1 : 0, s);
 }
 
+void attention_split_rows(const float* kcache, const float* vcache, uint16_t* khi, uint16_t* klo,
+                          uint16_t* vthi, uint16_t* vtlo, int kv_heads, int ctx, int ctx_pad, int hd,
+                          int r0, int r1, hipStream_t s) {
+  if (r0 % 32 || r0 < 0 || r1 > ctx || ctx_pad % 32 || ctx_pad < ctx)
+    ST_DIE("attention_split_rows: rows must start at a multiple of 32 and stay in the cache");
+  if (r1 <= r0) return;
+  const dim3 grid((r1 - r0 + 31) / 32, kv_heads);
+  switch (hd) {
+#define SPLIT_CASE(HD)                                                                                \
+  case HD:                                                                                            \
+    hipLaunchKernelGGL(split_rows_kernel<HD>, grid, dim3(256), 0, s, kcache, vcache, khi, klo, vthi, \
+                       vtlo, ctx, ctx_pad, r0, r1);                                                   \
+    break;
+    SPLIT_CASE(16)
+    SPLIT_CASE(32)
+    SPLIT_CASE(64)
+    SPLIT_CASE(128)
+#undef SPLIT_CASE
+    default: ST_DIE("attention supports head_dim 16, 32, 64 or 128");
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
 void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s) {
   if (p.T <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
   if (!p.out_hi) ST_DIE("prefill attention writes bf16 planes");
+  if (variant == 0 && (!p.khi || !p.klo || !p.vthi || !p.vtlo || p.ctx_pad % 32 || p.ctx_pad < p.ctx))
+    ST_DIE("split-bf16 prefill attention needs the cache's bf16 planes");
   if (variant != 0 && variant != 1) ST_DIE("prefill attention variant is 0 (split bf16) or 1 (fp32)");
   dim3 grid((p.T + PQ - 1) / PQ, p.q_heads);
   const bool fp32 = variant == 1;

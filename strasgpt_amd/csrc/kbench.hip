@@ -435,10 +435,25 @@ extern "C" int strasgpt_kbench_attn_prefill(int T, int P, int q_heads, int kv_he
   hipLaunchKernelGGL(fill_f32, dim3(1024), dim3(256), 0, s, kc, nkv, 12u);
   hipLaunchKernelGGL(fill_f32, dim3(1024), dim3(256), 0, s, vc, nkv, 13u);
   HIP_CHECK(hipMemcpyAsync(pos, &P, sizeof(int), hipMemcpyHostToDevice, s));
+  const int ctx_pad = (ctx + 31) / 32 * 32;
+  uint16_t *khi, *klo, *vhi, *vlo;
+  const size_t nvt = (size_t)kv_heads * hd * ctx_pad;
+  HIP_CHECK(hipMalloc(&khi, nkv * 2));
+  HIP_CHECK(hipMalloc(&klo, nkv * 2));
+  HIP_CHECK(hipMalloc(&vhi, nvt * 2));
+  HIP_CHECK(hipMalloc(&vlo, nvt * 2));
+  HIP_CHECK(hipMemsetAsync(vhi, 0, nvt * 2, s));
+  HIP_CHECK(hipMemsetAsync(vlo, 0, nvt * 2, s));
+  sg::attention_split_rows(kc, vc, khi, klo, vhi, vlo, kv_heads, ctx, ctx_pad, hd, 0, ctx, s);
   sg::AttnParams p{};
   p.q = q;
   p.kcache = kc;
   p.vcache = vc;
+  p.khi = khi;
+  p.klo = klo;
+  p.vthi = vhi;
+  p.vtlo = vlo;
+  p.ctx_pad = ctx_pad;
   p.out_hi = hi;
   p.out_lo = lo;
   p.pos = pos;
@@ -456,6 +471,10 @@ extern "C" int strasgpt_kbench_attn_prefill(int T, int P, int q_heads, int kv_he
   HIP_CHECK(hipFree(hi));
   HIP_CHECK(hipFree(lo));
   HIP_CHECK(hipFree(pos));
+  HIP_CHECK(hipFree(khi));
+  HIP_CHECK(hipFree(klo));
+  HIP_CHECK(hipFree(vhi));
+  HIP_CHECK(hipFree(vlo));
   HIP_CHECK(hipStreamDestroy(s));
   return 0;
 }

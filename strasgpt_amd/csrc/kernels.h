@@ -160,6 +160,13 @@ struct AttnParams {
   float eps;
   const float* rope;
   int pair_bound, pair_offset, pair_stride;
+  // prefill, split-bf16 kernel: the layer's cache rows as bf16 planes,
+  // K [kv_heads][ctx][hd] (hi, lo) and V transposed [kv_heads][hd][ctx_pad]
+  const uint16_t* khi;
+  const uint16_t* klo;
+  const uint16_t* vthi;
+  const uint16_t* vtlo;
+  int ctx_pad;           // ctx rounded up to a multiple of 32
   float* partial;        // [q_heads][splits][hd + 2]
   int splits;            // key chunks per kv head, at most (attention_decode_chunks)
   unsigned* counters;    // [kv_heads], zero between launches
@@ -167,6 +174,11 @@ struct AttnParams {
 void attention_prefill(const AttnParams& p, hipStream_t s);
 // variant 0: split-bf16 matrix cores, 1: fp32 matrix cores
 void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s);
+// Cache rows [r0, r1) of every kv head of one layer into the bf16 planes the
+// split-bf16 prefill kernel reads (AttnParams khi .. vtlo).
+void attention_split_rows(const float* kcache, const float* vcache, uint16_t* khi, uint16_t* klo,
+                          uint16_t* vthi, uint16_t* vtlo, int kv_heads, int ctx, int ctx_pad, int hd,
+                          int r0, int r1, hipStream_t s);
 void attention_decode(const AttnParams& p, hipStream_t s);
 int attention_decode_chunks(int kv_heads);
 // Sets the decode kernels' LDS limits; called once per device before use.

@@ -153,6 +153,12 @@ struct transformer_device {
   unsigned long long* dec_trace = nullptr;  // phase tracer (see sg_decode_trace)
   size_t dec_trace_steps = 0;
   float *kc = nullptr, *vc = nullptr, *rope = nullptr;
+  // The cache rows as bf16 hi/lo planes for the split-bf16 prefill
+  // attention: K [L][kvh][ctx][hd], V transposed [L][kvh][hd][ctx_pad];
+  // zero-initialised, rows [0, split_pos) converted (every layer).
+  uint16_t *kp_hi = nullptr, *kp_lo = nullptr, *vt_hi = nullptr, *vt_lo = nullptr;
+  int ctx_pad = 0;
+  size_t split_pos = 0;
   int *tok = nullptr, *pos = nullptr, *next = nullptr, *seq = nullptr, *seq_len = nullptr;
   int seq_cap = 0;
   float* attn_part = nullptr;
@@ -592,7 +598,21 @@ int residual_gemm(Dev* D, const uint16_t* a_hi, const uint16_t* a_lo, int lda,
   return splits;
 }
 
-constexpr int kAttnRows = 512;  // queries per prefill attention launch
+// Queries per prefill attention launch (measured on the 8192-token chunk):
+// 512 for the fp32 kernel (one block per CU: a launch over a long chunk
+// balances its causal ranges less well); 2048 for the split-bf16 kernel,
+// which holds two blocks per CU (512-query launches leave half of them
+// empty: 3.5 vs 2.5 ms per layer). STRASGPT_ATTN_ROWS overrides (>= 64).
+int attn_rows() {
+  const char* e = getenv("STRASGPT_ATTN_ROWS");
+  if (e && *e) {
+    const int v = atoi(e);
+    if (v < 64) ST_DIE("STRASGPT_ATTN_ROWS must be at least 64");
+    return v;
+  }
+  const char* k = getenv("STRASGPT_PREFILL_ATTN");
+  return k && !strcmp(k, "fp32") ? 512 : 2048;
+}
 
 // One layer over T > 1 rows. On entry D->xn_hi/lo hold the layer's input
 // RMSNorm; on exit x holds the layer output and, if next_norm is given, the
@@ -632,10 +652,27 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
                      D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
                      D->po, D->pst, s);
   }
+  // cache rows not yet in the bf16 planes: this chunk's, and any written by
+  // decode steps since the last prefill (from a multiple of 32)
+  const size_t P0 = D->host_pos;
+  const size_t vt_layer = (size_t)D->kvh * D->hd * D->ctx_pad;
+  {
+    const int r0 = (int)(std::min(D->split_pos, P0) / 32 * 32), r1 = (int)(P0 + T);
+    Prof pr(D, K_ELEM, 2.0 * (r1 - r0) * D->kvd * 4 * 2, 0);
+    sg::attention_split_rows(kc, vc, D->kp_hi + l * cache_layer, D->kp_lo + l * cache_layer,
+                             D->vt_hi + l * vt_layer, D->vt_lo + l * vt_layer, D->kvh, D->ctx,
+                             D->ctx_pad, D->hd, r0, r1, s);
+  }
+  if (l == D->L - 1) D->split_pos = P0 + T;
   sg::AttnParams a{};
   a.q = D->q;
   a.kcache = kc;
   a.vcache = vc;
+  a.khi = D->kp_hi + l * cache_layer;
+  a.klo = D->kp_lo + l * cache_layer;
+  a.vthi = D->vt_hi + l * vt_layer;
+  a.vtlo = D->vt_lo + l * vt_layer;
+  a.ctx_pad = D->ctx_pad;
   a.out_hi = D->att_hi;
   a.out_lo = split ? D->att_lo : nullptr;
   a.pos = D->pos;
@@ -649,12 +686,12 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
     const double pairs = M * (double)D->host_pos + M * (M + 1) / 2;
     Prof pr(D, K_ATT_PRE, 2.0 * D->kvh * ((double)D->host_pos + M) * D->hd * 4,
             4.0 * D->qh * D->hd * pairs);
-    // launches of at most kAttnRows queries (one launch over a long chunk
-    // balances its causal ranges less well)
-    for (int q0 = 0; q0 < T; q0 += kAttnRows) {
+    // launches of at most attn_rows() queries
+    const int rows = attn_rows();
+    for (int q0 = 0; q0 < T; q0 += rows) {
       sg::AttnParams b = a;
       b.q0 = q0;
-      b.T = std::min(kAttnRows, T - q0);
+      b.T = std::min(rows, T - q0);
       b.q = D->q + (size_t)q0 * D->qd;
       b.out_hi = D->att_hi + (size_t)q0 * D->qd;
       b.out_lo = split ? D->att_lo + (size_t)q0 * D->qd : nullptr;
@@ -1199,6 +1236,18 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->vc = dalloc<float>(cache);
   HIP_CHECK(hipMemsetAsync(D->kc, 0, cache * sizeof(float), D->stream));
   HIP_CHECK(hipMemsetAsync(D->vc, 0, cache * sizeof(float), D->stream));
+  D->ctx_pad = (D->ctx + 31) / 32 * 32;
+  {
+    const size_t kn = cache, vn = (size_t)D->L * D->kvh * D->hd * D->ctx_pad;
+    D->kp_hi = dalloc<uint16_t>(kn);
+    D->kp_lo = dalloc<uint16_t>(kn);
+    D->vt_hi = dalloc<uint16_t>(vn);
+    D->vt_lo = dalloc<uint16_t>(vn);
+    HIP_CHECK(hipMemsetAsync(D->kp_hi, 0, kn * 2, D->stream));
+    HIP_CHECK(hipMemsetAsync(D->kp_lo, 0, kn * 2, D->stream));
+    HIP_CHECK(hipMemsetAsync(D->vt_hi, 0, vn * 2, D->stream));
+    HIP_CHECK(hipMemsetAsync(D->vt_lo, 0, vn * 2, D->stream));
+  }
   std::vector<float> rope;
   build_rope_table(c, rope);
   D->rope = dalloc<float>(rope.size());
@@ -1258,6 +1307,7 @@ extern "C" void sg_free(transformer_t* t) {
     void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
                     D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part, D->attn_cnt,
                     D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
+                    D->kp_hi, D->kp_lo, D->vt_hi, D->vt_lo,
                     D->moe_sel, D->moe_w, D->moe_act, D->moe_logits, D->moe_offs, D->moe_order, D->moe_out,
                     D->xn_hi, D->xn_lo,
                     D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws,
