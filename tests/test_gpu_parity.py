@@ -174,6 +174,31 @@ def test_predict_host_loop_equals_device_loop(model_dir):
     assert host == dev
 
 
+@pytest.mark.parametrize("name", ["tiny-chunk", "tiny-long"])
+def test_prefill_after_decode_steps(name, model_dir):
+    """A prompt fed as one prefill, and as a prefill of its first 37 tokens,
+    then 11 single-token steps (the decode path, which writes cache rows
+    without converting them to the prefill attention's bf16 planes), then
+    one chunk of the rest: the second prefill converts the rows the decode
+    steps wrote (from a multiple of 32) before attending to them. Last-row
+    logits agree within 2e-3 of their largest magnitude (different kernels
+    and summation orders; rows left out of the planes read as zero and move
+    the logits by orders of magnitude more)."""
+    rt = runtime()
+    prompt = synth.prompt_tokens(128, 300 if name == "tiny-chunk" else 600, 23)
+    with rt.Transformer(model_dir(name)) as t:
+        whole = t.predict(prompt)[0]
+        t.reset()
+        t.predict(prompt[:37])
+        for tok in prompt[37:48]:
+            t.predict([tok])
+        parts = t.predict(prompt[48:])[0]
+    err = np.abs(parts - whole).max()
+    scale = max(1.0, float(np.abs(whole).max()))
+    log(f"{name}: max |logit difference| {err:.3g} (largest |logit| {scale:.3g})")
+    assert err <= 2e-3 * scale
+
+
 @pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk", "tiny-long"])
 def test_decode_modes_agree(name, model_dir):
     """The persistent decode step (one launch per token), the graph-replayed
