@@ -753,6 +753,271 @@ __global__ __launch_bounds__(256) void group_gemm_kernel(MoeGemmParams p) {
     }
 }
 
+// ------------------------------------- prefill: pipelined grouped GEMM --
+//
+// Same product as group_gemm_kernel, restructured for the memory system:
+// * A (the slots' activation rows) comes pre-split into bf16 hi/lo planes in
+//   expert order (moe_gather_split), so a tile's rows are contiguous and go
+//   to LDS by the global-to-LDS DMA in 128-byte row segments (K steps of
+//   64), 3-stage ring;
+// * the MXFP4 code bytes of the tile's 128 weight rows (gate 64 + up 64, or
+//   128 rows of one matrix, 4 KiB per step) stream through a 3-stage DMA
+//   ring, codes of step t + QNB - QNA + 1 issued with the A rows of step t;
+//   the rows' E8M0 scales are DMA'd once per block;
+// * per step every thread decodes one 32-value block (hardware FP4
+//   conversion, exact in bf16) into the next bf16 B tile while the waves
+//   multiply the current one: 32 slots (experts average about 32 slots per
+//   chunk: 64-slot tiles would be half empty) x 128 rows x 64 K, 16 MFMAs
+//   per wave (2 x 2 waves: 16 slots x 32 output columns of each matrix);
+//   80 KiB of LDS at K = 2880, two blocks per CU (a second wave per SIMD
+//   overlaps each step's decode and LDS round trips).
+// Each step issues exactly QAI A + 1 code DMA instructions per wave
+// (indexes past the last step are clamped to it and never read), so the
+// wait before a step is a constant: the groups of the QNA - 2 later steps
+// may stay in flight.
+constexpr int QBM = 32, QKS = 64, QBR = 128;  // slots, K per step, weight rows per block
+constexpr int QNA = 3, QNB = 3;              // A ring, code ring stages
+constexpr int QAI = 2 * QBM * QKS * 2 / 1024 / 4;  // A DMA instructions per wave and step
+constexpr int kQMaxNb = 256;                  // K / 32 <= 256 (scales per row)
+
+// Scale bytes per run (one run per matrix): rows x nb, in whole 1 KiB DMA
+// instructions so that the runs' tails never overlap.
+__host__ __device__ constexpr int q_scale_run(int rows, int nb) { return (rows * nb + 1023) / 1024 * 1024; }
+
+struct QLds {
+  static constexpr int a_stage = 2 * QBM * QKS * 2;  // hi + lo rows of 128 bytes
+  static constexpr int b_stage = QBR * 32;           // 2 code blocks per row
+  static constexpr int bt = QBR * QKS * 2;           // bf16 B tile
+  static constexpr int a = 0;
+  static constexpr int b = a + QNA * a_stage;
+  static constexpr int tile = b + QNB * b_stage;
+  static constexpr int sc = tile + 2 * bt;           // scales: QBR rows x nb bytes
+};
+
+__device__ __forceinline__ int q_swz(int r) { return (r >> 1) & 7; }  // 128-byte rows
+
+// LDS reads of DMA-written data use vector types: through HIP's uint4
+// struct the compiler waits for every DMA in flight before the read (the
+// explicit waits and barriers order the data).
+typedef unsigned q_u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool DUAL>
+__global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
+  // one LDS object (a second one makes the compiler wait for every LDS DMA
+  // before any LDS read); the tile lookup result sits in the B tile area,
+  // which is first written after it has been read
+  extern __shared__ __attribute__((aligned(1024))) unsigned char ql[];
+  int* tile_info = (int*)(ql + QLds::tile);
+  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+  const int wm = wave / 2, wn = wave % 2;
+  if (wave == 0) {
+    int e_found = -1, m0 = 0, base = 0;
+    for (int e0 = 0; e0 < p.E && e_found < 0; e0 += WAVE) {
+      const int e = e0 + lane;
+      const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
+      int tiles = (c + QBM - 1) / QBM, incl = tiles;
+#pragma unroll
+      for (int off = 1; off < WAVE; off <<= 1) {
+        const int v = __shfl_up(incl, off, WAVE);
+        if (lane >= off) incl += v;
+      }
+      const int excl = base + incl - tiles;
+      const bool mine = (int)blockIdx.x >= excl && (int)blockIdx.x < excl + tiles;
+      const unsigned long long m = __ballot(mine);
+      if (m) {
+        const int src = __ffsll((long long)m) - 1;
+        e_found = __shfl(e0 + lane, src, WAVE);
+        m0 = ((int)blockIdx.x - __shfl(excl, src, WAVE)) * QBM;
+      }
+      base += __shfl(incl, WAVE - 1, WAVE);
+    }
+    if (lane == 0) {
+      tile_info[0] = e_found;
+      tile_info[1] = m0;
+    }
+  }
+  __syncthreads();
+  const int e = tile_info[0], m0 = tile_info[1];
+  __syncthreads();  // every thread has read tile_info before decode(0) writes the B tile
+  if (e < 0) return;  // past the last tile (the grid is an upper bound)
+  const int rbeg = p.offs[e], cnt = p.offs[e + 1] - rbeg;
+  const int cols = DUAL ? QBR / 2 : QBR;  // output columns per block
+  const int n0 = blockIdx.y * cols;
+  const int K = p.K, nb = K / 32, nk = K / QKS;
+
+  // --- DMA sources (per lane) ---
+  // A: instruction i (< QAI) of this wave covers stage rows 8 (QAI wave + i)
+  // .., rows 0..QBM-1 hi, QBM..2 QBM-1 lo; lane -> row + lane / 8, physical
+  // chunk lane % 8.
+  const uint16_t* asrc[QAI];
+#pragma unroll
+  for (int i = 0; i < QAI; i++) {
+    const int row = 8 * (QAI * wave + i) + lane / 8;
+    const int c = (lane % 8) ^ q_swz(row);
+    const int r = row % QBM;
+    const int grow = rbeg + min(m0 + r, cnt - 1);  // rows past the tile load its last row
+    asrc[i] = (row < QBM ? p.a_hi : p.a_lo) + (size_t)grow * K + 8 * c;
+  }
+  // codes: instruction of wave w covers weight rows 32 w .. 32 w + 31, lane
+  // -> row 32 w + lane / 2, block lane % 2 of the step
+  const uint8_t* bsrc;
+  {
+    const int br = 32 * wave + lane / 2;
+    const bool up = DUAL && br >= QBR / 2;
+    const int n = min(n0 + (DUAL ? br % (QBR / 2) : br), p.N - 1);
+    bsrc = (up ? p.blocks2 : p.blocks) + ((size_t)e * p.N + n) * nb * 16 + (lane % 2) * 16;
+  }
+
+  // scales of the block's rows: per matrix a contiguous run of rows x nb
+  // bytes (16-byte aligned: the host checks N % 16 == 0), 1 KiB per
+  // instruction; lanes past the run read in-bounds bytes that are not used
+  {
+    const int runs = DUAL ? 2 : 1, rows = QBR / runs;
+    const int run = q_scale_run(rows, nb), ni = run / 1024;
+    const size_t off0 = ((size_t)e * p.N + n0) * nb;
+    const size_t limit = ((size_t)(e + 1) * p.N) * nb - 16;  // last 16-byte chunk of expert e's scales
+    for (int rr = 0; rr < runs; rr++) {
+      const uint8_t* sb = rr == 0 ? p.scales : p.scales2;
+      for (int n = wave; n < ni; n += 4) {
+        const size_t o = min(off0 + (size_t)n * 1024 + 16 * lane, limit);
+        __builtin_amdgcn_global_load_lds((const void*)(sb + o), (lds_ptr)(ql + QLds::sc + rr * run + n * 1024),
+                                         16, 0, 0);
+      }
+    }
+  }
+  // decode of step t's codes (stage t % QNB) into B tile buffer t % 2:
+  // thread -> weight row tid / 2, block tid % 2 of the step
+  const int dr = tid / 2, dk = tid % 2;
+  const int srow = DUAL ? (dr / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (dr % (QBR / 2)) * nb : dr * nb;
+  auto decode = [&](int t) {  // codes of step t, into B tile buffer t % 2
+    const unsigned char* bs = ql + QLds::b + (t % QNB) * QLds::b_stage;
+    const q_u32x4 w = *(const q_u32x4*)(bs + dr * 32 + dk * 16);
+    const float sc = e8m0_scale(ql[QLds::sc + srow + 2 * t + dk]);
+    const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
+    uint32_t o[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float2v v0 = fp4_pair<0>(ww[i], sc), v1 = fp4_pair<1>(ww[i], sc);
+      const float2v v2 = fp4_pair<2>(ww[i], sc), v3 = fp4_pair<3>(ww[i], sc);
+      // exact in bf16 (E2M1 value x power of two): keep the high halves
+      o[4 * i + 0] = (__float_as_uint(v0.x) >> 16) | (__float_as_uint(v0.y) & 0xFFFF0000u);
+      o[4 * i + 1] = (__float_as_uint(v1.x) >> 16) | (__float_as_uint(v1.y) & 0xFFFF0000u);
+      o[4 * i + 2] = (__float_as_uint(v2.x) >> 16) | (__float_as_uint(v2.y) & 0xFFFF0000u);
+      o[4 * i + 3] = (__float_as_uint(v3.x) >> 16) | (__float_as_uint(v3.y) & 0xFFFF0000u);
+    }
+    unsigned char* bt = ql + QLds::tile + (t & 1) * QLds::bt + dr * 128;
+#pragma unroll
+    for (int c = 0; c < 4; c++)  // logical chunks 4 dk + c (8 values each)
+      *(q_u32x4*)(bt + (((4 * dk + c) ^ q_swz(dr)) << 4)) = (q_u32x4){o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
+  };
+  auto frag = [&](const unsigned char* base, int r, int j) -> bf16x8 {
+    const int c = 4 * j + lane / 16;
+    return *(const bf16x8*)(base + r * 128 + ((c ^ q_swz(r)) << 4));
+  };
+  // weight row of B fragment j of this wave
+  auto brow = [&](int j) -> int {
+    if (DUAL) return (j < 2 ? 0 : QBR / 2) + 32 * wn + 16 * (j % 2);
+    return 64 * wn + 16 * j;
+  };
+
+  constexpr int MI = QBM / 32;  // 16-slot sub-tiles per wave
+  f32x4 acc[MI][4];
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int fr = lane % 16;
+
+  // prologue: scales, codes(0 .. QNB - QNA), then groups
+  // [A(t), codes(t + QNB - QNA + 1)] for t < QNA - 1
+  auto issue_codes = [&](int c) {
+    const int tb = min(c, nk - 1);
+    unsigned char* bs = ql + QLds::b + (c % QNB) * QLds::b_stage;
+    __builtin_amdgcn_global_load_lds((const void*)(bsrc + (size_t)tb * 32), (lds_ptr)(bs + wave * 1024), 16, 0,
+                                     0);
+  };
+  auto issue_group = [&](int t) {  // A(t) then codes(t + QNB - QNA + 1), indexes clamped
+    const int tc = min(t, nk - 1);
+    unsigned char* as = ql + QLds::a + (t % QNA) * QLds::a_stage;
+#pragma unroll
+    for (int i = 0; i < QAI; i++)
+      __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + tc * QKS),
+                                       (lds_ptr)(as + (QAI * wave + i) * 1024), 16, 0, 0);
+    issue_codes(t + QNB - QNA + 1);
+  };
+  for (int c = 0; c <= QNB - QNA; c++) issue_codes(c);
+  for (int t = 0; t < QNA - 1; t++) issue_group(t);
+  wait_dma_behind<(QAI + 1) * (QNA - 1)>();  // scales and codes(0) landed
+  __syncthreads();
+  decode(0);
+  for (int kt = 0; kt < nk; kt++) {
+    // A(kt) was issued in the group of step kt - QNA + 1 (codes(kt + 1)
+    // earlier); the QNA - 2 later groups may stay in flight
+    wait_dma_behind<(QAI + 1) * (QNA - 2)>();
+    __syncthreads();  // B tile kt decoded by every thread; slots of step kt - 1 free
+    // group [A(kt + QNA - 1), codes(kt + QNB)]: A slot (kt - 1) % QNA (read
+    // at step kt - 1), code slot kt % QNB (decoded at step kt - 1)
+    issue_group(kt + QNA - 1);
+    if (kt + 1 < nk) decode(kt + 1);  // into the other B tile buffer
+    const unsigned char* as = ql + QLds::a + (kt % QNA) * QLds::a_stage;
+    const unsigned char* bt = ql + QLds::tile + (kt & 1) * QLds::bt;
+#pragma unroll
+    for (int ks = 0; ks < QKS / 32; ks++) {
+      bf16x8 b[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[j] = frag(bt, brow(j) + fr, ks);
+#pragma unroll
+      for (int mi = 0; mi < MI; mi++) {
+        const int r = (QBM / 2) * wm + 16 * mi + fr;
+        const bf16x8 ah = frag(as, r, ks), al = frag(as, QBM + r, ks);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          acc[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[j], acc[mi][j], 0, 0, 0);
+          acc[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], acc[mi][j], 0, 0, 0);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the clamped tail loads land before the wave ends
+  // lane holds C[4 (lane / 16) + i][lane % 16] of each 16 x 16 tile
+#pragma unroll
+  for (int mi = 0; mi < MI; mi++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = (QBM / 2) * wm + 16 * mi + (lane / 16) * 4 + i;
+      if (m0 + r >= cnt) continue;
+      const int s2 = p.order[rbeg + m0 + r];
+#pragma unroll
+      for (int j = 0; j < (DUAL ? 2 : 4); j++) {
+        const int n = n0 + (DUAL ? 32 * wn : 64 * wn) + 16 * j + lane % 16;
+        if (n >= p.N) continue;
+        p.y[(size_t)s2 * p.N + n] = DUAL ? silu_mul(acc[mi][j][i], acc[mi][j + 2][i]) : acc[mi][j][i];
+      }
+    }
+}
+
+// Rows of A in expert order as bf16 hi/lo planes: block i converts the row
+// of slot order[i].
+__global__ __launch_bounds__(256) void gather_split_kernel(MoeGemmParams p) {
+  const int i = blockIdx.x;
+  const int slot = p.order[i];
+  const float* src = p.a + (size_t)(p.a_per_token ? slot / p.topk : slot) * p.K;
+  uint16_t* hi = p.a_hi + (size_t)i * p.K;
+  uint16_t* lo = p.a_lo + (size_t)i * p.K;
+  for (int k = 4 * threadIdx.x; k < p.K; k += 4 * 256) {
+    const float4 x = *(const float4*)(src + k);
+    uint16_t h[4], l[4];
+    const float v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      h[j] = f32_to_bf16_rne(v[j]);
+      l[j] = f32_to_bf16_rne(v[j] - bf16_to_f32(h[j]));
+    }
+    *(uint2*)(hi + k) = make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+    *(uint2*)(lo + k) = make_uint2(l[0] | ((unsigned)l[1] << 16), l[2] | ((unsigned)l[3] << 16));
+  }
+}
+
 // x[t][n] += sum over j in top-k order of fmaf(w_j, out[t k + j][n], .).
 __global__ void combine_kernel(const float* out, const float* w, int T, int k, int N, float* x) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -857,8 +1122,36 @@ void moe_group(const int* sel, int n, int E, int* offs, int* order, hipStream_t 
   HIP_CHECK(hipGetLastError());
 }
 
+bool moe_group_gemm2_ok(const MoeGemmParams& p) {
+  return p.a_hi && p.a_lo && p.K % QKS == 0 && p.K / 32 <= kQMaxNb && p.N % 16 == 0 &&
+         !(((uintptr_t)p.blocks | (uintptr_t)p.scales | (uintptr_t)(p.blocks2 ? p.blocks2 : p.blocks) |
+            (uintptr_t)(p.scales2 ? p.scales2 : p.scales) | (uintptr_t)p.a_hi | (uintptr_t)p.a_lo) % 16);
+}
+
+void moe_gather_split(const MoeGemmParams& p, hipStream_t s) {
+  if (!p.a_hi || !p.a_lo || p.K % 4 || (uintptr_t)p.a % 16 || p.slots <= 0) ST_DIE("MoE gather: bad shape");
+  hipLaunchKernelGGL(gather_split_kernel, dim3(p.slots), dim3(256), 0, s, p);
+  HIP_CHECK(hipGetLastError());
+}
+
 void moe_group_gemm(const MoeGemmParams& p, hipStream_t s) {
   if (p.K % 32 || p.N <= 0 || p.slots <= 0) ST_DIE("MoE grouped GEMM shape");
+  if (moe_group_gemm2_ok(p)) {
+    const bool dual = p.blocks2 != nullptr;
+    const int nb = p.K / 32, runs = dual ? 2 : 1;
+    const size_t shm = QLds::sc + (size_t)runs * q_scale_run(QBR / runs, nb);
+    const int cols = dual ? QBR / 2 : QBR;
+    const dim3 grid((p.slots + QBM - 1) / QBM + p.E, (p.N + cols - 1) / cols);
+    if (dual) {
+      set_lds(group_gemm2_kernel<true>, shm);
+      hipLaunchKernelGGL(group_gemm2_kernel<true>, grid, dim3(256), shm, s, p);
+    } else {
+      set_lds(group_gemm2_kernel<false>, shm);
+      hipLaunchKernelGGL(group_gemm2_kernel<false>, grid, dim3(256), shm, s, p);
+    }
+    HIP_CHECK(hipGetLastError());
+    return;
+  }
   if (((uintptr_t)p.a % 16) || p.K % 4) ST_DIE("MoE grouped GEMM rows must be 16-byte aligned");
   const dim3 grid((p.slots + GBM - 1) / GBM + p.E, (p.N + GBN - 1) / GBN);
   if (p.blocks2)

@@ -74,8 +74,18 @@ struct MoeGemmParams {
   const int *offs, *order;           // moe_group output
   int slots, topk, E, N, K;
   float* y;                          // [slot][N]: silu(g) * u, or the product
+  // optional: the A rows gathered in expert order (row i = the row of slot
+  // order[i]) as bf16 hi/lo planes [slots][K] (moe_gather_split); with them
+  // the pipelined kernel runs (needs K % 64 == 0, N % 16 == 0)
+  uint16_t *a_hi, *a_lo;
 };
 void moe_group_gemm(const MoeGemmParams& p, hipStream_t s);
+// a_hi/a_lo[i] = split of the A row of slot order[i] (a[order[i] / topk] when
+// a_per_token, else a[order[i]]), i < slots.
+void moe_gather_split(const MoeGemmParams& p, hipStream_t s);
+// Whether moe_group_gemm takes the pipelined kernel for p (a_hi/a_lo set,
+// K % 64 == 0, K <= 8192, N % 16 == 0, 16-byte aligned operands).
+bool moe_group_gemm2_ok(const MoeGemmParams& p);
 // x[t][n] += sum_j in top-k order fmaf(w[t k + j], out[t k + j][n], .)
 void moe_combine(const float* out, const float* w, int T, int k, int N, float* x, hipStream_t s);
 // The device MXFP4 decode of the expert kernels on `nblocks` blocks of 32

@@ -179,6 +179,8 @@ struct transformer_device {
   int* moe_sel = nullptr;
   float* moe_w = nullptr;
   float* moe_act = nullptr;
+  // MoE prefill: the grouped GEMMs' A rows in expert order, bf16 hi/lo
+  uint16_t *moe_ahi = nullptr, *moe_alo = nullptr;
   float* moe_logits = nullptr;  // [E] router logits of a decode step
   int* moe_offs = nullptr;   // [E + 1] grouped prefill: slot ranges per expert
   int* moe_order = nullptr;  // [T * topk] slots sorted by expert
@@ -393,8 +395,12 @@ void ffn_moe(Dev* D, int l, int T) {
     g.N = D->H;
     g.K = D->d;
     g.y = D->moe_act;
+    g.a_hi = D->moe_ahi;
+    g.a_lo = D->moe_alo;
+    if (!sg::moe_group_gemm2_ok(g)) g.a_hi = g.a_lo = nullptr;
     {
       Prof pr(D, K_MOE_GU_PRE, used * mxfp4_bytes(2 * H * d), 4.0 * n * H * d);
+      if (g.a_hi) sg::moe_gather_split(g, s);
       sg::moe_group_gemm(g, s);
     }
     sg::MoeGemmParams dn{};
@@ -410,8 +416,12 @@ void ffn_moe(Dev* D, int l, int T) {
     dn.N = D->d;
     dn.K = D->H;
     dn.y = D->moe_out;
+    dn.a_hi = D->moe_ahi;
+    dn.a_lo = D->moe_alo;
+    if (!sg::moe_group_gemm2_ok(dn)) dn.a_hi = dn.a_lo = nullptr;
     {
       Prof pr(D, K_MOE_DOWN_PRE, used * mxfp4_bytes(H * d), 2.0 * n * H * d);
+      if (dn.a_hi) sg::moe_gather_split(dn, s);
       sg::moe_group_gemm(dn, s);
       sg::moe_combine(D->moe_out, D->moe_w, T, D->topk, D->d, D->x, s);
     }
@@ -1273,6 +1283,8 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
     D->moe_offs = dalloc<int>(D->E + 1);
     D->moe_order = dalloc<int>(T * D->topk);
     D->moe_out = dalloc<float>(T * D->topk * d);
+    D->moe_ahi = dalloc<uint16_t>((size_t)T * D->topk * std::max(d, H));
+    D->moe_alo = dalloc<uint16_t>((size_t)T * D->topk * std::max(d, H));
   }
   HIP_CHECK(hipHostMalloc((void**)&D->h_tok, T * sizeof(int), hipHostMallocDefault));
   HIP_CHECK(hipHostMalloc((void**)&D->h_pos, sizeof(int), hipHostMallocDefault));
@@ -1309,6 +1321,7 @@ extern "C" void sg_free(transformer_t* t) {
                     D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
                     D->kp_hi, D->kp_lo, D->vt_hi, D->vt_lo,
                     D->moe_sel, D->moe_w, D->moe_act, D->moe_logits, D->moe_offs, D->moe_order, D->moe_out,
+                    D->moe_ahi, D->moe_alo,
                     D->xn_hi, D->xn_lo,
                     D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws,
                     D->dec_layers, D->dec_buf, D->dec_am_i, D->dec_sync, D->dec_trace,
