@@ -35,31 +35,87 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const uint
 // 1439-1445, 1498-1504); then the reference RMSNorm (source/transformer.c:
 // 978-999) is written as fp32 and/or as the bf16 hi/lo planes that the next
 // GEMM consumes (hi = bf16(y), lo = bf16(y - hi)).
+// One block per row, the row held in registers (NV float4 per thread,
+// d <= 1024 NV): x and every split's partial are loaded before any is
+// used, then one reduction and the normalised stores. Partials are added in
+// split order.
+template <int NV>
 __global__ __launch_bounds__(256) void residual_norm_kernel(NormParams p) {
   __shared__ float red[4];
-  const int row = blockIdx.x, d = p.d;
-  float* xr = p.x + (size_t)row * d;
-  float ss = 0.0f;
-  for (int e = threadIdx.x; e < d; e += 256) {
-    float v = xr[e];
-    if (p.splits > 0) {
-      float o = p.part[(size_t)row * d + e];
-      for (int sp = 1; sp < p.splits; sp++) o += p.part[((size_t)sp * p.rows + row) * d + e];
-      v += o;
-      xr[e] = v;
+  const int row = blockIdx.x, d4 = p.d / 4, tid = threadIdx.x;
+  float4* xr = (float4*)(p.x + (size_t)row * p.d);
+  float4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int e = tid + 256 * i;
+    v[i] = e < d4 ? xr[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (p.splits > 0) {
+    float4 o[NV];
+    const float4* p0 = (const float4*)(p.part + (size_t)row * p.d);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = tid + 256 * i;
+      o[i] = e < d4 ? p0[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    ss = fmaf(v, v, ss);
+    for (int sp = 1; sp < p.splits; sp++) {
+      const float4* ps = (const float4*)(p.part + ((size_t)sp * p.rows + row) * p.d);
+#pragma unroll
+      for (int i = 0; i < NV; i++) {
+        const int e = tid + 256 * i;
+        if (e < d4) {
+          const float4 q = ps[e];
+          o[i].x += q.x;
+          o[i].y += q.y;
+          o[i].z += q.z;
+          o[i].w += q.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = tid + 256 * i;
+      if (e < d4) {
+        v[i].x += o[i].x;
+        v[i].y += o[i].y;
+        v[i].z += o[i].z;
+        v[i].w += o[i].w;
+        xr[e] = v[i];
+      }
+    }
   }
   if (!p.w) return;
-  const float s = rms_scale(block_sum<256>(ss, red), d, p.eps);
-  for (int e = threadIdx.x; e < d; e += 256) {
-    const float y = (xr[e] * s) * bf16_to_f32(p.w[e]);
-    const size_t i = (size_t)row * d + e;
-    if (p.y) p.y[i] = y;
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    ss = fmaf(v[i].x, v[i].x, ss);
+    ss = fmaf(v[i].y, v[i].y, ss);
+    ss = fmaf(v[i].z, v[i].z, ss);
+    ss = fmaf(v[i].w, v[i].w, ss);
+  }
+  const float s = rms_scale(block_sum<256>(ss, red), p.d, p.eps);
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int e = tid + 256 * i;
+    if (e >= d4) continue;
+    const uint2 w2 = *(const uint2*)(p.w + 4 * e);
+    const float wv[4] = {__uint_as_float(w2.x << 16), __uint_as_float(w2.x & 0xFFFF0000u),
+                         __uint_as_float(w2.y << 16), __uint_as_float(w2.y & 0xFFFF0000u)};
+    const float xv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) y[j] = (xv[j] * s) * wv[j];
+    const size_t idx = (size_t)row * p.d + 4 * e;
+    if (p.y) *(float4*)(p.y + idx) = make_float4(y[0], y[1], y[2], y[3]);
     if (p.y_hi) {
-      const uint16_t h = f32_to_bf16_rne(y);
-      p.y_hi[i] = h;
-      if (p.y_lo) p.y_lo[i] = f32_to_bf16_rne(y - bf16_to_f32(h));
+      uint16_t h[4], l[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        h[j] = f32_to_bf16_rne(y[j]);
+        l[j] = f32_to_bf16_rne(y[j] - bf16_to_f32(h[j]));
+      }
+      *(uint2*)(p.y_hi + idx) = make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+      if (p.y_lo) *(uint2*)(p.y_lo + idx) = make_uint2(l[0] | ((unsigned)l[1] << 16), l[2] | ((unsigned)l[3] << 16));
     }
   }
 }
@@ -200,7 +256,18 @@ void rmsnorm_rows(const float* x, const uint16_t* w, float* y, int rows, int d, 
 void residual_norm(const NormParams& p, hipStream_t s) {
   if (p.rows <= 0 || p.d <= 0) ST_DIE("residual_norm needs rows, d > 0");
   if (p.splits > 0 && !p.part) ST_DIE("residual_norm needs the partial sums");
-  hipLaunchKernelGGL(residual_norm_kernel, dim3(p.rows), dim3(256), 0, s, p);
+  if (p.d % 4 || p.d > 8192) ST_DIE("residual_norm needs d % 4 == 0 and d <= 8192");
+  if ((uintptr_t)p.x % 16 || (p.part && (uintptr_t)p.part % 16) || (p.y && (uintptr_t)p.y % 16) ||
+      (p.y_hi && (uintptr_t)p.y_hi % 8) || (p.y_lo && (uintptr_t)p.y_lo % 8) || (p.w && (uintptr_t)p.w % 8))
+    ST_DIE("residual_norm operands must be aligned");
+  const int nv = (p.d / 4 + 255) / 256;
+  switch (nv) {
+#define RN_CASE(N) \
+  case N: hipLaunchKernelGGL(residual_norm_kernel<N>, dim3(p.rows), dim3(256), 0, s, p); break;
+    RN_CASE(1) RN_CASE(2) RN_CASE(3) RN_CASE(4) RN_CASE(5) RN_CASE(6) RN_CASE(7) RN_CASE(8)
+#undef RN_CASE
+    default: ST_DIE("residual_norm: row too long");
+  }
   HIP_CHECK(hipGetLastError());
 }
 
