@@ -36,10 +36,12 @@ constexpr int kDecMinChunk = 32;  // keys per chunk, at least
 
 // Split of `total` keys into nch chunks of len keys (the last may be
 // shorter, none is empty): as many chunks as allowed, each of at least
-// kDecMinChunk keys.
+// kDecMinChunk keys and a whole number of kDecTile-key tiles (a chunk of 33
+// keys would cost two tile steps for one key more).
 __host__ __device__ inline void attention_decode_split(int total, int max_chunks, int& nch, int& len) {
   nch = total < max_chunks * kDecMinChunk ? (total + kDecMinChunk - 1) / kDecMinChunk : max_chunks;
   len = (total + nch - 1) / nch;
+  len = (len + kDecTile - 1) / kDecTile * kDecTile;
   nch = (total + len - 1) / len;
 }
 
