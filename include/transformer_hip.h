@@ -149,8 +149,10 @@ int transformer_profile_read(
  * step), bracketed by one pair of events on the library's stream. Writes
  * the average duration per launch (one inter-kernel gap included, as in a
  * decode step) and the algorithmic bytes per launch. Supported for the
- * dense gate/up GEMV (TRANSFORMER_K_GATE_UP_GEMV), whose launches write
- * only scratch activations; returns -1 for other classes. No reference
+ * dense gate/up GEMV (TRANSFORMER_K_GATE_UP_GEMV) and the MoE expert
+ * gate/up GEMV (TRANSFORMER_K_MOE_GATE_UP; experts from the last step's
+ * router logits, the same for every layer), whose launches write only
+ * scratch activations; returns -1 for other classes. No reference
  * counterpart (measurement hook). */
 int transformer_kernel_rate(
     transformer_t* transformer, int kernel_class, int reps, double* avg_us,

@@ -1545,10 +1545,33 @@ extern "C" void sg_profile(transformer_t* t, int enable) {
 
 extern "C" int sg_kernel_rate(transformer_t* t, int cls, int reps, double* avg_us, double* bytes) {
   Dev* D = t->device;
-  if (cls != K_GU_GEMV || D->moe || reps <= 0) return -1;
+  const bool dense = cls == K_GU_GEMV && !D->moe, moe = cls == K_MOE_GU && D->moe;
+  if (!(dense || moe) || reps <= 0) return -1;
   hipStream_t s = D->stream;
   const double d = D->d;
+  // MoE: the decode launch of one token, experts from the router logits (or
+  // selection) left by the last step, the same for every layer; each
+  // layer's experts are its own weights, so every launch streams from HBM.
+  const bool fused = sg::moe_route_logits_supported(D->E, D->topk, D->d);
+  if (moe && !fused) return -1;  // the selection buffer may not hold valid expert ids yet
   auto launch = [&](int l) {
+    if (moe) {
+      sg::MoeGemvParams g{};
+      g.blocks = W8(D, W_GB, l);
+      g.scales = W8(D, W_GS, l);
+      g.blocks2 = W8(D, W_UB, l);
+      g.scales2 = W8(D, W_US, l);
+      g.x = D->xn;
+      g.logits = D->moe_logits;  // top-k in the kernel: ids always in [0, E)
+      g.E = D->E;
+      g.tokens = 1;
+      g.topk = D->topk;
+      g.N = D->H;
+      g.K = D->d;
+      g.y = D->moe_act;  // scratch: the generation state is untouched
+      sg::moe_gemv_swiglu(g, s);
+      return;
+    }
     sg::GemvParams f{};
     f.w = W16(D, W_GATE, l);
     f.w2 = W16(D, W_UP, l);
@@ -1575,7 +1598,7 @@ extern "C" int sg_kernel_rate(transformer_t* t, int cls, int reps, double* avg_u
   HIP_CHECK(hipEventDestroy(a));
   HIP_CHECK(hipEventDestroy(b));
   *avg_us = ms * 1e3 / ((double)reps * D->L);
-  *bytes = 2.0 * D->H * d * 2;
+  *bytes = moe ? D->topk * mxfp4_bytes(2.0 * D->H * d) : 2.0 * D->H * d * 2;
   return 0;
 }
 

@@ -432,3 +432,31 @@ def test_llama32_1b_shape_tokens(model_dir):
 @pytest.mark.timeout(900)
 def test_qwen3_4b_shape_tokens(model_dir):
     _full_size("qwen3-4b", model_dir)
+
+
+@pytest.mark.parametrize("name,cls", [("tiny-qwen", "gate_up_gemv"), ("tiny-moe", "moe_gate_up")])
+def test_kernel_rate_hook(name, cls, model_dir):
+    """The sustained-rate hook (back-to-back launches of one decode kernel
+    class over every layer) returns a positive duration and the class's
+    algorithmic bytes, refuses other classes, and leaves the generation
+    state alone: the next decode step's logits are bit-identical."""
+    rt = runtime()
+    d = model_dir(name)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(256, shp.prompt_len, PROMPT_SEED)
+    with rt.Transformer(d) as t:
+        t.predict(prompt)
+        ref = t.predict([5])
+        t.reset()
+        t.predict(prompt)
+        r = t.kernel_rate(cls, reps=2)
+        after = t.predict([5])
+        refused = t.kernel_rate("attention_decode", reps=1)
+    assert r is not None and r[0] > 0
+    if shp.experts:
+        want = shp.experts_per_tok * 2 * shp.hidden * shp.dim * (0.5 + 1 / 32)
+    else:
+        want = 2 * shp.hidden * shp.dim * 2
+    assert r[1] == pytest.approx(want)
+    assert refused is None
+    np.testing.assert_array_equal(after, ref)
