@@ -1,11 +1,13 @@
 """Benchmark: StrasGPT transformer forward pass on one MI355X.
 
 Workload (one "step" = one full greedy generation, KV cache reset first):
-the Qwen3-4B-shaped decoder (d 2560, FFN 9728, 36 layers, 32/8 heads of
-128, QK RMSNorm, vocab 151936, tied; random-init bf16 N(0, 0.02) weights,
-norm weights 1.0), a 512-token uniform-random prompt, then 128 greedy decode
-tokens. Weights are read from a seeded synthetic safetensors directory and
-are HBM-resident before the timed region.
+the Mistral-Small-24B-shaped decoder (d 5120, FFN 32768, 40 layers, 32/8
+heads of 128, vocab 131072, untied output, RoPE theta 1e8; random-init bf16
+N(0, 0.02) weights, norm weights 1.0; 47 GB of weights), a 2048-token
+uniform-random prompt, then 128 greedy decode tokens: the largest benchmark
+configuration, which fits one MI355X. --config selects another (llama3.2-1b,
+qwen3-4b, llama3.1-8b, moe-mxfp4). Weights are read from a seeded synthetic
+safetensors directory and are HBM-resident before the timed region.
 
 value = decode tokens/s (decode_count / sum of decode time over the timed
 steps); prefill tokens/s is reported beside it (prompt tokens / prefill
@@ -14,14 +16,19 @@ share of event-measured decode time in an eager profiling pass of the
 same workload); its duration is timed with one pair of HIP events on the
 library's stream around back-to-back launches over every layer's weights
 (the per-launch event figure, which also brackets each dispatch gap, is
-reported beside it); the
-cpu_baseline is the oracle (C + OpenMP restatement of the reference
-forward pass) timed on a bounded sample of the same model on the host.
+reported beside it). The cpu_baseline is the reference's own C sources
+(oracle/_ref/ref_baseline, built with the reference's flags, -march=x86-64-v3
+for -march=native) driven by the reference's greedy loop on a bounded
+sample of the same model files on the host cores, with the reference's
+timing boundaries (source/strasgpt.c:206-274); where that binary is absent,
+the oracle (the C + OpenMP restatement of the reference forward pass).
 """
 import argparse
 import json
 import os
+import subprocess
 import sys
+import tempfile
 import time
 
 REPO = os.path.dirname(os.path.abspath(__file__))
@@ -50,13 +57,59 @@ def ensure_model(shp, seed):
     return d
 
 
-def cpu_baseline(d, shp, prompt, threads, decode_tokens):
-    """Oracle on the host cores: a short prefill then `decode_tokens` steps."""
+def host_cpu():
+    """(threads this process may use, physical cores of the host, CPU model)."""
+    avail = len(os.sched_getaffinity(0))
+    cores = None
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True,
+                             timeout=30).stdout
+        cores = len({ln for ln in out.splitlines() if ln and not ln.startswith("#")})
+    except (OSError, subprocess.SubprocessError):
+        pass
+    model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return avail, cores, model
+
+
+def cpu_baseline(d, shp, prompt, threads, prefill_tokens, decode_tokens):
+    """The reference forward pass on the host cores: a short prefill, then
+    `decode_tokens` greedy steps, timed like the reference driver."""
+    from oracle import ref_manifest
+    avail, phys, model = host_cpu()
+    threads = max(1, min(threads, avail))
+    sample_prompt = prompt[:prefill_tokens]
+    info = {"cores": threads, "host_physical_cores": phys, "threads_available": avail,
+            "cpu_model": model}
+    if os.path.exists(ref_manifest.BASELINE):
+        with tempfile.TemporaryDirectory(prefix="strasgpt_cpu_") as tmp:
+            man = ref_manifest.write(d, sample_prompt, decode_tokens + 1,
+                                     os.path.join(tmp, "manifest.txt"))
+            env = dict(os.environ, OMP_WAIT_POLICY="ACTIVE")  # as source/strasgpt.c:79
+            t0 = time.time()
+            r = subprocess.run([ref_manifest.BASELINE, man, os.path.join(tmp, "out.bin"),
+                                str(threads)], capture_output=True, text=True, env=env)
+            if r.returncode != 0:
+                raise RuntimeError(f"reference CPU baseline failed: {r.stderr[-1000:]}")
+            fields = [ln for ln in r.stderr.splitlines() if ln.startswith("timing ")][-1].split()
+            prefill_s, decode_s, n = float(fields[1]), float(fields[2]), int(fields[3])
+            log(f"cpu baseline: reference run in {time.time() - t0:.1f}s ({threads} threads)")
+        return {"value": n / decode_s, "unit": "tok/s", "kind": "reference", **info,
+                "prefill_tok_s": len(sample_prompt) / prefill_s,
+                "sample": (f"{shp.name}: {len(sample_prompt)}-token prefill then {n} greedy "
+                           f"decode steps, the reference's C sources (oracle/_ref/ref_baseline: "
+                           f"-O3 -march=x86-64-v3 -ffast-math -fno-finite-math-only -fopenmp), "
+                           f"OMP_WAIT_POLICY=ACTIVE, {threads} threads")}
     from oracle import oracle as orc
     t0 = time.time()
     om = orc.OracleModel(d, threads=threads)
     log(f"cpu baseline: oracle loaded in {time.time() - t0:.1f}s ({threads} threads)")
-    sample_prompt = prompt[:16]
     t0 = time.time()
     logits = om.predict(sample_prompt)
     t_prefill = time.time() - t0
@@ -67,7 +120,7 @@ def cpu_baseline(d, shp, prompt, threads, decode_tokens):
     t_decode = time.time() - t0
     om.close()
     return {
-        "value": decode_tokens / t_decode, "unit": "tok/s", "cores": threads, "kind": "port",
+        "value": decode_tokens / t_decode, "unit": "tok/s", "kind": "port", **info,
         "prefill_tok_s": len(sample_prompt) / t_prefill,
         "sample": (f"{shp.name}: {len(sample_prompt)}-token prefill then {decode_tokens} "
                    f"greedy decode steps, oracle/oracle.c (OpenMP, {threads} threads)"),
@@ -75,8 +128,10 @@ def cpu_baseline(d, shp, prompt, threads, decode_tokens):
 
 
 COPY_PROBE_BYTES = 256 << 20
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_decode_kernels_qwen3-4b.json")
-TRAFFIC_CONFIG = "qwen3-4b"  # the workload the counter summary was taken on
+
+
+def traffic_file(config):
+    return os.path.join(REPO, "profiles", f"traffic_decode_kernels_{config}.json")
 
 
 def probe_traffic(t, prompt):
@@ -98,12 +153,10 @@ def probe_traffic(t, prompt):
 
 def traffic_for(kernel, config):
     """HBM bytes per launch of a decode kernel class from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated on copy_probe_kernel), or None.
-    The summary covers the Qwen3-4B-shaped workload only."""
-    if config != TRAFFIC_CONFIG:
-        return None
+    summary of this workload (FETCH_SIZE + WRITE_SIZE, calibrated on
+    copy_probe_kernel), or None where no summary exists."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(traffic_file(config)) as f:
             table = json.load(f)
         return table["kernels"][kernel]["traffic_bytes"]
     except (OSError, KeyError, ValueError):
@@ -115,9 +168,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="qwen3-4b")
+    ap.add_argument("--config", default="mistral-small-24b")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=16,
+                    help="upper bound; the baseline uses at most the CPUs this process may run on")
+    ap.add_argument("--cpu-prefill-tokens", type=int, default=16)
     ap.add_argument("--cpu-decode-tokens", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--precision", type=int, default=0, help="prefill GEMM: 0 bf16x2, 1 bf16")
@@ -218,7 +273,6 @@ def main():
     decode_tok_s = decode_n / decode_s
     prefill_tok_s = args.steps * len(prompt) / prefill_s
     decode_bytes = sum(v["bytes"] for k, v in stats.items() if k in decode_kernels)
-    decode_ms = sum(v["total_ms"] for k, v in stats.items() if k in decode_kernels)
     ntok = steps_per_gen - 1
     out = {
         "metric": "decode tok/s @batch1 + prefill tok/s; % of HBM BW / MFMA peak",
@@ -234,7 +288,6 @@ def main():
         "prefill_tok_s": round(prefill_tok_s, 1),
         "decode_ms_per_token": round(decode_s / decode_n * 1e3, 4),
         "decode_effective_gbs": round(decode_bytes / ntok / (decode_s / decode_n) / 1e9, 1),
-        "decode_kernel_busy_frac": round(decode_ms / 1e3 / (decode_s / args.steps), 3),
         "roofline": roofline,
         "roofline_prefill": roofline_prefill,
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
@@ -242,7 +295,8 @@ def main():
         "tokens_head": tokens[:8],
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(d, shp, prompt, args.cpu_threads, args.cpu_decode_tokens)
+        out["cpu_baseline"] = cpu_baseline(d, shp, prompt, args.cpu_threads,
+                                           args.cpu_prefill_tokens, args.cpu_decode_tokens)
     print(json.dumps(out), flush=True)
 
 

@@ -1,0 +1,28 @@
+/*
+ * Token selection on the device. The reference samples on the host
+ * (source/sampler.c); these entry points run its selection rules on the
+ * GPU.
+ */
+#ifndef SAMPLER_HIP_H
+#define SAMPLER_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The reference's sample_argmax (source/sampler.c:92-102) on the device:
+ * the first index holding the maximum of probability[0 .. n). A NaN never
+ * wins over an earlier value, and a NaN at index 0 is never replaced (the
+ * scan compares with a strict ">"). probability is a host array; each call
+ * allocates device memory for a copy of it and for the per-block partial
+ * results, runs two kernels on the GPU and frees the memory. Dies (like
+ * every error of this library) when n is 0 or above INT_MAX. */
+size_t sampler_argmax(const float* probability, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAMPLER_HIP_H */

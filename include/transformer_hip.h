@@ -29,14 +29,12 @@ typedef struct transformer_timing {
  * --temp 0): one prefill over the prompt, then step_count - 1 single-token
  * steps, each feeding back the argmax. The loop stays on the device: the
  * next token never leaves HBM between steps. By default the step's
- * kernels are replayed from a captured HIP graph; a dense model can instead
- * run each step as one persistent kernel launch (see
+ * kernels are replayed from a captured HIP graph (see
  * transformer_set_decode_mode). Writes step_count token ids to out. Stops
  * early (like the reference) when eos_token_id >= 0 is produced; returns
  * the number of ids written. timing may be NULL. Environment:
- * STRASGPT_DECODE_PERSISTENT=1 selects the persistent step by default;
- * STRASGPT_DECODE_GRAPH=0 launches the graph path's kernels eagerly
- * instead (for tools that do not follow graph launches). */
+ * STRASGPT_DECODE_GRAPH=0 launches the step's kernels eagerly instead (for
+ * tools that do not follow graph launches). */
 size_t transformer_generate_greedy(
     transformer_t* transformer,
     size_t token_count,
@@ -71,44 +69,17 @@ void transformer_capture_hidden(
  * Returns the previous mode. */
 int transformer_set_prefill_precision(transformer_t* transformer, int mode);
 
-/* Decode step implementation used by transformer_generate_greedy and by
- * single-token transformer_predict calls (no reference counterpart):
- *   TRANSFORMER_DECODE_PERSISTENT: one launch per token, all blocks
- *     resident, phases separated by grid barriers (dense models; others
- *     fall back to the graph path),
- *   TRANSFORMER_DECODE_GRAPH (default): one kernel per operation, replayed
- *     from a captured HIP graph by transformer_generate_greedy,
- *   TRANSFORMER_DECODE_EAGER: the same kernels launched one by one.
+/* Decode step implementation used by transformer_generate_greedy (no
+ * reference counterpart): one kernel per operation, either
+ *   TRANSFORMER_DECODE_GRAPH (default): replayed from a captured HIP graph,
+ *   TRANSFORMER_DECODE_EAGER: launched one by one.
  * Returns the previous mode. Profiling (transformer_profile) always uses
  * the eager path. */
 enum transformer_decode_mode {
-  TRANSFORMER_DECODE_PERSISTENT = 0,
   TRANSFORMER_DECODE_GRAPH = 1,
   TRANSFORMER_DECODE_EAGER = 2
 };
 int transformer_set_decode_mode(transformer_t* transformer, int mode);
-
-/* 1 when the loaded model can use TRANSFORMER_DECODE_PERSISTENT. */
-int transformer_decode_persistent_supported(const transformer_t* transformer);
-
-/* Phase tracer of the persistent decode step (measurement hook, no
- * reference counterpart). While enabled, the first worker block of every
- * step records wall-clock times around each grid barrier. transformer_decode_trace_read
- * returns the barrier count n (0 when the tracer was never enabled) and
- * writes up to max_values per-step averages in microseconds as 8 rows of n:
- *   row 0: work before barrier k (since leaving the previous one),
- *   row 1: wait inside barrier k,
- *   rows 2-4: for the phase that barrier k starts, time from leaving the
- *          barrier to the end of input staging, of the weight loop (for
- *          attention: of the key tiles) and of the epilogue (attention: of
- *          the work item),
- *   rows 5-7: for a GEMV phase started by barrier k, time from leaving the
- *          barrier until the first stream wave starts its weight loop,
- *          ends it, and has issued the next phase's first loads.
- * Barrier k ends phase k; phases are in launch order: per layer QKV,
- * attention, O, gate/up, down, then the logits (n = 5 x layer_count + 1). */
-void transformer_decode_trace(transformer_t* transformer, int enable);
-int transformer_decode_trace_read(transformer_t* transformer, double* us, int max_values);
 
 /* Measurement hooks (no reference counterpart; the reference only times
  * whole predict calls, source/strasgpt.c:206-274). While enabled, every
@@ -150,8 +121,9 @@ int transformer_profile_read(
  * the average duration per launch (one inter-kernel gap included, as in a
  * decode step) and the algorithmic bytes per launch. Supported for the
  * dense gate/up GEMV (TRANSFORMER_K_GATE_UP_GEMV) and the MoE expert
- * gate/up GEMV (TRANSFORMER_K_MOE_GATE_UP; experts from the last step's
- * router logits, the same for every layer), whose launches write only
+ * gate/up GEMV (TRANSFORMER_K_MOE_GATE_UP; the experts that the router
+ * logits of the last decode step select, the same for every layer, or
+ * experts 0 .. top-k - 1 before any decode step), whose launches write only
  * scratch activations; returns -1 for other classes. No reference
  * counterpart (measurement hook). */
 int transformer_kernel_rate(

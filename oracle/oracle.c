@@ -41,6 +41,9 @@ static inline float bf16f(uint16_t w) {
 }
 
 float oracle_bf16_to_f32(uint16_t w) { return bf16f(w); }
+void oracle_bf16_to_f32_array(const uint16_t* w, size_t n, float* out) {
+  for (size_t i = 0; i < n; i++) out[i] = bf16f(w[i]);
+}
 
 /* OCP Microscaling v1.0: E2M1 element (sign, 2-bit exponent, 1-bit
  * mantissa) times an E8M0 scale 2^(s-127); s = 255 encodes NaN. No
@@ -83,6 +86,25 @@ float oracle_dot_bf16(size_t len, const float* a, const uint16_t* w) {
     }
   }
   return reduce_4x8(acc);
+}
+
+/* oracle_dot_bf16 of one weight row with two activation rows at once
+ * (independent accumulators, the same roundings as two separate calls). */
+static void dot2_bf16(size_t len, const float* a0, const float* a1, const uint16_t* w,
+                      float* r0, float* r1) {
+  float acc0[4][8] = {{0}}, acc1[4][8] = {{0}};
+  for (size_t i = 0; i < len; i += 32) {
+    for (int j = 0; j < 4; j++) {
+      for (int l = 0; l < 8; l++) {
+        size_t k = i + 8 * (size_t)j + (size_t)l;
+        float wk = bf16f(w[k]);
+        acc0[j][l] = fmaf(a0[k], wk, acc0[j][l]);
+        acc1[j][l] = fmaf(a1[k], wk, acc1[j][l]);
+      }
+    }
+  }
+  *r0 = reduce_4x8(acc0);
+  *r1 = reduce_4x8(acc1);
 }
 
 /* Same accumulation order with fp32 weights (dequantised MXFP4 rows). */
@@ -149,21 +171,30 @@ void oracle_attention_row(size_t hd, size_t count, const float* q, const float* 
                           const float* v, float* out) {
   float* p = malloc(count * sizeof(float));
   float scale = sqrtf((float)hd);
-  for (size_t s = 0; s < count; s++) {
+  /* 8 keys at a time: independent chains, each still summed over h in
+   * order (the same roundings as one key at a time) */
+  size_t s = 0;
+  for (; s + 8 <= count; s += 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (size_t h = 0; h < hd; h++)
+      for (int j = 0; j < 8; j++) acc[j] = fmaf(q[h], k[(s + j) * hd + h], acc[j]);
+    for (int j = 0; j < 8; j++) p[s + j] = acc[j] / scale;
+  }
+  for (; s < count; s++) {
     float acc = 0.0f;
     for (size_t h = 0; h < hd; h++) acc = fmaf(q[h], k[s * hd + h], acc);
     p[s] = acc / scale;
   }
   float mx = p[0];
-  for (size_t s = 1; s < count; s++) mx = p[s] > mx ? p[s] : mx;
+  for (s = 1; s < count; s++) mx = p[s] > mx ? p[s] : mx;
   float sum = 0.0f;
-  for (size_t s = 0; s < count; s++) {
+  for (s = 0; s < count; s++) {
     p[s] = expf(p[s] - mx);
     sum += p[s];
   }
-  for (size_t s = 0; s < count; s++) p[s] /= sum;
+  for (s = 0; s < count; s++) p[s] /= sum;
   for (size_t h = 0; h < hd; h++) out[h] = 0.0f;
-  for (size_t s = 0; s < count; s++) {
+  for (s = 0; s < count; s++) {
     for (size_t h = 0; h < hd; h++) out[h] = fmaf(p[s], v[s * hd + h], out[h]);
   }
   free(p);
@@ -373,6 +404,48 @@ static void moe_token(const oracle_model_t* m, size_t l, const float* xn, float*
   free(row);
 }
 
+/* out(r, t) = dot(K, x[t], w[r]) for r < R, t < T, in blocks of 16 rows x
+ * 32 tokens so that both stay in the core's caches (the reference loops
+ * over rows then tokens; each dot product is the same either way). */
+typedef void (*store_fn)(void* ctx, size_t r, size_t t, float v);
+static void project(size_t R, size_t T, size_t K, const uint16_t* w, const float* x, size_t ldx,
+                    store_fn st, void* ctx) {
+  const size_t RB = 16, TB = 32;
+  const size_t nrb = (R + RB - 1) / RB, ntb = (T + TB - 1) / TB;
+  #pragma omp parallel for collapse(2) schedule(static)
+  for (size_t rb = 0; rb < nrb; rb++) {
+    for (size_t tb = 0; tb < ntb; tb++) {
+      const size_t r1 = rb * RB + RB < R ? rb * RB + RB : R;
+      const size_t t1 = tb * TB + TB < T ? tb * TB + TB : T;
+      for (size_t r = rb * RB; r < r1; r++) {
+        size_t t = tb * TB;
+        for (; t + 2 <= t1; t += 2) {
+          float v0, v1;
+          dot2_bf16(K, x + t * ldx, x + (t + 1) * ldx, w + r * K, &v0, &v1);
+          st(ctx, r, t, v0);
+          st(ctx, r, t + 1, v1);
+        }
+        if (t < t1) st(ctx, r, t, oracle_dot_bf16(K, x + t * ldx, w + r * K));
+      }
+    }
+  }
+}
+
+typedef struct {
+  float* base;
+  size_t ctx, hd, P, ld;
+} store_ctx_t;
+/* cache row P + t of head r / hd: base[(head ctx + P + t) hd + r % hd] */
+static void store_cache(void* c_, size_t r, size_t t, float v) {
+  store_ctx_t* c = c_;
+  c->base[((r / c->hd) * c->ctx + c->P + t) * c->hd + r % c->hd] = v;
+}
+/* row-major [t][ld] */
+static void store_rows(void* c_, size_t r, size_t t, float v) {
+  store_ctx_t* c = c_;
+  c->base[t * c->ld + r] = v;
+}
+
 /* Reference transformer_predict_chunk (source/transformer.c:1186-1602). */
 static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc, float* logits,
                           size_t cap_row, size_t cap_rows) {
@@ -394,15 +467,10 @@ static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc
     for (size_t t = 0; t < T; t++) oracle_rmsnorm(d, xn + t * d, x + t * d, W(m, ORACLE_MHA_NORM, l), eps);
 
     /* K and V projections into the cache (source/transformer.c:1271-1291) */
-    #pragma omp parallel for schedule(static)
-    for (size_t r = 0; r < kvh * hd; r++) {
-      size_t head = r / hd, h = r % hd;
-      const uint16_t* wk = W(m, ORACLE_K, l) + r * d;
-      const uint16_t* wv = W(m, ORACLE_V, l) + r * d;
-      for (size_t t = 0; t < T; t++) {
-        kc[(head * ctx + P + t) * hd + h] = oracle_dot_bf16(d, xn + t * d, wk);
-        vc[(head * ctx + P + t) * hd + h] = oracle_dot_bf16(d, xn + t * d, wv);
-      }
+    {
+      store_ctx_t sk = {kc, ctx, hd, P, 0}, sv = {vc, ctx, hd, P, 0};
+      project(kvh * hd, T, d, W(m, ORACLE_K, l), xn, d, store_cache, &sk);
+      project(kvh * hd, T, d, W(m, ORACLE_V, l), xn, d, store_cache, &sv);
     }
     /* K-norm and RoPE on the new keys (source/transformer.c:1293-1323) */
     #pragma omp parallel for collapse(2) schedule(static)
@@ -414,10 +482,9 @@ static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc
       }
     }
     /* Q projection, Q-norm, RoPE (source/transformer.c:1327-1373) */
-    #pragma omp parallel for schedule(static)
-    for (size_t r = 0; r < qd; r++) {
-      const uint16_t* wq = W(m, ORACLE_Q, l) + r * d;
-      for (size_t t = 0; t < T; t++) q[t * qd + r] = oracle_dot_bf16(d, xn + t * d, wq);
+    {
+      store_ctx_t sq = {q, 0, 0, 0, qd};
+      project(qd, T, d, W(m, ORACLE_Q, l), xn, d, store_rows, &sq);
     }
     #pragma omp parallel for collapse(2) schedule(static)
     for (size_t head = 0; head < qh; head++) {
@@ -437,10 +504,9 @@ static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc
       }
     }
     /* Output projection + residual (source/transformer.c:1426-1445) */
-    #pragma omp parallel for schedule(static)
-    for (size_t e = 0; e < d; e++) {
-      const uint16_t* wo = W(m, ORACLE_O, l) + e * qd;
-      for (size_t t = 0; t < T; t++) tmp[t * d + e] = oracle_dot_bf16(qd, att + t * qd, wo);
+    {
+      store_ctx_t so = {tmp, 0, 0, 0, d};
+      project(d, T, qd, W(m, ORACLE_O, l), att, qd, store_rows, &so);
     }
     for (size_t i = 0; i < T * d; i++) x[i] += tmp[i];
 
@@ -449,21 +515,12 @@ static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc
 
     if (c->expert_count == 0) {
       /* Gate, up, SwiGLU, down + residual (source/transformer.c:1461-1504) */
+      store_ctx_t sg_ = {g, 0, 0, 0, H}, su = {u, 0, 0, 0, H}, sd = {tmp, 0, 0, 0, d};
+      project(H, T, d, W(m, ORACLE_GATE, l), xn, d, store_rows, &sg_);
+      project(H, T, d, W(m, ORACLE_UP, l), xn, d, store_rows, &su);
       #pragma omp parallel for schedule(static)
-      for (size_t h = 0; h < H; h++) {
-        const uint16_t* wg = W(m, ORACLE_GATE, l) + h * d;
-        const uint16_t* wu = W(m, ORACLE_UP, l) + h * d;
-        for (size_t t = 0; t < T; t++) {
-          float gv = oracle_dot_bf16(d, xn + t * d, wg);
-          float uv = oracle_dot_bf16(d, xn + t * d, wu);
-          g[t * H + h] = silu_mul(gv, uv);
-        }
-      }
-      #pragma omp parallel for schedule(static)
-      for (size_t e = 0; e < d; e++) {
-        const uint16_t* wd = W(m, ORACLE_DOWN, l) + e * H;
-        for (size_t t = 0; t < T; t++) tmp[t * d + e] = oracle_dot_bf16(H, g + t * H, wd);
-      }
+      for (size_t i = 0; i < T * H; i++) g[i] = silu_mul(g[i], u[i]);
+      project(d, T, H, W(m, ORACLE_DOWN, l), g, H, store_rows, &sd);
     } else {
       #pragma omp parallel for schedule(dynamic, 1)
       for (size_t t = 0; t < T; t++) moe_token(m, l, xn + t * d, tmp + t * d);
@@ -471,7 +528,6 @@ static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc
     for (size_t i = 0; i < T * d; i++) x[i] += tmp[i];
     if (m->cap) memcpy(m->cap + (l * cap_rows + cap_row) * d, x, T * d * sizeof(float));
   }
-  (void)u;
 
   /* Final RMSNorm in place, classifier for the last lc rows
    * (source/transformer.c:1580-1601) */

@@ -82,6 +82,8 @@ size_t oracle_argmax(const float* x, size_t n);
 
 /* Primitive restatements, exported for unit pinning. */
 float oracle_bf16_to_f32(uint16_t w);
+/* The same over n codes into out (bit patterns kept, signaling NaNs included). */
+void oracle_bf16_to_f32_array(const uint16_t* w, size_t n, float* out);
 float oracle_mxfp4_value(uint8_t code, uint8_t scale);
 void oracle_mxfp4_dequant(const uint8_t* blocks, const uint8_t* scales,
                           size_t value_count, float* out);

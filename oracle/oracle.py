@@ -104,6 +104,7 @@ def load_lib():
     lib.oracle_argmax.restype = sz
     lib.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
     lib.oracle_bf16_to_f32.restype = ctypes.c_float
+    lib.oracle_bf16_to_f32_array.argtypes = [P, sz, fp]
     lib.oracle_mxfp4_value.argtypes = [ctypes.c_uint8, ctypes.c_uint8]
     lib.oracle_mxfp4_value.restype = ctypes.c_float
     lib.oracle_mxfp4_dequant.argtypes = [P, P, sz, fp]

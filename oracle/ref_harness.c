@@ -21,11 +21,16 @@
  * Output (binary, little endian): int32 generated[step_count],
  *   float32 logits_after_prompt[vocab], float32 final_norm[T][embedding_dim]
  *   for the last chunk of the prompt (the reference's state->embedding).
- * With a 4th argument L, only layers < L are loaded and run (per-layer
- * hidden-state pins).
+ * With a 4th argument L (> 0), only layers < L are loaded and run
+ * (per-layer hidden-state pins).
+ * Timing: stderr gets one line "timing <prefill_s> <decode_s> <decode_count>"
+ * with the reference driver's boundaries (source/strasgpt.c:206-274): the
+ * first transformer_predict over the prompt, and the sum of the
+ * single-token steps (sampling excluded), on a monotonic clock.
  */
 #include <omp.h>
 #include <stdio.h>
+#include <time.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -33,6 +38,12 @@
 #include "safetensors.h"
 #include "sampler.h"
 #include "transformer.h"
+
+static double now_s(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
 
 static int layer_of(const char* name) {
   const char* p = strstr(name, "layers.");
@@ -48,7 +59,7 @@ int main(int argc, char** argv) {
   FILE* mf = fopen(argv[1], "r");
   if (!mf) return 2;
   int threads = atoi(argv[3]);
-  long keep_layers = argc > 4 ? atol(argv[4]) : -1;
+  long keep_layers = argc > 4 && atol(argv[4]) > 0 ? atol(argv[4]) : -1;
 
   safetensors_t* s = safetensors_malloc();
   int inter;
@@ -104,26 +115,32 @@ int main(int argc, char** argv) {
   int* gen = calloc(steps ? steps : 1, sizeof(int));
   size_t count = 0;
   int next = 0;
+  double start = now_s(), prefill_s = 0.0, decode_s = 0.0;
 
   #pragma omp parallel
   {
     transformer_predict(tr, T, tok, 1, logits);
     #pragma omp single
     {
+      prefill_s = now_s() - start;
       memcpy(first, logits, V * sizeof(float));
       memcpy(hidden, tr->state->embedding, last_chunk * d * sizeof(float));
       next = (int)sampler_sample(sm, logits, tok[T - 1]);
       gen[count++] = next;
+      start = now_s();
     }
     while (count < steps) {
       transformer_predict(tr, 1, &next, 1, logits);
       #pragma omp single
       {
+        decode_s += now_s() - start;
         next = (int)sampler_sample(sm, logits, next);
         gen[count++] = next;
+        start = now_s();
       }
     }
   }
+  fprintf(stderr, "timing %.9f %.9f %zu\n", prefill_s, decode_s, count - 1);
 
   FILE* out = fopen(argv[2], "wb");
   if (!out) return 4;

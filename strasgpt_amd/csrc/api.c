@@ -87,18 +87,6 @@ int transformer_set_decode_mode(transformer_t* transformer, int mode) {
   return transformer ? sg_set_decode_mode(transformer, mode) : -1;
 }
 
-int transformer_decode_persistent_supported(const transformer_t* transformer) {
-  return transformer ? sg_decode_persistent_supported(transformer) : 0;
-}
-
-void transformer_decode_trace(transformer_t* transformer, int enable) {
-  if (transformer) sg_decode_trace(transformer, enable);
-}
-
-int transformer_decode_trace_read(transformer_t* transformer, double* us, int max_values) {
-  return transformer ? sg_decode_trace_read(transformer, us, max_values) : 0;
-}
-
 void transformer_profile(transformer_t* transformer, int enable) {
   if (transformer) sg_profile(transformer, enable);
 }

@@ -417,55 +417,4 @@ void gemv(const GemvParams& p, int epi, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
-// Launch-shape variants for the micro-benchmark (STORE epilogue, or
-// SwiGLU when `dual`): rows per wavefront R, steps per chunk U, block cap.
-int gemv_variant_count() { return 18; }
-
-void gemv_variant(const GemvParams& p, bool dual, int v, hipStream_t s) {
-  check(p, dual ? GEMV_SWIGLU : GEMV_STORE);
-#define V(R, U, CAP)                                                   \
-  if (dual) launch<R, U, GEMV_SWIGLU>(p, s, CAP);                      \
-  else launch<R, U, GEMV_STORE>(p, s, CAP);                            \
-  break;
-  switch (v) {
-    case 0: V(1, 2, 2048)
-    case 1: V(1, 4, 2048)
-    case 2: V(1, 8, 2048)
-    case 3: V(2, 2, 2048)
-    case 4: V(2, 4, 2048)
-    case 5: V(4, 2, 2048)
-    case 6: V(1, 4, 1024)
-    case 7: V(2, 4, 1024)
-    case 8: V(1, 4, 512)
-    case 9: V(2, 2, 512)
-    case 10: V(4, 4, 1024)
-    case 11: V(1, 4, 4096)
-    case 12:  // the flat-stream form, block caps 2048 .. 256 (falls back to variant 1 when the row does not fit)
-    case 13:
-    case 14:
-    case 15: {
-      const int cap = 2048 >> (v - 12);
-      if (dual) {
-        if (!launch_v2<GEMV_SWIGLU>(p, s, cap)) launch<1, 4, GEMV_SWIGLU>(p, s, 2048);
-      } else {
-        if (!launch_v2<GEMV_STORE>(p, s, cap)) launch<1, 4, GEMV_STORE>(p, s, 2048);
-      }
-      break;
-    }
-    case 16:  // the flat-stream form, 2 (SwiGLU) or 4 steps in flight, caps 2048 and 1024
-    case 17: {
-      const int cap = 2048 >> (v - 16);
-      if (dual) {
-        if (!launch_v2<GEMV_SWIGLU, 2>(p, s, cap)) launch<1, 4, GEMV_SWIGLU>(p, s, 2048);
-      } else {
-        if (!launch_v2<GEMV_STORE, 4>(p, s, cap)) launch<1, 4, GEMV_STORE>(p, s, 2048);
-      }
-      break;
-    }
-    default: ST_DIE("unknown GEMV variant");
-  }
-#undef V
-  HIP_CHECK(hipGetLastError());
-}
-
 }  // namespace sg

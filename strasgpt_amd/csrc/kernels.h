@@ -217,72 +217,4 @@ int argmax_blocks();
 void moe_route(const float* xn, int T, const uint16_t* router, int E, int d, int k,
                int* sel, float* sel_w, hipStream_t s);
 
-// ------------------------------------------------- persistent decode --
-// One launch computes a whole decode step for a dense model: embedding of
-// *next, every layer, final norm, logits, argmax into *next (appended to
-// seq), *pos += 1. The grid is one block per compute unit, all resident;
-// phases are separated by grid barriers (grid_sync.h).
-struct DecodeLayer {
-  const uint16_t *qkv, *o, *gate, *up, *down;    // bf16 weights
-  const uint16_t *attn_norm, *ffn_norm;          // [d]
-  const uint16_t *q_norm, *k_norm;               // [hd] or null
-  float *kcache, *vcache;                        // [kv_heads][ctx][hd]
-};
-
-// Work split of one GEMV phase: `rb` output rows per block, each row cut
-// into `S` slices of `ks` 8-element chunks (the last slice may be shorter).
-struct DecodeGemvPlan {
-  int rb, S, ks;
-};
-
-struct DecodeParams {
-  const DecodeLayer* layers;  // device array [L]
-  int L, d, H, qh, kvh, hd, qd, kvd, qkv_rows, V, ctx;
-  float eps;
-  const uint16_t *emb, *out_norm, *out_w;
-  const float* rope;
-  int pb, po, pst;
-  const int* tok;        // token of this step (device)
-  int *pos, *next;       // *pos: its position, incremented; *next: the argmax
-  int *seq, *seq_len;    // argmax appended to seq when seq is not null
-  float* logits;         // [V], or null when only the argmax is wanted
-  float* cap;            // null, or [L][d]: the residual stream after each layer
-  float* cap_final;      // null, or [d]: the final RMSNorm output
-  // activations shared between blocks (agent-coherent accesses only)
-  float *x, *qkv, *att, *act, *part, *am_v;
-  int* am_i;
-  unsigned *sync_state, *sync_err, *epoch;
-  // null, or [kDecodeTraceRows][decode_barriers(L)] wall-clock ticks
-  // (100 MHz) summed over launches, seen by block 0 (see
-  // transformer_decode_trace_read); block 0 accumulates a launch in LDS at
-  // byte offset trace_lds (decode_lds_bytes)
-  unsigned long long* trace;
-  size_t trace_lds;
-  int layer_lds;        // LDS float offset of the layer table (decode_work_floats)
-  int max_chunks;       // attention key chunks per kv head (decode_max_chunks)
-  unsigned* att_cnt;    // [kvh] attention items done per kv head, zero between launches
-  DecodeGemvPlan p_qkv, p_o, p_gu, p_down, p_logits;
-};
-
-// Host helpers: plan for an N x K GEMV over `blocks` blocks; LDS bytes the
-// kernel needs; whether the model shape is supported; the launch.
-DecodeGemvPlan decode_gemv_plan(int N, int K, int blocks);
-size_t decode_work_floats(const DecodeParams& p);
-size_t decode_lds_bytes(const DecodeParams& p);
-size_t decode_trace_lds_bytes(int L);
-bool decode_supported(int L, int d, int H, int qh, int kvh, int hd, int qd, int V, int blocks,
-                      size_t lds_limit);
-int decode_blocks();  // compute units of the current device
-int decode_max_chunks(int kvh, int blocks);
-// Phases per layer (QKV, attention, O, gate/up, down), each ended by a grid
-// barrier, plus the logits phase.
-constexpr int kDecodePhases = 5;
-__host__ __device__ inline int decode_barriers(int L) { return kDecodePhases * L + 1; }
-constexpr int kDecodeTraceRows = 8;
-// `p` is the host copy, `dp` the same parameters already in device memory
-// (stream-ordered before the launch).
-void decode_step(const DecodeParams& p, const DecodeParams* dp, int blocks, hipStream_t s);
-constexpr int kDecodeThreads = 768;
-constexpr int kDecodePartMax = 2048;  // per-block slice sums held in LDS
-
 }  // namespace sg

@@ -30,9 +30,6 @@ void sg_capture_hidden(transformer_t* t, float* out, float* out_final);
 int sg_set_prefill_precision(transformer_t* t, int mode);
 const char* sg_version(void);
 int sg_set_decode_mode(transformer_t* t, int mode);
-int sg_decode_persistent_supported(const transformer_t* t);
-void sg_decode_trace(transformer_t* t, int enable);
-int sg_decode_trace_read(transformer_t* t, double* us, int max_values);
 void sg_profile(transformer_t* t, int enable);
 int sg_profile_read(transformer_t* t, int kernel_class, transformer_kernel_stat_t* out);
 int sg_kernel_rate(transformer_t* t, int kernel_class, int reps, double* avg_us, double* bytes);

@@ -26,7 +26,6 @@
 
 #include <vector>
 
-#include "grid_sync.h"
 #include "hip_check.h"
 #include "kernels.h"
 #include "runtime.h"
@@ -139,19 +138,7 @@ struct transformer_device {
   int logits_rows = 0;
   size_t host_pos = 0;  // host mirror of *pos (profiling byte counts)
   bool use_graph = true;  // STRASGPT_DECODE_GRAPH=0: eager decode steps
-  // Persistent decode step (k_decode.hip): one launch per token.
   int decode_mode = TRANSFORMER_DECODE_GRAPH;
-  bool dec_ok = false;  // model shape supported by the persistent step
-  int dec_blocks = 0;
-  size_t dec_lds_limit = 0;
-  sg::DecodeParams dec{};
-  sg::DecodeLayer* dec_layers = nullptr;
-  float* dec_buf = nullptr;
-  int* dec_am_i = nullptr;
-  unsigned* dec_sync = nullptr;  // barrier state, error flag, epoch
-  sg::DecodeParams* dec_dev = nullptr;  // [2] device copies: generate, predict
-  unsigned long long* dec_trace = nullptr;  // phase tracer (see sg_decode_trace)
-  size_t dec_trace_steps = 0;
   float *kc = nullptr, *vc = nullptr, *rope = nullptr;
   // The cache rows as bf16 hi/lo planes for the split-bf16 prefill
   // attention: K [L][kvh][ctx][hd], V transposed [L][kvh][hd][ctx_pad];
@@ -815,9 +802,6 @@ void argmax_to(Dev* D, const float* row, bool log_seq, bool bump_pos) {
   sg::argmax(p, D->stream);
 }
 
-bool persistent_ok(const Dev* D);
-void check_decode_error(Dev* D);
-
 // The reference chunk loop over `token` (source/transformer.c:1643-1726):
 // logits of the caller's window [T - lc, T) are copied to host_logits (if
 // given); the last chunk's rows stay on the device.
@@ -840,22 +824,7 @@ void predict_device(transformer_t* t, size_t T, const int* token, size_t lc,
     ensure_logits(D, (int)(clc > 0 ? clc : 1));
     upload_tokens(D, token + c0, (int)n);
     set_pos(D, t->state->cached_count);
-    if (n == 1 && persistent_ok(D)) {
-      // One token: the persistent step, logits written, argmax not logged.
-      sg::DecodeParams q = D->dec;
-      q.tok = D->tok;
-      q.seq = nullptr;
-      q.seq_len = nullptr;
-      q.logits = D->logits;
-      q.cap = D->cap_out ? D->cap_dev : nullptr;
-      q.cap_final = D->cap_out ? D->cap_final_dev : nullptr;
-      HIP_CHECK(hipMemcpyAsync(D->dec_dev + 1, &q, sizeof(q), hipMemcpyHostToDevice, D->stream));
-      sg::decode_step(q, D->dec_dev + 1, D->dec_blocks, D->stream);
-      HIP_CHECK(hipStreamSynchronize(D->stream));
-      check_decode_error(D);
-    } else {
-      forward_chunk(D, D->tok, (int)n, (int)clc);
-    }
+    forward_chunk(D, D->tok, (int)n, (int)clc);
     if (clc > 0 && host_logits) {
       HIP_CHECK(hipMemcpyAsync(host_logits + (lo - start) * D->V, D->logits,
                                clc * D->V * sizeof(float), hipMemcpyDeviceToHost, D->stream));
@@ -872,111 +841,6 @@ void predict_device(transformer_t* t, size_t T, const int* token, size_t lc,
     D->cap_out = nullptr;
     D->cap_final = nullptr;
   }
-}
-
-// Device state and parameters of the persistent decode step, when the
-// model shape allows it (dense models; MoE layers use the per-kernel path).
-void init_decode(Dev* D) {
-  if (D->moe) return;
-  int dev, lds_limit = 0;
-  HIP_CHECK(hipGetDevice(&dev));
-  HIP_CHECK(hipDeviceGetAttribute(&lds_limit, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
-                                  dev));
-  const int blocks = sg::decode_blocks();
-  if (blocks > sg::kSyncMaxBlocks ||
-      !sg::decode_supported(D->L, D->d, D->H, D->qh, D->kvh, D->hd, D->qd, D->V, blocks,
-                            (size_t)lds_limit))
-    return;
-  sg::DecodeParams& p = D->dec;
-  std::vector<sg::DecodeLayer> layers(D->L);
-  const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
-  for (int l = 0; l < D->L; l++) {
-    sg::DecodeLayer& y = layers[l];
-    y.qkv = W16(D, W_Q, l);
-    y.o = W16(D, W_O, l);
-    y.gate = W16(D, W_GATE, l);
-    y.up = W16(D, W_UP, l);
-    y.down = W16(D, W_DOWN, l);
-    y.attn_norm = W16(D, W_MHA_NORM, l);
-    y.ffn_norm = W16(D, W_FFN_NORM, l);
-    y.q_norm = D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr;
-    y.k_norm = D->qk_norm ? W16(D, W_K_NORM, l) : nullptr;
-    y.kcache = D->kc + l * cache_layer;
-    y.vcache = D->vc + l * cache_layer;
-  }
-  D->dec_layers = dalloc<sg::DecodeLayer>(D->L);
-  HIP_CHECK(hipMemcpy(D->dec_layers, layers.data(), layers.size() * sizeof(sg::DecodeLayer),
-                      hipMemcpyHostToDevice));
-  p.layers = D->dec_layers;
-  p.L = D->L;
-  p.d = D->d;
-  p.H = D->H;
-  p.qh = D->qh;
-  p.kvh = D->kvh;
-  p.hd = D->hd;
-  p.qd = D->qd;
-  p.kvd = D->kvd;
-  p.qkv_rows = D->qkv_rows;
-  p.V = D->V;
-  p.ctx = D->ctx;
-  p.eps = D->eps;
-  p.emb = W16(D, W_EMB);
-  p.out_norm = W16(D, W_OUT_NORM);
-  p.out_w = D->tied ? W16(D, W_EMB) : W16(D, W_OUT);
-  p.rope = D->rope;
-  p.pb = D->pb;
-  p.po = D->po;
-  p.pst = D->pst;
-  p.tok = D->next;
-  p.pos = D->pos;
-  p.next = D->next;
-  p.seq = D->seq;
-  p.seq_len = D->seq_len;
-  p.logits = nullptr;
-  const int workers = blocks - 1;  // block 0 coordinates the grid barriers
-  p.max_chunks = sg::decode_max_chunks(D->kvh, blocks);
-  p.layer_lds = (int)sg::decode_work_floats(p);
-  const size_t part = (size_t)D->qh * p.max_chunks * (D->hd + 2);
-  const size_t nbuf = (size_t)D->d + D->qkv_rows + D->qd + D->H + part + blocks;
-  D->dec_buf = dalloc<float>(nbuf);
-  p.x = D->dec_buf;
-  p.qkv = p.x + D->d;
-  p.att = p.qkv + D->qkv_rows;
-  p.act = p.att + D->qd;
-  p.part = p.act + D->H;
-  p.am_v = p.part + part;
-  D->dec_am_i = dalloc<int>(blocks);
-  p.am_i = D->dec_am_i;
-  // barrier state, error flag, epoch, attention counters
-  const size_t nsync = sg::kSyncStateWords + 2 + D->kvh;
-  D->dec_sync = dalloc<unsigned>(nsync);
-  HIP_CHECK(hipMemset(D->dec_sync, 0, nsync * sizeof(unsigned)));
-  p.sync_state = D->dec_sync;
-  p.sync_err = D->dec_sync + sg::kSyncStateWords;
-  p.epoch = D->dec_sync + sg::kSyncStateWords + 1;
-  p.att_cnt = D->dec_sync + sg::kSyncStateWords + 2;
-  p.p_qkv = sg::decode_gemv_plan(D->qkv_rows, D->d, workers);
-  p.p_o = sg::decode_gemv_plan(D->d, D->qd, workers);
-  p.p_gu = sg::decode_gemv_plan(D->H, D->d, workers);
-  p.p_down = sg::decode_gemv_plan(D->d, D->H, workers);
-  p.p_logits = sg::decode_gemv_plan(D->V, D->d, workers);
-  D->dec_dev = dalloc<sg::DecodeParams>(2);
-  D->dec_blocks = blocks;
-  D->dec_lds_limit = (size_t)lds_limit;
-  D->dec_ok = true;
-}
-
-// A failed barrier wait inside the persistent step invalidates its results.
-void check_decode_error(Dev* D) {
-  unsigned err = 0;
-  HIP_CHECK(hipMemcpy(&err, D->dec.sync_err, sizeof(err), hipMemcpyDeviceToHost));
-  if (err) ST_DIE("persistent decode step: a grid barrier timed out (blocks not co-resident?)");
-}
-
-// Whether single-token steps use the persistent kernel (not while
-// profiling per kernel class).
-bool persistent_ok(const Dev* D) {
-  return !D->prof && D->dec_ok && D->decode_mode == TRANSFORMER_DECODE_PERSISTENT;
 }
 
 void build_decode_graph(Dev* D) {
@@ -1077,8 +941,6 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   {
     const char* g = getenv("STRASGPT_DECODE_GRAPH");
     D->use_graph = !(g && g[0] == '0');
-    const char* m = getenv("STRASGPT_DECODE_PERSISTENT");
-    if (m && m[0] == '1') D->decode_mode = TRANSFORMER_DECODE_PERSISTENT;
   }
 
   // Per-layer byte sizes of each weight class.
@@ -1280,6 +1142,9 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
     D->moe_w = dalloc<float>(T * D->topk);
     D->moe_act = dalloc<float>(T * D->topk * H);
     D->moe_logits = dalloc<float>(D->E);
+    // all-zero router logits select experts 0 .. topk-1 (ties go to the
+    // lowest id) until a decode step writes them
+    HIP_CHECK(hipMemsetAsync(D->moe_logits, 0, D->E * sizeof(float), D->stream));
     D->moe_offs = dalloc<int>(D->E + 1);
     D->moe_order = dalloc<int>(T * D->topk);
     D->moe_out = dalloc<float>(T * D->topk * d);
@@ -1291,7 +1156,6 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   HIP_CHECK(hipHostMalloc((void**)&D->h_next, sizeof(int), hipHostMallocDefault));
   ensure_logits(D, 1);
   HIP_CHECK(hipStreamSynchronize(D->stream));
-  init_decode(D);
 
   ss->embedding = D->x;
   ss->mha_q = D->q;
@@ -1323,9 +1187,7 @@ extern "C" void sg_free(transformer_t* t) {
                     D->moe_sel, D->moe_w, D->moe_act, D->moe_logits, D->moe_offs, D->moe_order, D->moe_out,
                     D->moe_ahi, D->moe_alo,
                     D->xn_hi, D->xn_lo,
-                    D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws,
-                    D->dec_layers, D->dec_buf, D->dec_am_i, D->dec_sync, D->dec_trace,
-                    D->dec_dev};
+                    D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws};
     for (void* b : bufs)
       if (b) HIP_CHECK(hipFree(b));
     if (D->h_tok) HIP_CHECK(hipHostFree(D->h_tok));
@@ -1419,19 +1281,11 @@ extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* toke
     stop = *D->h_next == eos;
   }
   if (steps > 1 && !stop) {
-    const bool persistent = persistent_ok(D);
-    const bool eager =
-        !persistent && (D->prof || !D->use_graph || D->decode_mode == TRANSFORMER_DECODE_EAGER);
-    if (!eager && !persistent) build_decode_graph(D);
-    if (persistent)
-      HIP_CHECK(hipMemcpyAsync(D->dec_dev, &D->dec, sizeof(D->dec), hipMemcpyHostToDevice,
-                               D->stream));
+    const bool eager = D->prof || !D->use_graph || D->decode_mode == TRANSFORMER_DECODE_EAGER;
+    if (!eager) build_decode_graph(D);
     set_pos(D, t->state->cached_count);
     for (size_t i = 1; i < steps && !stop; i++) {
-      if (persistent) {
-        sg::decode_step(D->dec, D->dec_dev, D->dec_blocks, D->stream);
-        if (D->dec.trace) D->dec_trace_steps++;
-      } else if (eager) {
+      if (eager) {
         // Eager step (events around every launch); same kernels as the graph.
         D->host_pos = t->state->cached_count + produced - 1;
         forward_chunk(D, D->next, 1, 1);
@@ -1449,7 +1303,6 @@ extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* toke
       }
     }
     HIP_CHECK(hipStreamSynchronize(D->stream));
-    if (persistent) check_decode_error(D);
     t->state->cached_count += produced - 1;
   }
   const double t2 = now_s();
@@ -1462,7 +1315,13 @@ extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* toke
   return produced;
 }
 
-extern "C" void sg_reset(transformer_t* t) { t->state->cached_count = 0; }
+// The bf16 planes of the cache (prefill attention) are valid for rows
+// [0, split_pos) of the current sequence only: a new sequence starts with
+// none converted.
+extern "C" void sg_reset(transformer_t* t) {
+  t->state->cached_count = 0;
+  t->device->split_pos = 0;
+}
 
 extern "C" void sg_capture_hidden(transformer_t* t, float* out, float* out_final) {
   Dev* D = t->device;
@@ -1487,52 +1346,13 @@ extern "C" int sg_set_prefill_precision(transformer_t* t, int mode) {
 }
 
 extern "C" int sg_set_decode_mode(transformer_t* t, int mode) {
-  if (mode != TRANSFORMER_DECODE_PERSISTENT && mode != TRANSFORMER_DECODE_GRAPH &&
-      mode != TRANSFORMER_DECODE_EAGER)
+  if (mode != TRANSFORMER_DECODE_GRAPH && mode != TRANSFORMER_DECODE_EAGER)
     ST_DIE("unknown decode mode");
   Dev* D = t->device;
   HIP_CHECK(hipStreamSynchronize(D->stream));
   const int old = D->decode_mode;
   D->decode_mode = mode;
   return old;
-}
-
-extern "C" void sg_decode_trace(transformer_t* t, int enable) {
-  Dev* D = t->device;
-  if (!D->dec_ok) return;
-  HIP_CHECK(hipStreamSynchronize(D->stream));
-  const size_t n = sg::kDecodeTraceRows * (size_t)sg::decode_barriers(D->L);
-  if (enable) {
-    if (!D->dec_trace) D->dec_trace = dalloc<unsigned long long>(n);
-    HIP_CHECK(hipMemset(D->dec_trace, 0, n * sizeof(unsigned long long)));
-    D->dec_trace_steps = 0;
-    const size_t at = (sg::decode_lds_bytes(D->dec) + 15) / 16 * 16;
-    if (at + sg::decode_trace_lds_bytes(D->L) > D->dec_lds_limit)
-      ST_DIE("decode trace: LDS too small for this model");
-    D->dec.trace = D->dec_trace;
-    D->dec.trace_lds = at;
-  } else {
-    D->dec.trace = nullptr;
-  }
-}
-
-extern "C" int sg_decode_trace_read(transformer_t* t, double* us, int max_values) {
-  Dev* D = t->device;
-  if (!D->dec_trace) return 0;
-  HIP_CHECK(hipStreamSynchronize(D->stream));
-  const int nbar = sg::decode_barriers(D->L);
-  const size_t n = sg::kDecodeTraceRows * (size_t)nbar;
-  std::vector<unsigned long long> h(n);
-  HIP_CHECK(hipMemcpy(h.data(), D->dec_trace, n * sizeof(unsigned long long),
-                      hipMemcpyDeviceToHost));
-  const double steps = D->dec_trace_steps ? (double)D->dec_trace_steps : 1.0;
-  for (size_t i = 0; i < n && (int)i < max_values; i++)
-    us[i] = h[i] * 0.01 / steps;  // 100 MHz ticks
-  return nbar;
-}
-
-extern "C" int sg_decode_persistent_supported(const transformer_t* t) {
-  return t->device->dec_ok ? 1 : 0;
 }
 
 extern "C" void sg_profile(transformer_t* t, int enable) {

@@ -44,7 +44,7 @@ typedef struct {
   size_t dim, hidden, layers, heads, kv_heads, head_dim, vocab, ctx;
   size_t experts, experts_per_tok;
   double theta, eps, stddev;
-  int qk_norm, untied, bos, eos;
+  int qk_norm, untied, rope_interleaved, bos, eos;
   uint64_t seed;
   size_t shard_bytes;
   const char* out;
@@ -225,6 +225,7 @@ int main(int argc, char** argv) {
     else if (ARG("--threads")) omp_set_num_threads(atoi(v));
     else if (strcmp(a, "--qk-norm") == 0) c.qk_norm = 1;
     else if (strcmp(a, "--untied") == 0) c.untied = 1;
+    else if (strcmp(a, "--rope-interleaved") == 0) c.rope_interleaved = 1;
     else DIE("unknown or incomplete argument %s", a);
 #undef ARG
   }
@@ -310,12 +311,14 @@ int main(int argc, char** argv) {
       "  \"num_key_value_heads\": %zu,\n  \"head_dim\": %zu,\n"
       "  \"vocab_size\": %zu,\n  \"max_position_embeddings\": %zu,\n"
       "  \"rms_norm_eps\": %.9g,\n  \"rope_theta\": %.1f,\n"
-      "  \"rope_scaling\": null,\n"
+      "  \"rope_scaling\": %s,\n"
       "  \"bos_token_id\": %d,\n  \"eos_token_id\": %d,\n"
       "  \"tie_word_embeddings\": %s,\n  \"torch_dtype\": \"bfloat16\"",
       c.experts ? "StrasMoeForCausalLM" : "LlamaForCausalLM", c.model_type,
       c.dim, c.hidden, c.layers, c.heads, c.kv_heads, c.head_dim, c.vocab,
-      c.ctx, c.eps, c.theta, c.bos, c.eos, c.untied ? "false" : "true");
+      c.ctx, c.eps, c.theta,
+      c.rope_interleaved ? "{\"mrope_interleaved\": true}" : "null",
+      c.bos, c.eos, c.untied ? "false" : "true");
   if (c.experts)
     p += snprintf(cfgtxt + p, sizeof(cfgtxt) - p,
                   ",\n  \"num_local_experts\": %zu,\n  \"num_experts_per_tok\": %zu",

@@ -94,18 +94,15 @@ def lib():
     L.transformer_set_prefill_precision.argtypes = [TP, ctypes.c_int]
     L.transformer_set_decode_mode.restype = ctypes.c_int
     L.transformer_set_decode_mode.argtypes = [TP, ctypes.c_int]
-    L.transformer_decode_persistent_supported.restype = ctypes.c_int
-    L.transformer_decode_persistent_supported.argtypes = [TP]
-    L.transformer_decode_trace.argtypes = [TP, ctypes.c_int]
     dp = ctypes.POINTER(ctypes.c_double)
-    L.transformer_decode_trace_read.restype = ctypes.c_int
-    L.transformer_decode_trace_read.argtypes = [TP, dp, ctypes.c_int]
     L.transformer_hip_version.restype = ctypes.c_char_p
     L.transformer_profile.argtypes = [TP, ctypes.c_int]
     L.transformer_profile_read.restype = ctypes.c_int
     L.transformer_profile_read.argtypes = [TP, ctypes.c_int, ctypes.POINTER(KernelStat)]
     L.transformer_kernel_rate.restype = ctypes.c_int
     L.transformer_kernel_rate.argtypes = [TP, ctypes.c_int, ctypes.c_int, dp, dp]
+    L.sampler_argmax.restype = sz
+    L.sampler_argmax.argtypes = [fp, sz]
     _LIB = L
     return L
 
@@ -121,7 +118,7 @@ def _ints(seq: Sequence[int]):
 
 # Kernel classes reported by transformer_profile_read (include/transformer_hip.h).
 # transformer_set_decode_mode (include/transformer_hip.h)
-DECODE_PERSISTENT, DECODE_GRAPH, DECODE_EAGER = 0, 1, 2
+DECODE_GRAPH, DECODE_EAGER = 1, 2
 
 PROFILE_KERNELS = ["qkv_gemv", "attention_decode", "o_gemv", "gate_up_gemv", "down_gemv",
                    "logits_gemv", "argmax", "moe_route", "moe_gate_up", "moe_down",
@@ -201,27 +198,8 @@ class Transformer:
         return int(self._lib.transformer_set_prefill_precision(self._t, mode))
 
     def set_decode_mode(self, mode: int) -> int:
-        """DECODE_PERSISTENT, DECODE_GRAPH or DECODE_EAGER; returns the old mode."""
+        """DECODE_GRAPH or DECODE_EAGER; returns the old mode."""
         return int(self._lib.transformer_set_decode_mode(self._t, mode))
-
-    @property
-    def decode_persistent_supported(self) -> bool:
-        return bool(self._lib.transformer_decode_persistent_supported(self._t))
-
-    def decode_trace(self, enable: bool):
-        self._lib.transformer_decode_trace(self._t, 1 if enable else 0)
-
-    def decode_trace_read(self) -> np.ndarray:
-        """[8][n] per-step average microseconds per grid barrier of the
-        persistent step (rows: work, wait, staged, loop end, epilogue end,
-        stream-wave loop start, loop end, next-phase loads issued; see
-        transformer_decode_trace_read); empty if never traced."""
-        n = self._lib.transformer_decode_trace_read(self._t, None, 0)
-        out = np.zeros((8, n), dtype=np.float64)
-        if n:
-            self._lib.transformer_decode_trace_read(
-                self._t, out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), out.size)
-        return out
 
     def profile(self, enable: bool):
         self._lib.transformer_profile(self._t, int(enable))
@@ -243,6 +221,12 @@ class Transformer:
                 out[name] = {"launches": st.launches, "total_ms": st.total_ms,
                              "bytes": st.bytes, "flops": st.flops}
         return out
+
+
+def argmax(values: np.ndarray) -> int:
+    """sampler_argmax: the reference's sample_argmax on the device."""
+    v = np.ascontiguousarray(values, np.float32)
+    return int(lib().sampler_argmax(_fp(v), v.size))
 
 
 def version() -> str:

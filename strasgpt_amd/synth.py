@@ -41,6 +41,7 @@ class ModelShape:
     model_type: str = "llama"
     ctx: Optional[int] = None
     std: float = 0.02
+    rope_interleaved: bool = False
 
     @property
     def context_len(self) -> int:
@@ -109,14 +110,31 @@ TINY: Dict[str, ModelShape] = {
     "mid-moe": ModelShape("mid-moe", 2880, 2880, 2, 8, 2, 64, 512, 150000.0, 1e-5, 6, 10,
                           untied=True, experts=8, experts_per_tok=4, model_type="stras_moe",
                           std=0.02),
+    # Interleaved RoPE pairs (2j, 2j + 1), written as
+    # rope_scaling.mrope_interleaved = true, with QK RMSNorm.
+    "tiny-rope-il": ModelShape("tiny-rope-il", 96, 192, 3, 6, 2, 32, 300, 10000.0, 1e-5,
+                               12, 8, qk_norm=True, model_type="qwen3", std=0.25,
+                               rope_interleaved=True),
+    # Interleaved RoPE with head_dim 128 and no QK-norm, over a prompt longer
+    # than one 32-key decode attention tile.
+    "tiny-rope-il128": ModelShape("tiny-rope-il128", 256, 256, 2, 4, 2, 128, 200, 500000.0,
+                                  1e-5, 80, 6, untied=True, std=0.25, rope_interleaved=True),
+}
+
+
+# The benchmark shapes at full width and full prompt/decode length but only
+# two layers: small enough for the CPU oracle to run the whole workload
+# (every prefill chunk, every decode step) in seconds to minutes.
+TRUNCATED: Dict[str, ModelShape] = {
+    f"{n}-2l": dataclasses.replace(PRESETS[n], name=f"{n}-2l", layers=2)
+    for n in ("llama3.1-8b", "moe-mxfp4", "mistral-small-24b")
 }
 
 
 def shape(name: str) -> ModelShape:
-    if name in PRESETS:
-        return PRESETS[name]
-    if name in TINY:
-        return TINY[name]
+    for table in (PRESETS, TINY, TRUNCATED):
+        if name in table:
+            return table[name]
     raise KeyError(f"unknown model shape {name!r}")
 
 
@@ -135,6 +153,8 @@ def write_model(shp: ModelShape, out_dir: str, seed: int = 1234,
         args.append("--qk-norm")
     if shp.untied:
         args.append("--untied")
+    if shp.rope_interleaved:
+        args.append("--rope-interleaved")
     if shp.experts:
         args += ["--experts", str(shp.experts), "--experts-per-tok",
                  str(shp.experts_per_tok)]

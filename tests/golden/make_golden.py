@@ -15,7 +15,6 @@ tiny seeded synthetic models. Each fixture (<shape>.npz) holds:
 Usage: python tests/golden/make_golden.py [shape ...]
 """
 import hashlib
-import json
 import os
 import subprocess
 import sys
@@ -25,36 +24,13 @@ import numpy as np
 
 REPO = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, REPO)
+from oracle import ref_manifest  # noqa: E402
 from strasgpt_amd import synth  # noqa: E402
 
-HARNESS = os.path.join(REPO, "oracle", "_ref", "ref_harness")
-SHAPES = ["tiny-llama", "tiny-qwen", "tiny-chunk"]
+HARNESS = ref_manifest.HARNESS
+SHAPES = ["tiny-llama", "tiny-qwen", "tiny-chunk", "tiny-rope-il", "tiny-rope-il128"]
 MODEL_SEED = 7
 PROMPT_SEED = 3
-
-
-def manifest(model_dir, prompt, steps):
-    cfg = json.load(open(os.path.join(model_dir, "config.json")))
-    table = synth.tensor_table(model_dir)
-    files = []
-    for t in table:
-        if t[3] not in files:
-            files.append(t[3])
-    head_dim = cfg.get("head_dim") or cfg["hidden_size"] // cfg["num_attention_heads"]
-    lines = [" ".join(str(v) for v in (
-        cfg["hidden_size"], head_dim, cfg["intermediate_size"],
-        cfg["num_hidden_layers"], cfg["num_attention_heads"],
-        cfg["num_key_value_heads"], cfg["vocab_size"],
-        cfg["max_position_embeddings"], repr(cfg["rms_norm_eps"]),
-        repr(cfg["rope_theta"]), 0))]
-    lines.append(f"{len(files)} " + " ".join(files))
-    lines.append(str(len(table)))
-    lines += [f"{n} {files.index(p)} {o} {s}" for n, _, _, p, o, s in table]
-    lines.append(f"{len(prompt)} " + " ".join(map(str, prompt)))
-    lines.append(str(steps))
-    path = os.path.join(model_dir, "manifest.txt")
-    open(path, "w").write("\n".join(lines) + "\n")
-    return path
 
 
 def run(manifest_path, out, layers=None):
@@ -69,7 +45,7 @@ def make(name):
     synth.write_model(shp, d, seed=MODEL_SEED)
     prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, PROMPT_SEED)
     steps = shp.decode_len + 1
-    man = manifest(d, prompt, steps)
+    man = ref_manifest.write(d, prompt, steps)
     last = len(prompt) % 512 or 512
     hidden = []
     for layers in range(1, shp.layers + 1):

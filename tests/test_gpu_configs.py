@@ -1,0 +1,164 @@
+"""The benchmark configurations that are too large for the CPU oracle at full
+depth, on the GPU through the C-ABI:
+
+* Llama-3.1-8B-shaped, 8192-token prompt + 256 decode tokens (16 prefill
+  chunks of the reference's 512, decode attention over 8.4K keys),
+* the MXFP4 MoE decoder (32 experts, top-4, 64 q heads, vocab 201088),
+  256-token prompt + 128 decode tokens,
+* Mistral-Small-24B-shaped (d 5120, FFN 32768), 2048-token prompt + 128
+  decode tokens.
+
+Two checks per configuration:
+
+1. Full width and full prompt/decode length on two layers, against the
+   oracle: the prefill logits and the logits of every decode step within
+   2e-2 relative / 1e-3 absolute, greedy tokens identical (host loop over
+   transformer_predict, and the device-resident greedy loop).
+2. Full depth (every layer), properties that need no CPU reference:
+   graph-replayed and eager decode give identical tokens; the logits of
+   single-token decode steps equal the last rows of one prefill over
+   prompt + generated tokens (different kernels: GEMV vs MFMA GEMM,
+   split-K vs tiled attention); the host argmax of each step's logits is
+   the token the device loop chose; for prompts longer than 512 tokens,
+   device prefill chunks of 512 rows and of the whole prompt give the same
+   last-row logits.
+"""
+import contextlib
+import os
+import shutil
+import tempfile
+import time
+
+import numpy as np
+import pytest
+
+from strasgpt_amd import synth
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+RTOL, ATOL = 2e-2, 1e-3
+MODEL_SEED = 7
+
+
+def log(msg):
+    print(f"[configs] {msg}", flush=True)
+
+
+def runtime():
+    from strasgpt_amd import runtime as rt
+    rt.lib()
+    return rt
+
+
+def ref_argmax():
+    """The reference sample_argmax (source/sampler.c:92-102) from the oracle."""
+    from oracle import oracle as orc
+    lib = orc.load_lib()
+    return lambda row: int(lib.oracle_argmax(orc.fptr(np.ascontiguousarray(row, np.float32)),
+                                             row.size))
+
+
+@contextlib.contextmanager
+def written_model(name):
+    """A model directory written for one test and deleted after it (the
+    full-depth models take 14-47 GB of host memory under /dev/shm)."""
+    base = "/dev/shm" if os.access("/dev/shm", os.W_OK) else None
+    d = tempfile.mkdtemp(prefix=f"strasgpt_{name}_", dir=base)
+    try:
+        t0 = time.time()
+        synth.write_model(synth.shape(name), d, seed=MODEL_SEED)
+        log(f"{name}: model written in {time.time() - t0:.1f}s")
+        yield d
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def check_logits(got, want, what):
+    err = float(np.abs(got - want).max())
+    log(f"{what}: max |logit error| {err:.3g} (largest |logit| {float(np.abs(want).max()):.3g})")
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL, err_msg=what)
+
+
+@pytest.mark.timeout(1200)
+@pytest.mark.parametrize("name", ["llama3.1-8b-2l", "moe-mxfp4-2l", "mistral-small-24b-2l"])
+def test_truncated_config_against_oracle(name):
+    rt = runtime()
+    from oracle import oracle as orc
+    amax = ref_argmax()
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, 42)
+    steps = shp.decode_len + 1
+    with written_model(name) as d:
+        t0 = time.time()
+        with rt.Transformer(d) as t:
+            g_logits = [t.predict(prompt)[0]]
+            g_tok = [amax(g_logits[0])]
+            while len(g_tok) < steps:
+                g_logits.append(t.predict([g_tok[-1]])[0])
+                g_tok.append(amax(g_logits[-1]))
+            t.reset()
+            dev_tok, _ = t.generate(prompt, steps)
+        log(f"{name}: GPU host loop and device loop done in {time.time() - t0:.1f}s")
+        t0 = time.time()
+        om = orc.OracleModel(d, threads=16)
+        ol = om.predict(prompt)[0]
+        log(f"{name}: oracle prefill of {len(prompt)} tokens in {time.time() - t0:.1f}s")
+        check_logits(g_logits[0], ol, f"{name} prefill")
+        o_tok = [amax(ol)]
+        worst = 0.0
+        t0 = time.time()
+        while len(o_tok) < steps:
+            if o_tok != g_tok[:len(o_tok)]:
+                break  # inputs differ from here on: the token assertion reports it
+            row = om.predict([o_tok[-1]])[0]
+            np.testing.assert_allclose(g_logits[len(o_tok)], row, rtol=RTOL, atol=ATOL,
+                                       err_msg=f"{name} decode step {len(o_tok)}")
+            worst = max(worst, float(np.abs(g_logits[len(o_tok)] - row).max()))
+            o_tok.append(amax(row))
+        om.close()
+        log(f"{name}: oracle decode of {len(o_tok) - 1} steps in {time.time() - t0:.1f}s; "
+            f"max |logit error| over the steps {worst:.3g}")
+    log(f"{name}: tokens {g_tok[:10]}...")
+    assert g_tok == o_tok
+    assert dev_tok == o_tok
+
+
+@pytest.mark.timeout(1200)
+@pytest.mark.parametrize("name", ["llama3.1-8b", "moe-mxfp4", "mistral-small-24b"])
+def test_full_config_properties(name, monkeypatch):
+    rt = runtime()
+    amax = ref_argmax()
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, 42)
+    steps = shp.decode_len + 1
+    n_chk = 8
+    with written_model(name) as d:
+        with rt.Transformer(d) as t:
+            log(f"{name}: loaded ({shp.layers} layers)")
+            gtok, tm = t.generate(prompt, steps)
+            log(f"{name}: graph decode {tm.decode_count} tokens in {tm.decode_s * 1e3:.1f} ms, "
+                f"prefill {tm.prefill_s * 1e3:.1f} ms")
+            t.set_decode_mode(rt.DECODE_EAGER)
+            t.reset()
+            etok, _ = t.generate(prompt, steps)
+            t.set_decode_mode(rt.DECODE_GRAPH)
+            assert etok == gtok, "eager and graph-replayed decode differ"
+            # single-token steps over the first generated tokens
+            t.reset()
+            first = t.predict(prompt)[0]
+            assert amax(first) == gtok[0]
+            step_logits = [t.predict([tok])[0] for tok in gtok[:n_chk]]
+            for i, row in enumerate(step_logits):
+                assert amax(row) == gtok[i + 1], f"step {i + 1}: host argmax != device loop"
+            # the same positions as the last rows of one prefill
+            t.reset()
+            rows = t.predict(prompt + gtok[:n_chk], logits_count=n_chk)
+            for i in range(n_chk):
+                check_logits(rows[i], step_logits[i], f"{name} prefill row vs decode step {i + 1}")
+        if len(prompt) > 512:
+            monkeypatch.setenv("STRASGPT_PREFILL_CHUNK", "512")
+            with rt.Transformer(d) as t:
+                small = t.predict(prompt)[0]
+            check_logits(small, first, f"{name} prefill in 512-row chunks vs one chunk")
+            assert amax(small) == gtok[0]
+    log(f"{name}: tokens {gtok[:10]}...")

@@ -37,7 +37,10 @@ def oracle_model(d, threads=16):
     return orc.OracleModel(d, threads=threads)
 
 
-@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk"])
+GOLDEN_SHAPES = ["tiny-llama", "tiny-qwen", "tiny-chunk", "tiny-rope-il", "tiny-rope-il128"]
+
+
+@pytest.mark.parametrize("name", GOLDEN_SHAPES)
 def test_tiny_golden(name, model_dir):
     """Tokens identical to the reference C run; logits within tolerance."""
     rt = runtime()
@@ -199,12 +202,12 @@ def test_prefill_after_decode_steps(name, model_dir):
     assert err <= 2e-3 * scale
 
 
-@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk", "tiny-long"])
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk", "tiny-long",
+                                  "tiny-rope-il", "tiny-rope-il128"])
 def test_decode_modes_agree(name, model_dir):
-    """The persistent decode step (one launch per token), the graph-replayed
-    per-kernel step and the same kernels launched eagerly give identical
-    greedy tokens, equal to the oracle's; a second persistent run after
-    reset repeats the first (barrier state carried across launches)."""
+    """The graph-replayed decode step and the same kernels launched eagerly
+    give identical greedy tokens, equal to the oracle's; a second graph run
+    after reset repeats the first."""
     rt = runtime()
     d = model_dir(name)
     shp = synth.shape(name)
@@ -213,30 +216,27 @@ def test_decode_modes_agree(name, model_dir):
     om = oracle_model(d, 4)
     otok = om.generate(prompt, steps)
     with rt.Transformer(d) as t:
-        assert t.decode_persistent_supported
         got = {}
-        for mode in (rt.DECODE_PERSISTENT, rt.DECODE_GRAPH, rt.DECODE_EAGER):
+        for mode in (rt.DECODE_GRAPH, rt.DECODE_EAGER):
             t.set_decode_mode(mode)
             t.reset()
             got[mode], _ = t.generate(prompt, steps)
-        t.set_decode_mode(rt.DECODE_PERSISTENT)
+        t.set_decode_mode(rt.DECODE_GRAPH)
         t.reset()
         again, _ = t.generate(prompt, steps)
     log(f"{name}: oracle {otok}")
-    log(f"{name}: persistent {got[rt.DECODE_PERSISTENT]} graph {got[rt.DECODE_GRAPH]}")
-    assert got[rt.DECODE_PERSISTENT] == otok
+    log(f"{name}: graph {got[rt.DECODE_GRAPH]} eager {got[rt.DECODE_EAGER]}")
     assert got[rt.DECODE_GRAPH] == otok
     assert got[rt.DECODE_EAGER] == otok
     assert again == otok
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-long"])
-def test_persistent_step_logits(name, model_dir):
-    """Single-token transformer_predict in DECODE_PERSISTENT mode runs the
-    persistent decode step; its logits (every layer, attention over the
-    cache, final norm) and its captured hidden states agree with the
-    oracle's at each of several positions, and the logits with the
-    per-kernel path's (DECODE_EAGER)."""
+@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-rope-il128"])
+def test_decode_step_logits(name, model_dir):
+    """Single-token transformer_predict calls (decode GEMVs, split-K
+    attention over the cache, final norm): logits at each of several
+    positions and the hidden states of the last step agree with the
+    oracle's."""
     rt = runtime()
     d = model_dir(name)
     shp = synth.shape(name)
@@ -245,12 +245,9 @@ def test_persistent_step_logits(name, model_dir):
     om = oracle_model(d, 4)
     om.predict(prompt)
     with rt.Transformer(d) as t:
-        assert t.decode_persistent_supported
-        t.set_decode_mode(rt.DECODE_PERSISTENT)
         t.predict(prompt)
         for i, tok in enumerate(nxt):
-            capture = i == len(nxt) - 1  # residual stream after every layer too
-            if capture:
+            if i == len(nxt) - 1:  # the residual stream after every layer too
                 ol, oh, of = om.predict([tok], capture=True)
                 gl, gh, gf = t.predict([tok], capture=True)
                 np.testing.assert_allclose(gh, oh, rtol=RTOL, atol=ATOL)
@@ -259,37 +256,103 @@ def test_persistent_step_logits(name, model_dir):
                 ol = om.predict([tok])
                 gl = t.predict([tok])
             err = np.abs(gl - ol).max()
-            log(f"{name}: persistent step logits max |error| {err:.3g}")
+            log(f"{name}: decode step logits max |error| {err:.3g}")
             np.testing.assert_allclose(gl, ol, rtol=RTOL, atol=ATOL)
             assert err < 1e-3
-        t.reset()
-        t.set_decode_mode(rt.DECODE_EAGER)
-        t.predict(prompt)
-        el = [t.predict([tok]) for tok in nxt]
-        t.reset()
-        t.set_decode_mode(rt.DECODE_PERSISTENT)
-        t.predict(prompt)
-        pl = [t.predict([tok]) for tok in nxt]
-    for a, b in zip(el, pl):
-        np.testing.assert_allclose(b, a, rtol=1e-4, atol=1e-5)
 
 
-def test_grid_barrier_visibility():
-    """The fence-free grid barrier of the persistent decode step: values
-    written with agent-coherent stores before a barrier are read back by
-    another block after it, on every round (no stale value, no time-out)."""
-    import ctypes
+def test_reset_starts_a_new_sequence(model_dir):
+    """After transformer_reset, a new sequence that starts with single-token
+    steps (which write cache rows but not the prefill attention's bf16
+    planes) and then prefills the rest attends to its own rows, not to the
+    previous sequence's: last-row logits agree with the oracle on the new
+    sequence alone."""
     rt = runtime()
-    L = rt.lib()
-    d = ctypes.c_double
-    fn = L.strasgpt_kbench_barrier
-    fn.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(d), ctypes.POINTER(ctypes.c_int),
-                                        ctypes.POINTER(ctypes.c_int)]
-    for blocks in (64, 256):
-        us, bad, to = d(), ctypes.c_int(), ctypes.c_int()
-        rc = fn(blocks, 300, 2, 256, ctypes.byref(us), ctypes.byref(bad), ctypes.byref(to))
-        log(f"barrier: {blocks} blocks, {us.value:.2f} us/round")
-        assert rc == 0 and bad.value == 0 and to.value == 0
+    d = model_dir("tiny-chunk")
+    a = synth.prompt_tokens(128, 300, 41)
+    b = synth.prompt_tokens(128, 120, 43)
+    om = oracle_model(d, 4)
+    ol = om.predict(b)
+    with rt.Transformer(d) as t:
+        t.predict(a)
+        t.reset()
+        for tok in b[:45]:
+            t.predict([tok])
+        gl = t.predict(b[45:])
+    err = np.abs(gl - ol).max()
+    log(f"reset: max |logit error| {err:.3g}")
+    np.testing.assert_allclose(gl, ol, rtol=RTOL, atol=ATOL)
+    assert err < 1e-3
+
+
+def _ref_argmax(x):
+    """sample_argmax (source/sampler.c:92-102), as a sequential scan."""
+    best, bv = 0, x[0]
+    for i in range(1, len(x)):
+        if x[i] > bv:
+            best, bv = i, x[i]
+    return best
+
+
+def test_device_argmax_planted():
+    """sampler_argmax on the device against the reference's sequential scan
+    on planted cases: ties across block boundaries (the device reduces 512
+    blocks of 256-element slices), NaN at index 0 (never replaced), NaNs
+    elsewhere (never win), infinities, all-equal and single-element inputs,
+    the benchmark vocabulary sizes."""
+    rt = runtime()
+    rng = np.random.default_rng(5)
+    cases = []
+    for n in (1, 7, 256, 257, 131072, 151936, 201088):
+        cases.append(("random", rng.standard_normal(n).astype(np.float32)))
+    n = 201088
+    base = rng.standard_normal(n).astype(np.float32)
+    tie = base.copy(); tie[[300, 70000, 200000]] = 9.0  # ties in different blocks
+    cases.append(("ties across blocks", tie))
+    tie2 = base.copy(); tie2[[511, 512]] = 9.0  # adjacent, straddling a slice edge
+    cases.append(("adjacent tie", tie2))
+    late = base.copy(); late[n - 1] = 9.0
+    cases.append(("max at the end", late))
+    nan0 = base.copy(); nan0[0] = np.nan; nan0[1000] = 9.0
+    cases.append(("NaN at 0", nan0))
+    nans = base.copy(); nans[::7] = np.nan; nans[12345] = 9.0; nans[99999] = 9.0
+    cases.append(("NaNs elsewhere", nans))
+    allnan = np.full(1000, np.nan, np.float32); allnan[0] = 1.0
+    cases.append(("all NaN but the first", allnan))
+    inf = base.copy(); inf[[10, 150000]] = np.inf
+    cases.append(("+inf ties", inf))
+    ninf = np.full(70000, -np.inf, np.float32)
+    cases.append(("all -inf", ninf))
+    ninf2 = ninf.copy(); ninf2[[40000, 50000]] = -1.0
+    cases.append(("-inf but two", ninf2))
+    same = np.full(100000, 0.5, np.float32)
+    cases.append(("all equal", same))
+    zeros = np.zeros(3000, np.float32); zeros[0] = -0.0; zeros[2999] = 0.0
+    cases.append(("signed zeros", zeros))
+    for what, x in cases:
+        got, want = rt.argmax(x), _ref_argmax(x.tolist())
+        log(f"argmax {what} (n={x.size}): device {got} reference {want}")
+        assert got == want, what
+
+
+def test_strasgpt_host_loop_openmp_team(model_dir):
+    """The reference's calling convention (source/strasgpt.c:206-252): the
+    driver's --host-loop calls transformer_predict from every thread of an
+    8-thread OpenMP team and samples on the host; the ids equal the
+    reference run's golden ids, and equal the device loop's."""
+    from strasgpt_amd import _paths
+    g = np.load(os.path.join(GOLDEN_DIR, "tiny-qwen.npz"))
+    prompt = " ".join(str(int(v)) for v in g["prompt"])
+    want = [int(v) for v in g["generated"]]
+    d = model_dir("tiny-qwen")
+    exe = _paths.driver_exe()
+    for extra in (["--host-loop", "-t", "8"], []):
+        cmd = [exe, "-m", d, "-n", str(len(want)), "--temp", "0", "--pre-tokenized", "-p", prompt] + extra
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+        log(f"strasgpt {' '.join(extra) or '(device loop)'}: rc {r.returncode} out {r.stdout.strip()}")
+        assert r.returncode == 0, r.stderr[-2000:]
+        assert [int(v) for v in r.stdout.split()] == want
+        assert "Prompt processing (prefill)" in r.stderr
 
 
 def test_mxfp4_device_decode_exact():
@@ -351,7 +414,6 @@ def test_moe_tiny_against_oracle(name, model_dir):
     om.reset()
     otok = om.generate(prompt, 9)
     with rt.Transformer(d) as t:
-        assert not t.decode_persistent_supported  # MoE layers: per-kernel path
         gl = t.predict(prompt)
         t.reset()
         gtok, _ = t.generate(prompt, 9)

@@ -90,8 +90,9 @@ def write_min_model(d, config, header_obj=None, dtype="BF16"):
         f.write(config)
     hdr = header_obj or {"model.norm.weight": {"dtype": dtype, "shape": [4], "data_offsets": [0, 8]}}
     h = json.dumps(hdr).encode()
+    end = max(v["data_offsets"][1] for k, v in hdr.items() if k != "__metadata__")
     with open(os.path.join(d, "model.safetensors"), "wb") as f:
-        f.write(struct.pack("<Q", len(h)) + h + b"\0" * 8)
+        f.write(struct.pack("<Q", len(h)) + h + b"\0" * end)
 
 
 def run_loader(d):
@@ -111,7 +112,10 @@ def test_config_semantics(tmp_path):
     write_min_model(d, '{"hidden_size": 64, "num_attention_heads": 4, "rms_norm_eps": 1e-06,'
                        ' "rope_theta": 1e6, "text_config": {"num_hidden_layers": 3},'
                        ' "rope_scaling": {"mrope_section": [2, 3], "mrope_interleaved": true},'
-                       ' "eos_token_id": [7, 8], "unknown": {"model": [1, {"vocab": null}]}}')
+                       ' "eos_token_id": [7, 8], "unknown": {"model": [1, {"vocab": null}]}}',
+                    header_obj={"__metadata__": {"format": "pt"},
+                                "model.norm.weight": {"dtype": "BF16", "shape": [4],
+                                                      "data_offsets": [24, 32]}})
     lib, p = load(d)
     s = p.contents
     assert s.head_dim == 16  # hidden_size / heads default (json_parser.y:616-619)
@@ -119,7 +123,11 @@ def test_config_semantics(tmp_path):
     assert s.rope_interleaved
     assert list(s.mrope_section[:s.mrope_section_count]) == [2, 3]
     assert s.eos_token_id == 7
-    assert s.tensor_count == 1 and s.tensor[0].offset == 8 + s.tensor[0].offset - 8
+    # file offset of a tensor = 8 + header length + data_offsets begin
+    hl, hdr = synth.read_header(os.path.join(d, "model.safetensors"))
+    assert hdr["model.norm.weight"]["data_offsets"] == [24, 32]
+    assert s.tensor_count == 1 and s.tensor[0].offset == 8 + hl + 24
+    assert s.tensor[0].size == 8
 
 
 @pytest.mark.parametrize("config,msg", [
