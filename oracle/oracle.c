@@ -55,9 +55,27 @@ float oracle_mxfp4_value(uint8_t code, uint8_t scale) {
   return (code & 8) ? -v : v;
 }
 
+/* The same values as oracle_mxfp4_value element by element: per 32-value
+ * block, the 16 codes times the block's power of two (2^(scale - 127),
+ * subnormal for scale 0), each product exact. */
 void oracle_mxfp4_dequant(const uint8_t* blocks, const uint8_t* scales,
                           size_t value_count, float* out) {
-  for (size_t i = 0; i < value_count; i++) {
+  static const float val[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                                -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+  for (size_t b = 0; b < value_count / 32; b++) {
+    const uint8_t sc = scales[b];
+    if (sc == 255) {
+      for (int i = 0; i < 32; i++) out[b * 32 + i] = NAN;
+      continue;
+    }
+    const float p2 = ldexpf(1.0f, (int)sc - 127);
+    for (int i = 0; i < 16; i++) {
+      const uint8_t byte = blocks[b * 16 + i];
+      out[b * 32 + 2 * i] = val[byte & 15] * p2;
+      out[b * 32 + 2 * i + 1] = val[byte >> 4] * p2;
+    }
+  }
+  for (size_t i = value_count / 32 * 32; i < value_count; i++) {
     uint8_t byte = blocks[i / 2];
     uint8_t code = (i & 1) ? (byte >> 4) : (byte & 15);
     out[i] = oracle_mxfp4_value(code, scales[i / 32]);
@@ -364,44 +382,81 @@ static const uint16_t* W(const oracle_model_t* m, int cls, size_t layer) {
   return (const uint16_t*)m->w[cls] + layer * m->per_layer[cls];
 }
 
-/* Expert FFN of one token: reference SwiGLU FFN (source/transformer.c:
- * 1461-1504) with MXFP4 weights, per selected expert, accumulated as
- * acc = fmaf(weight_j, expert_j(x), acc) in top-k order. */
-static void moe_token(const oracle_model_t* m, size_t l, const float* xn, float* out) {
+/* Expert FFN of T tokens: per token, the router logits (bf16 dot), top-k
+ * with softmax over the selected logits, then the reference SwiGLU FFN
+ * (source/transformer.c:1461-1504) with MXFP4 weights per selected expert,
+ * accumulated as out = fmaf(weight_j, expert_j(x), out) in top-k order from
+ * 0. Work is grouped by expert so that each weight row is dequantised once
+ * per chunk; every dot product and the accumulation order per token are
+ * those of the per-token formulation. */
+static void moe_chunk(const oracle_model_t* m, size_t l, size_t T, const float* xn, float* out) {
   const oracle_config_t* c = &m->c;
   size_t d = c->embedding_dim, H = c->hidden_dim, E = c->expert_count, K = c->expert_used_count;
-  float logits[1024];
-  int sel[64];
-  float wsel[64];
-  for (size_t e = 0; e < E; e++) logits[e] = oracle_dot_bf16(d, xn, W(m, ORACLE_ROUTER, l) + e * d);
-  oracle_topk_softmax(E, logits, K, sel, wsel);
-  float* a = malloc(H * sizeof(float));
-  float* row = malloc((H > d ? H : d) * sizeof(float));
-  for (size_t e = 0; e < d; e++) out[e] = 0.0f;
+  int* sel = malloc(T * K * sizeof(int));
+  float* wsel = malloc(T * K * sizeof(float));
+  float* act = malloc(T * K * H * sizeof(float));
+  float* dn = malloc(T * K * d * sizeof(float));
+  size_t* pairs = malloc(T * K * sizeof(size_t));
+  #pragma omp parallel for schedule(static)
+  for (size_t t = 0; t < T; t++) {
+    float logits[1024];
+    for (size_t e = 0; e < E; e++)
+      logits[e] = oracle_dot_bf16(d, xn + t * d, W(m, ORACLE_ROUTER, l) + e * d);
+    oracle_topk_softmax(E, logits, K, sel + t * K, wsel + t * K);
+  }
   const uint8_t* gb = (const uint8_t*)m->w[ORACLE_GATE_BLOCKS] + l * m->per_layer[ORACLE_GATE_BLOCKS];
   const uint8_t* gs = (const uint8_t*)m->w[ORACLE_GATE_SCALES] + l * m->per_layer[ORACLE_GATE_SCALES];
   const uint8_t* ub = (const uint8_t*)m->w[ORACLE_UP_BLOCKS] + l * m->per_layer[ORACLE_UP_BLOCKS];
   const uint8_t* us = (const uint8_t*)m->w[ORACLE_UP_SCALES] + l * m->per_layer[ORACLE_UP_SCALES];
   const uint8_t* db = (const uint8_t*)m->w[ORACLE_DOWN_BLOCKS] + l * m->per_layer[ORACLE_DOWN_BLOCKS];
   const uint8_t* ds = (const uint8_t*)m->w[ORACLE_DOWN_SCALES] + l * m->per_layer[ORACLE_DOWN_SCALES];
-  for (size_t j = 0; j < K; j++) {
-    size_t e = (size_t)sel[j];
-    for (size_t h = 0; h < H; h++) {
-      size_t r = e * H + h;
-      oracle_mxfp4_dequant(gb + r * d / 2, gs + r * d / 32, d, row);
-      float g = dot_f32(d, xn, row);
-      oracle_mxfp4_dequant(ub + r * d / 2, us + r * d / 32, d, row);
-      float u = dot_f32(d, xn, row);
-      a[h] = silu_mul(g, u);
+  for (size_t e = 0; e < E; e++) {
+    size_t np = 0;  /* (token, slot) pairs routed to expert e */
+    for (size_t p = 0; p < T * K; p++)
+      if ((size_t)sel[p] == e) pairs[np++] = p;
+    if (!np) continue;
+    #pragma omp parallel
+    {
+      float* rg = malloc(d * sizeof(float));
+      float* ru = malloc(d * sizeof(float));
+      #pragma omp for schedule(static)
+      for (size_t h = 0; h < H; h++) {
+        size_t r = e * H + h;
+        oracle_mxfp4_dequant(gb + r * d / 2, gs + r * d / 32, d, rg);
+        oracle_mxfp4_dequant(ub + r * d / 2, us + r * d / 32, d, ru);
+        for (size_t i = 0; i < np; i++) {
+          const float* x = xn + (pairs[i] / K) * d;
+          act[pairs[i] * H + h] = silu_mul(dot_f32(d, x, rg), dot_f32(d, x, ru));
+        }
+      }
+      free(rg);
+      free(ru);
     }
-    for (size_t o = 0; o < d; o++) {
-      size_t r = e * d + o;
-      oracle_mxfp4_dequant(db + r * H / 2, ds + r * H / 32, H, row);
-      out[o] = fmaf(wsel[j], dot_f32(H, a, row), out[o]);
+    #pragma omp parallel
+    {
+      float* rd = malloc(H * sizeof(float));
+      #pragma omp for schedule(static)
+      for (size_t o = 0; o < d; o++) {
+        size_t r = e * d + o;
+        oracle_mxfp4_dequant(db + r * H / 2, ds + r * H / 32, H, rd);
+        for (size_t i = 0; i < np; i++) dn[pairs[i] * d + o] = dot_f32(H, act + pairs[i] * H, rd);
+      }
+      free(rd);
     }
   }
-  free(a);
-  free(row);
+  #pragma omp parallel for schedule(static)
+  for (size_t t = 0; t < T; t++) {
+    for (size_t o = 0; o < d; o++) {
+      float acc = 0.0f;
+      for (size_t j = 0; j < K; j++) acc = fmaf(wsel[t * K + j], dn[(t * K + j) * d + o], acc);
+      out[t * d + o] = acc;
+    }
+  }
+  free(sel);
+  free(wsel);
+  free(act);
+  free(dn);
+  free(pairs);
 }
 
 /* out(r, t) = dot(K, x[t], w[r]) for r < R, t < T, in blocks of 16 rows x
@@ -522,8 +577,7 @@ static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc
       for (size_t i = 0; i < T * H; i++) g[i] = silu_mul(g[i], u[i]);
       project(d, T, H, W(m, ORACLE_DOWN, l), g, H, store_rows, &sd);
     } else {
-      #pragma omp parallel for schedule(dynamic, 1)
-      for (size_t t = 0; t < T; t++) moe_token(m, l, xn + t * d, tmp + t * d);
+      moe_chunk(m, l, T, xn, tmp);
     }
     for (size_t i = 0; i < T * d; i++) x[i] += tmp[i];
     if (m->cap) memcpy(m->cap + (l * cap_rows + cap_row) * d, x, T * d * sizeof(float));

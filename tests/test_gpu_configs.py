@@ -15,13 +15,24 @@ Two checks per configuration:
    2e-2 relative / 1e-3 absolute, greedy tokens identical (host loop over
    transformer_predict, and the device-resident greedy loop).
 2. Full depth (every layer), properties that need no CPU reference:
-   graph-replayed and eager decode give identical tokens; the logits of
-   single-token decode steps equal the last rows of one prefill over
-   prompt + generated tokens (different kernels: GEMV vs MFMA GEMM,
-   split-K vs tiled attention); the host argmax of each step's logits is
-   the token the device loop chose; for prompts longer than 512 tokens,
-   device prefill chunks of 512 rows and of the whole prompt give the same
-   last-row logits.
+   graph-replayed and eager decode give identical tokens; after the same
+   prompt prefill, single-token decode steps and one multi-token chunk of
+   the same tokens give the same logits (different kernels: GEMV vs MFMA
+   GEMM, split-K vs tiled attention, MoE expert GEMVs vs grouped GEMMs);
+   the host argmax of each step's logits is the token the device loop
+   chose; for dense models, the same logits as the last rows of one
+   prefill over prompt + generated tokens; for prompts longer than 512
+   tokens, device prefill chunks of 512 rows and of the whole prompt give
+   the same last-row logits.
+
+   The MoE model is not compared across different prompt prefills: top-k
+   routing is discontinuous, and over 24 layers x 256 tokens some router
+   logits tie to within fp32 rounding. Two computations that differ only in
+   summation order (a 256-row and a 264-row prefill choose different
+   split-K counts) can then route such a token differently; that token's
+   keys and values change and every later position moves by ~1e-3. (On the
+   workload's seed, token 117 at layer 1: the oracle, a 256-row device
+   prefill and a 260-row one pick two different expert sets.)
 """
 import contextlib
 import os
@@ -101,8 +112,12 @@ def test_truncated_config_against_oracle(name):
         log(f"{name}: GPU host loop and device loop done in {time.time() - t0:.1f}s")
         t0 = time.time()
         om = orc.OracleModel(d, threads=16)
-        ol = om.predict(prompt)[0]
-        log(f"{name}: oracle prefill of {len(prompt)} tokens in {time.time() - t0:.1f}s")
+        # the prompt in pieces of 1024 tokens (the oracle, like the
+        # reference, runs 512-token chunks either way), one line per piece
+        for c0 in range(0, len(prompt), 1024):
+            ol = om.predict(prompt[c0:c0 + 1024])[0]
+            log(f"{name}: oracle prefill through token {min(len(prompt), c0 + 1024)} "
+                f"at {time.time() - t0:.1f}s")
         check_logits(g_logits[0], ol, f"{name} prefill")
         o_tok = [amax(ol)]
         worst = 0.0
@@ -150,11 +165,18 @@ def test_full_config_properties(name, monkeypatch):
             step_logits = [t.predict([tok])[0] for tok in gtok[:n_chk]]
             for i, row in enumerate(step_logits):
                 assert amax(row) == gtok[i + 1], f"step {i + 1}: host argmax != device loop"
-            # the same positions as the last rows of one prefill
+            # the same tokens as one chunk after the same prompt prefill
             t.reset()
-            rows = t.predict(prompt + gtok[:n_chk], logits_count=n_chk)
+            t.predict(prompt)
+            chunk = t.predict(gtok[:n_chk], logits_count=n_chk)
             for i in range(n_chk):
-                check_logits(rows[i], step_logits[i], f"{name} prefill row vs decode step {i + 1}")
+                check_logits(chunk[i], step_logits[i], f"{name} chunk row vs decode step {i + 1}")
+            if not shp.experts:
+                # and as the last rows of one prefill over prompt + tokens
+                t.reset()
+                rows = t.predict(prompt + gtok[:n_chk], logits_count=n_chk)
+                for i in range(n_chk):
+                    check_logits(rows[i], step_logits[i], f"{name} prefill row vs decode step {i + 1}")
         if len(prompt) > 512:
             monkeypatch.setenv("STRASGPT_PREFILL_CHUNK", "512")
             with rt.Transformer(d) as t:

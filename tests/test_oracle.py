@@ -77,6 +77,34 @@ def test_mxfp4_dequant_layout():
     np.testing.assert_array_equal(out, want.astype(np.float32))
 
 
+def test_mxfp4_dequant_all_scales_bitwise():
+    """The block dequantisation equals the closed form bit for bit for all
+    16 codes in both nibble positions under every one of the 256 scales
+    (scale 0 gives subnormal values, 255 NaN; code 8 is -0.0)."""
+    L = lib()
+    nblocks = 256
+    codes = np.empty((nblocks, 16), np.uint8)
+    for i in range(16):
+        codes[:, i] = i | ((15 - i) << 4)
+    scales = np.arange(256, dtype=np.uint8)
+    out = np.zeros(nblocks * 32, np.float32)
+    L.oracle_mxfp4_dequant(codes.ctypes.data, scales.ctypes.data, nblocks * 32, orc.fptr(out))
+    mag = np.array([0, .5, 1, 1.5, 2, 3, 4, 6])
+    c = np.empty((nblocks, 32), np.uint8)
+    c[:, 0::2] = codes & 15
+    c[:, 1::2] = codes >> 4
+    want = (np.where(c & 8, -1.0, 1.0) * mag[c & 7] *
+            2.0 ** (scales[:, None].astype(np.float64) - 127)).astype(np.float32)
+    want[255] = np.nan
+    got = out.reshape(nblocks, 32)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
+    scalar = np.array([[L.oracle_mxfp4_value(int(c[b, i]), int(b)) for i in range(32)]
+                       for b in range(0, 255, 17)], np.float32)
+    np.testing.assert_array_equal(scalar.view(np.uint32), want[0:255:17].view(np.uint32))
+
+
 def dot_model(a, w):
     """Reference AVX2 dot order (source/transformer.c:1095-1167) in float32."""
     a = np.asarray(a, np.float32)
