@@ -21,6 +21,19 @@ extern "C" {
  * every error of this library) when n is 0 or above INT_MAX. */
 size_t sampler_argmax(const float* probability, size_t n);
 
+/* sampler_argmax without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The values and the partial results are staged in one
+ * statically allocated device array of about 1 MiB, which each GPU the
+ * library runs on holds until the process ends. n is at most
+ * SAMPLER_ARGMAX_NOALLOC_MAX (larger n dies with an error message). Every
+ * call on one GPU uses that GPU's array: calls that overlap on the same
+ * GPU (from several host threads) race and must be serialised by the
+ * caller. Same result as sampler_argmax. */
+#define SAMPLER_ARGMAX_NOALLOC_MAX 262144
+size_t sampler_argmax_noalloc(const float* probability, size_t n);
+
 #ifdef __cplusplus
 }
 #endif
