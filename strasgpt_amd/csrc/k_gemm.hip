@@ -33,7 +33,6 @@ namespace sg {
 namespace {
 
 constexpr int BK = 32;
-constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
 __device__ __forceinline__ void store_split(uint16_t* hi, uint16_t* lo, size_t i, float v,
@@ -111,9 +110,10 @@ __device__ __forceinline__ int lds_swz(int r) {
 // WD = 1: the W tiles get a ring one stage deeper than the A tiles (A is
 // re-read by every column block and stays in cache; W streams from HBM once
 // per XCD), loads issued so that W has one more K step of latency cover.
+// NW: wavefronts per block, arranged NW/2 (rows) x 2 (columns).
 template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false, int OCC = 0, int KS = 32,
-          int WD = 0>
-__global__ __launch_bounds__(kThreads, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_kernel(GemmParams p) {
+          int WD = 0, int NW = 4>
+__global__ __launch_bounds__(NW * WAVE, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_kernel(GemmParams p) {
   constexpr bool SPLIT = PREC == GEMM_SPLIT2;
   constexpr bool DUAL = EPI == GEMM_SWIGLU;
   static_assert(KS == 32 || KS == 64, "K per stage");
@@ -122,21 +122,23 @@ __global__ __launch_bounds__(kThreads, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_ker
   constexpr int CPR = ROWB / 16;               // 16-byte chunks per row
   constexpr int RPI = 1024 / ROWB;             // rows per 1 KiB load instruction
   constexpr int KSUB = KS / 32;                // MFMA k-steps per stage
-  constexpr int WM = BM / 2, WN = BN / 2;      // wavefront tile
+  constexpr int WGM = NW / 2;                  // wavefront rows
+  constexpr int WM = BM / WGM, WN = BN / 2;    // wavefront tile
   constexpr int MT = WM / 16, NT = WN / 16;    // 16x16 MFMA tiles per wavefront
   constexpr int A_ROWS = BM * (SPLIT ? 2 : 1);
   constexpr int ROWS = A_ROWS + BN;            // rows per stage
   constexpr int GROUPS = ROWS / RPI;           // 1 KiB load instructions per stage
-  constexpr int PER_WAVE = GROUPS / (kThreads / WAVE);
-  static_assert(GROUPS % (kThreads / WAVE) == 0, "stage loads must split evenly over waves");
+  constexpr int PER_WAVE = GROUPS / NW;
+  static_assert(GROUPS % NW == 0, "stage loads must split evenly over waves");
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wavefront tile");
   static_assert(!DUAL || NT % 2 == 0, "SwiGLU tiles pair gate and up sub-tiles");
   constexpr int STAGE = ROWS * ROWB;           // bytes
   static_assert(!WD || !PIPE, "deep W ring without fragment pipelining");
   constexpr int NSW = NS + WD;                 // W ring depth
   constexpr int A_BYTES = A_ROWS * ROWB, W_BYTES = BN * ROWB;
   constexpr int GA = A_ROWS / RPI, GW = BN / RPI;
-  constexpr int PWA = GA / (kThreads / WAVE), PWW = GW / (kThreads / WAVE);
-  static_assert(!WD || (GA % (kThreads / WAVE) == 0 && GW % (kThreads / WAVE) == 0),
+  constexpr int PWA = GA / NW, PWW = GW / NW;
+  static_assert(!WD || (GA % NW == 0 && GW % NW == 0),
                 "deep W ring: A and W loads must split evenly over waves");
 
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(kThreads, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_ker
 }
 
 template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false, int OCC = 0, int KS = 32,
-          int WD = 0>
+          int WD = 0, int NW = 4>
 void launch(const GemmParams& p, int splits, hipStream_t s) {
   const int cols = EPI == GEMM_SWIGLU ? BN / 2 : BN;
   const int tiles = ((p.N + cols - 1) / cols) * ((p.M + BM - 1) / BM);
@@ -393,12 +395,12 @@ void launch(const GemmParams& p, int splits, hipStream_t s) {
   static_assert(shm <= 160 * 1024, "GEMM stages exceed LDS");
   static bool attr = false;
   if (!attr) {
-    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD>,
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD, NW>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
     attr = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD>), dim3(tiles, 1, splits), dim3(kThreads),
-                     shm, s, p);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD, NW>), dim3(tiles, 1, splits),
+                     dim3(NW * WAVE), shm, s, p);
 }
 
 // Tile shape forced by STRASGPT_GEMM_TILE ("128x256", "128x128",

@@ -318,6 +318,151 @@ __global__ __launch_bounds__(kThreads) void gemv2_kernel(GemvParams p) {
   __builtin_amdgcn_s_waitcnt(0);  // no load left in flight at exit
 }
 
+// Third form: gemv2's flat stream, with the input row staged by the
+// global-to-LDS DMA instead of through registers. Order of issue: the
+// RMSNorm weights of this thread (registers, K / 1024 uint2 at most
+// kV3Nw), the DMA of the row (no registers held), then the first PD weight
+// loads of the ring; waiting until only the ring loads are in flight
+// completes the first two. The RMSNorm is then applied in LDS. Without the
+// row in registers a wavefront holds the ring and little else, so more
+// wavefronts (and weight bytes) are in flight per CU.
+constexpr int kV3Nw = 8;  // uint2 of norm weights per thread: K <= 8192 with RMSNorm
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Waits until at most N vector-memory operations of this wavefront are in
+// flight (N <= 63).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_sched_barrier(0);
+  // s_waitcnt encoding (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int EPI, bool NORM, bool EXACT, int kPD>
+__global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
+  constexpr int NT = kThreads, WV = kWaves;
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [S * kStep], zero past K
+  __shared__ float red[WV];
+  constexpr bool DUAL = EPI == GEMV_SWIGLU;
+  constexpr int LOADS = kPD * (DUAL ? 2 : 1);  // ring loads issued before the staging wait
+  const int lane = threadIdx.x % WAVE;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int K = p.K, N = p.N;
+  const int S = (K + kStep - 1) / kStep;
+  const int groups = (N + WV - 1) / WV;
+  const int G = gridDim.x, per = (groups + G - 1) / G;
+  const int v = (G % kXcds == 0) ? (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds : blockIdx.x;
+  const int g0 = v * per;
+  const int glast = N - 1 - wave >= 0 ? (N - 1 - wave) / WV : -1;
+  const int nrows = max(0, min(min(groups, g0 + per), glast + 1) - g0);
+  const int T = nrows * S;
+
+  // 1. this thread's RMSNorm weights (elements tid*4 + i*1024)
+  uint2 nv[NORM ? kV3Nw : 1];
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < kV3Nw; i++) {
+      const int k = min((int)threadIdx.x * 4 + i * NT * 4, K - 4);
+      nv[i] = *(const uint2*)(p.norm_w + k);
+    }
+  }
+  // 2. the row into LDS: 16 bytes per lane, 1 KiB per wavefront instruction
+  const int slots = K / 4;
+  for (int u0 = wave * WAVE; u0 < slots; u0 += NT) {
+    const int u = u0 + lane;
+    if (u < slots)  // inactive lanes write nothing
+      __builtin_amdgcn_global_load_lds((const void*)(p.x + u * 4), (lds_ptr_t)(xs + u0 * 4), 16, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the row's DMA is issued before the ring loads
+  // 3. the ring
+  uint4 w[kPD], w2[DUAL ? kPD : 1];
+  const int lk = lane * 8;
+  int rrow = 0, rstep = 0;
+  auto load = [&](uint4& a, uint4& b) {
+    const bool past = rrow >= nrows;  // wave-uniform
+    const size_t row = (size_t)min((g0 + rrow) * WV + wave, N - 1);
+    const int k = EXACT ? rstep * kStep + lk : min(rstep * kStep + lk, K - 8);
+    const uint16_t* wa = past ? (const uint16_t*)p.x + lk : p.w + row * K + k;
+    a = load_nt_u4(wa);
+    if (DUAL) b = load_nt_u4(past ? wa : p.w2 + row * K + k);
+    if (++rstep == S) {
+      rstep = 0;
+      rrow++;
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kPD; j++) load(w[j], w2[DUAL ? j : 0]);
+  wait_vm<LOADS>();  // norm weights and row landed; the ring stays in flight
+  __syncthreads();
+  for (int k = K + threadIdx.x; k < S * kStep; k += NT) xs[k] = 0.0f;
+  if (NORM) {  // (x * s) * w in LDS, the sum of squares in stage_row's partition and order
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kV3Nw; i++) {
+      const int k = (int)threadIdx.x * 4 + i * NT * 4;
+      if (k < K) {
+        const float4 xv = *(const float4*)(xs + k);
+        ss = fmaf(xv.x, xv.x, ss);
+        ss = fmaf(xv.y, xv.y, ss);
+        ss = fmaf(xv.z, xv.z, ss);
+        ss = fmaf(xv.w, xv.w, ss);
+      }
+    }
+    const float sc = rms_scale(block_sum<NT>(ss, red), K, p.eps);  // (contains a barrier)
+#pragma unroll
+    for (int i = 0; i < kV3Nw; i++) {
+      const int k = (int)threadIdx.x * 4 + i * NT * 4;
+      if (k < K) {
+        float4 o = *(const float4*)(xs + k);
+        o.x = (o.x * sc) * bf16_to_f32((uint16_t)(nv[i].x & 0xffffu));
+        o.y = (o.y * sc) * bf16_to_f32((uint16_t)(nv[i].x >> 16));
+        o.z = (o.z * sc) * bf16_to_f32((uint16_t)(nv[i].y & 0xffffu));
+        o.w = (o.w * sc) * bf16_to_f32((uint16_t)(nv[i].y >> 16));
+        *(float4*)(xs + k) = o;
+      }
+    }
+  }
+  __syncthreads();
+
+  float acc = 0.0f, acc2 = 0.0f;
+  int step = 0, rowi = 0;
+  for (int t0 = 0; t0 < T; t0 += kPD) {
+#pragma unroll
+    for (int j = 0; j < kPD; j++) {
+      if (t0 + j < T) {
+        const int k = step * kStep + lk;
+        uint4 a = w[j], b = w2[DUAL ? j : 0];
+        if (!EXACT) {  // past K: zero weights (x is zero there too)
+          const bool in = k < K;
+          a.x = in ? a.x : 0u;
+          a.y = in ? a.y : 0u;
+          a.z = in ? a.z : 0u;
+          a.w = in ? a.w : 0u;
+          b.x = in ? b.x : 0u;
+          b.y = in ? b.y : 0u;
+          b.z = in ? b.z : 0u;
+          b.w = in ? b.w : 0u;
+        }
+        const float4 xa = *(const float4*)(xs + k);
+        const float4 xb = *(const float4*)(xs + k + 4);
+        acc = dot8(a, xa, xb, acc);
+        if (DUAL) acc2 = dot8(b, xa, xb, acc2);
+        if (++step == S) {
+          const float r1 = wave_total(acc), r2 = DUAL ? wave_total(acc2) : 0.0f;
+          if (lane == 0) gemv_store<EPI>(p, (g0 + rowi) * WV + wave, r1, r2);
+          acc = acc2 = 0.0f;
+          step = 0;
+          rowi++;
+        }
+      }
+      load(w[j], w2[DUAL ? j : 0]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load left in flight at exit
+}
+
 // Blocks: at most `cap`, the same number of row groups for each block, and
 // a multiple of the XCD count when there are enough groups.
 int balanced_blocks(int groups, int cap) {
@@ -369,6 +514,38 @@ bool launch_v2(const GemvParams& p, hipStream_t s, int cap) {
   return true;
 }
 
+// The third form; false when the row does not fit (K >= 256, up to 64 KiB
+// of fp32 row; with RMSNorm K <= 8192).
+template <int EPI, int PD>
+bool launch_v3(const GemvParams& p, hipStream_t s, int cap) {
+  const int S = (p.K + kStep - 1) / kStep;
+  const size_t shm = (size_t)S * kStep * sizeof(float);
+  if (shm > (size_t)kV2Lds || p.K < 256 || (p.norm_w && p.K > kV3Nw * kThreads * 4)) return false;
+  const int groups = (p.N + kWaves - 1) / kWaves;
+  const int blocks = balanced_blocks(groups, cap);
+  static bool attr = false;
+  if (!attr) {
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemv3_kernel<EPI, true, true, PD>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kV2Lds));
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemv3_kernel<EPI, false, true, PD>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kV2Lds));
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemv3_kernel<EPI, true, false, PD>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kV2Lds));
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemv3_kernel<EPI, false, false, PD>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kV2Lds));
+    attr = true;
+  }
+  const bool exact = p.K % kStep == 0;
+  if (p.norm_w) {
+    if (exact) hipLaunchKernelGGL((gemv3_kernel<EPI, true, true, PD>), dim3(blocks), dim3(kThreads), shm, s, p);
+    else hipLaunchKernelGGL((gemv3_kernel<EPI, true, false, PD>), dim3(blocks), dim3(kThreads), shm, s, p);
+  } else {
+    if (exact) hipLaunchKernelGGL((gemv3_kernel<EPI, false, true, PD>), dim3(blocks), dim3(kThreads), shm, s, p);
+    else hipLaunchKernelGGL((gemv3_kernel<EPI, false, false, PD>), dim3(blocks), dim3(kThreads), shm, s, p);
+  }
+  return true;
+}
+
 template <int R, int U, int EPI>
 void launch(const GemvParams& p, hipStream_t s, int cap) {
   const bool lds = p.K <= kMaxLdsK;
@@ -397,20 +574,28 @@ void check(const GemvParams& p, int epi) {
 
 void gemv(const GemvParams& p, int epi, hipStream_t s) {
   check(p, epi);
+  // Forms and launch shapes from sweeps of the decode shapes on MI355X
+  // (weights streamed from HBM, back-to-back launches): the third form
+  // (row staged by DMA) where it was faster, else the flat-stream form,
+  // else the chunked form (rows beyond 64 KiB).
   switch (epi) {
-    // Flat-stream form where the row fits (steps in flight, block cap from
-    // sweeps of the decode shapes on MI355X), else the chunked form.
-    case GEMV_STORE:
-      if (!launch_v2<GEMV_STORE, 8>(p, s, 2048)) launch<1, 2, GEMV_STORE>(p, s, 2048);
+    case GEMV_STORE:  // logits
+      if (!launch_v3<GEMV_STORE, 4>(p, s, 8192) && !launch_v2<GEMV_STORE, 8>(p, s, 2048))
+        launch<1, 2, GEMV_STORE>(p, s, 2048);
       break;
-    case GEMV_RESIDUAL:
-      if (!launch_v2<GEMV_RESIDUAL, 8>(p, s, 256)) launch<1, 4, GEMV_RESIDUAL>(p, s, 4096);
+    case GEMV_RESIDUAL:  // O and down projections
+      if (!(p.N >= 2560 && launch_v3<GEMV_RESIDUAL, 4>(p, s, 768)) &&
+          !launch_v2<GEMV_RESIDUAL, 8>(p, s, 256))
+        launch<1, 4, GEMV_RESIDUAL>(p, s, 4096);
       break;
     case GEMV_QKV:
-      if (!launch_v2<GEMV_QKV, 4>(p, s, 1024)) launch<1, 2, GEMV_QKV>(p, s, 2048);
+      if (!launch_v3<GEMV_QKV, 4>(p, s, 768) && !launch_v2<GEMV_QKV, 4>(p, s, 1024))
+        launch<1, 2, GEMV_QKV>(p, s, 2048);
       break;
-    case GEMV_SWIGLU:
-      if (!launch_v2<GEMV_SWIGLU, 2>(p, s, 2048)) launch<1, 2, GEMV_SWIGLU>(p, s, 2048);
+    case GEMV_SWIGLU:  // gate/up: the third form pays from K > 4096
+      if (!(p.K > 4096 && launch_v3<GEMV_SWIGLU, 2>(p, s, 1024)) &&
+          !launch_v2<GEMV_SWIGLU, 2>(p, s, 2048))
+        launch<1, 2, GEMV_SWIGLU>(p, s, 2048);
       break;
     default: ST_DIE("unknown GEMV epilogue");
   }
