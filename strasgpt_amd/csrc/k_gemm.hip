@@ -105,19 +105,16 @@ __device__ __forceinline__ int lds_swz(int r) {
   return KS == 32 ? (0 - (r >> 2)) & 3 : (r >> 1) & 7;
 }
 
-// OCC: blocks per CU the register allocation must allow (0: two with
-// fragment pipelining, else one).
+// OCC: blocks per CU the register allocation must allow (0: one).
 // WD = 1: the W tiles get a ring one stage deeper than the A tiles (A is
 // re-read by every column block and stays in cache; W streams from HBM once
 // per XCD), loads issued so that W has one more K step of latency cover.
 // NW: wavefronts per block, arranged NW/2 (rows) x 2 (columns).
-template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false, int OCC = 0, int KS = 32,
-          int WD = 0, int NW = 4>
-__global__ __launch_bounds__(NW * WAVE, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_kernel(GemmParams p) {
+template <int BM, int BN, int NS, int EPI, int PREC, int OCC = 0, int KS = 32, int WD = 0, int NW = 4>
+__global__ __launch_bounds__(NW * WAVE, OCC ? OCC : 1) void gemm_kernel(GemmParams p) {
   constexpr bool SPLIT = PREC == GEMM_SPLIT2;
   constexpr bool DUAL = EPI == GEMM_SWIGLU;
   static_assert(KS == 32 || KS == 64, "K per stage");
-  static_assert(!PIPE || KS == 32, "fragment pipelining uses 32-deep stages");
   constexpr int ROWB = KS * 2;                 // bytes per LDS row
   constexpr int CPR = ROWB / 16;               // 16-byte chunks per row
   constexpr int RPI = 1024 / ROWB;             // rows per 1 KiB load instruction
@@ -133,7 +130,6 @@ __global__ __launch_bounds__(NW * WAVE, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_ke
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wavefront tile");
   static_assert(!DUAL || NT % 2 == 0, "SwiGLU tiles pair gate and up sub-tiles");
   constexpr int STAGE = ROWS * ROWB;           // bytes
-  static_assert(!WD || !PIPE, "deep W ring without fragment pipelining");
   constexpr int NSW = NS + WD;                 // W ring depth
   constexpr int A_BYTES = A_ROWS * ROWB, W_BYTES = BN * ROWB;
   constexpr int GA = A_ROWS / RPI, GW = BN / RPI;
@@ -274,66 +270,6 @@ __global__ __launch_bounds__(NW * WAVE, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_ke
 #pragma unroll
   for (int t = 0; t < NS - 1; t++)
     if (t < nk) issue(t);
-  if constexpr (PIPE) {
-    // Fragments of K step kt+1 are read from LDS while the MFMAs of step kt
-    // run (two register sets, alternating without copies). At step kt:
-    // wait for stage kt+1, barrier (every wave has read stage kt-1's
-    // fragments, so its buffer is free), issue stage kt+NS-1, read step
-    // kt+1's fragments, multiply step kt.
-    static_assert(NS >= 3, "fragment pipelining needs three stages");
-    struct Frags {
-      bf16x8 b[NT];
-      bf16x8 ahi[MT];
-      bf16x8 alo[SPLIT ? MT : 1];
-    };
-    auto read_frags = [&](int kt, Frags& F) {
-      const unsigned char* st = smem + (kt % NS) * STAGE;
-#pragma unroll
-      for (int j = 0; j < NT; j++) F.b[j] = frag(st + A_ROWS * ROWB, b_tile_row(j) + fr);
-#pragma unroll
-      for (int i = 0; i < MT; i++) {
-        const int r = wm * WM + i * 16 + fr;
-        F.ahi[i] = frag(st, r);
-        if (SPLIT) F.alo[i] = frag(st + BM * ROWB, r);
-      }
-    };
-    auto mma = [&](const Frags& F) {
-#pragma unroll
-      for (int i = 0; i < MT; i++) {
-#pragma unroll
-        for (int j = 0; j < NT; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(F.ahi[i], F.b[j], acc[i][j], 0, 0, 0);
-        if (SPLIT) {
-#pragma unroll
-          for (int j = 0; j < NT; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(F.alo[i], F.b[j], acc[i][j], 0, 0, 0);
-        }
-      }
-    };
-    auto step = [&](int kt, const Frags& cur, Frags& nxt) {
-      if (kt + 1 < nk) {
-        // stages issued so far: 0 .. min(kt + NS - 2, nk - 1); keep those
-        // after kt + 1 in flight
-        const int ahead = min(kt + NS - 2, nk - 1) - (kt + 1);
-        wait_vmcnt(ahead * PER_WAVE);
-        __builtin_amdgcn_s_barrier();
-        if (kt + NS - 1 < nk) issue(kt + NS - 1);
-        read_frags(kt + 1, nxt);
-      }
-      mma(cur);
-    };
-    Frags f0, f1;
-    if (nk > 0) {
-      wait_vmcnt(min(NS - 2, nk - 1) * PER_WAVE);
-      __builtin_amdgcn_s_barrier();
-      read_frags(0, f0);
-    }
-    for (int kt = 0; kt < nk; kt += 2) {
-      step(kt, f0, f1);
-      if (kt + 1 >= nk) break;
-      step(kt + 1, f1, f0);
-    }
-  } else
   for (int kt = 0; kt < nk; kt++) {
     const int ahead = min(NS - 2, nk - 1 - kt);  // stages still allowed in flight
     wait_vmcnt(ahead * PER_WAVE);
@@ -385,8 +321,286 @@ __global__ __launch_bounds__(NW * WAVE, OCC ? OCC : (PIPE ? 2 : 1)) void gemm_ke
   }
 }
 
-template <int BM, int BN, int NS, int EPI, int PREC, bool PIPE = false, int OCC = 0, int KS = 32,
-          int WD = 0, int NW = 4>
+// ------------------------------------------------- pipelined form --
+// Same operands, epilogues, tile order and split-K as gemm_kernel; the
+// main loop is rebuilt around v_mfma_f32_32x32x16_bf16 for the large
+// prefill shapes (measured faster there than the 16x16x32 tiles):
+// * stages of KS (32 or 64) K values, rows of 2 KS bytes in LDS, filled by
+//   the global-to-LDS DMA into NS buffers, one barrier per stage (the
+//   dispatched shape: 256 x 256, 32-deep, 3 stages = 144 KiB, eight
+//   wavefronts of 64 x 128);
+// * a stage is KS / 16 sub-steps; the fragments of sub-step u + 1 are read
+//   from LDS (double-buffered registers) between the MFMAs of sub-step u,
+//   and a stage's refill DMA between those of its last sub-step;
+// * at the last sub-step of stage t every wavefront has its reads of stage
+//   t back, so after the barrier the DMA of stage t + NS reuses stage t's
+//   buffer: NS - 1 stages in flight.
+// Fragments (32x32x16): lane l reads row l % 32, 16-byte chunk
+// 2 s + l / 32 of its stage row (s = sub-step). Chunk c of row r is stored
+// at chunk c ^ swz(r): within each 16-lane LDS phase of a 128-bit read
+// (lane quads of one bit parity per half wavefront), the rows that share
+// banks land on distinct chunks (no bank conflicts counted on the GPU).
+// Output of a 32x32 tile: lane l, element e holds
+// C[8 (e / 4) + 4 (l / 32) + e % 4][l % 32].
+template <int KS>
+__device__ __forceinline__ int swz3(int r) {
+  return KS == 32 ? (r >> 2) & 3 : (r >> 1) & 7;
+}
+
+template <int BM, int BN, int NS, int EPI, int PREC, int NW, int KS, int OCC>
+__global__ __launch_bounds__(NW * WAVE, OCC) void gemm3_kernel(GemmParams p) {
+  constexpr bool SPLIT = PREC == GEMM_SPLIT2;
+  constexpr bool DUAL = EPI == GEMM_SWIGLU;
+  constexpr int ROWB = 2 * KS, CPR = ROWB / 16, RPI = 1024 / ROWB;  // row bytes, chunks, rows per KiB
+  constexpr int SUB = KS / 16;                 // MFMA sub-steps per stage
+  constexpr int WGM = NW / 2;                  // wavefront rows x 2 columns
+  constexpr int WM = BM / WGM, WN = BN / 2;
+  constexpr int MT = WM / 32, NT = WN / 32;    // 32x32 tiles per wavefront
+  constexpr int A_ROWS = BM * (SPLIT ? 2 : 1);
+  constexpr int ROWS = A_ROWS + BN;
+  constexpr int STAGE = ROWS * ROWB;
+  constexpr int GROUPS = ROWS / RPI;           // 1 KiB DMA instructions per stage
+  constexpr int PER_WAVE = GROUPS / NW;
+  constexpr int NMFMA = MT * NT * (SPLIT ? 2 : 1);  // per sub-step
+  constexpr int NREAD = MT * (SPLIT ? 2 : 1) + NT;  // fragment reads per sub-step
+  static_assert(KS == 32 || KS == 64, "stage depth");
+  static_assert(GROUPS % NW == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+  static_assert(!DUAL || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
+  static_assert(NMFMA > NREAD, "interleave needs an MFMA per fragment read, and one for the refill");
+
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  // the wavefront index is uniform: in an SGPR, the DMA's LDS addresses are
+  // scalar arithmetic (no readfirstlane per load)
+  const int tid = threadIdx.x, lane = tid % WAVE, wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+  const int wm = wave / 2, wn = wave % 2;
+  const int cols = DUAL ? BN / 2 : BN;
+  const int mtiles = (p.M + BM - 1) / BM, ntiles = (p.N + cols - 1) / cols;
+  int m_tile, n_tile;
+  tile_of(mtiles, ntiles, m_tile, n_tile);
+  const int m0 = m_tile * BM, n0 = n_tile * cols;
+  const int M = p.M, N = p.N, K = p.K;
+  const int ksplit = gridDim.z, kper = ((K + KS - 1) / KS + ksplit - 1) / ksplit * KS;
+  const int kbeg = blockIdx.z * kper, kend = min(K, kbeg + kper);
+  const int nk = kend > kbeg ? (kend - kbeg) / KS : 0;
+  if (nk == 0) {  // an empty K range of a split-K launch: its partial sums are zero
+    if (EPI == GEMM_PARTIAL)
+      for (int x = tid; x < BM * cols; x += NW * WAVE) {
+        const int m = m0 + x / cols, n = n0 + x % cols;
+        if (m < M && n < N) p.c[((size_t)blockIdx.z * M + m) * p.ldc + n] = 0.0f;
+      }
+    return;
+  }
+
+  // DMA sources of this lane for its PER_WAVE load groups
+  const uint16_t* src[PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; i++) {
+    const int g = wave * PER_WAVE + i;
+    const int row = g * RPI + lane / CPR;
+    const int c = (lane % CPR) ^ swz3<KS>(row);
+    if (row < A_ROWS) {
+      const int m = min(m0 + row % BM, M - 1);  // rows past M load row M-1, never stored
+      const uint16_t* base = (SPLIT && row >= BM) ? p.a_lo : p.a_hi;
+      src[i] = base + (size_t)m * p.lda + c * 8;
+    } else {
+      const int r = row - A_ROWS;
+      const int nn = min(DUAL ? n0 + (r % (BN / 2)) : n0 + r, N - 1);
+      const uint16_t* base = (DUAL && r >= BN / 2) ? p.w2 : p.w;
+      src[i] = base + (size_t)nn * K + c * 8;
+    }
+  }
+  // DMA of stage t into buffer t % NS. Stages past the K range are issued
+  // all the same (re-reading the first stage, into a buffer no later read
+  // uses), so that every wait counts a constant number of newer loads.
+  auto issue = [&](int t) {
+    unsigned char* st = smem + (t % NS) * STAGE;
+    const int k0 = kbeg + (t < nk ? t : 0) * KS;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; i++)
+      __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
+                                       (lds_ptr)(st + (wave * PER_WAVE + i) * 1024), 16, 0, 0);
+  };
+  // fragment rows of this wavefront
+  const int fr = lane % 32, fh = lane / 32;
+  auto b_row = [&](int j) -> int {
+    if (!DUAL) return wn * WN + j * 32;
+    return (j < NT / 2 ? 0 : BN / 2) + wn * (WN / 2) + (j % (NT / 2)) * 32;
+  };
+  struct Frags {
+    bf16x8 a[MT], al[SPLIT ? MT : 1], b[NT];
+  };
+  auto rd = [&](const unsigned char* st, int r, int sub) -> bf16x8 {
+    const int c = 2 * sub + fh;
+    return *(const bf16x8*)(st + r * ROWB + ((c ^ swz3<KS>(r)) << 4));
+  };
+  auto read_frags = [&](int u, Frags& F) {  // sub-step u = SUB t + sub
+    const unsigned char* st = smem + ((u / SUB) % NS) * STAGE;
+    const int sub = u % SUB;
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+      const int r = wm * WM + i * 32 + fr;
+      F.a[i] = rd(st, r, sub);
+      if (SPLIT) F.al[i] = rd(st, BM + r, sub);
+    }
+#pragma unroll
+    for (int j = 0; j < NT; j++) F.b[j] = rd(st, A_ROWS + b_row(j) + fr, sub);
+  };
+
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+  // hi products of every tile, then the lo products: MT x NT independent
+  // MFMAs separate the two that update one accumulator
+  auto mfmas = [&](const Frags& F) {
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int j = 0; j < NT; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
+    if (SPLIT) {
+#pragma unroll
+      for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.al[i], F.b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // prologue: stages 0 .. NS-1 in flight, stage 0 landed, its first fragments
+  Frags F0, F1;
+#pragma unroll
+  for (int t = 0; t < NS; t++) issue(t);
+  wait_vmcnt((NS - 1) * PER_WAVE);
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, F0);
+  // A sub-step within a stage: the MFMAs of u from `cur`, the fragments of
+  // u + 1 (same stage) into `nxt`, one read per MFMA.
+  // The fragment reads go out with the first MFMAs of a sub-step, so that
+  // the rest of its MFMAs cover their latency; sched_barrier keeps every
+  // MFMA of a sub-step on its side of the stage barrier.
+  auto inner_step = [&](int u, Frags& cur, Frags& nxt) {
+    read_frags(u + 1, nxt);
+    mfmas(cur);
+#pragma unroll
+    for (int i = 0; i < NREAD; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA - NREAD, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // The last sub-step of stage t: stage t + 1 landed (t + 2 .. may stay in
+  // flight), every wavefront has its reads of stage t back: refill stage t's
+  // buffer. The fragments of stage t + 1 go out first (the next sub-step
+  // waits for them), the refill DMA after them, PER_MFMA per MFMA.
+  auto last_step = [&](int u, Frags& cur, Frags& nxt) {
+    const int t = u / SUB;
+    wait_vmcnt((NS - 2) * PER_WAVE);
+    __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(u + 1, nxt);
+    issue(t + NS);
+    mfmas(cur);
+#pragma unroll
+    for (int i = 0; i < NREAD; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    constexpr int DMA_MFMAS = NMFMA - NREAD;  // MFMAs that carry the refill
+    constexpr int PER = (PER_WAVE + DMA_MFMAS - 1) / DMA_MFMAS;
+#pragma unroll
+    for (int i = 0; i < (PER_WAVE + PER - 1) / PER; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // DMA
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, DMA_MFMAS - (PER_WAVE + PER - 1) / PER, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // every stage but the last: SUB sub-steps (fragment registers alternate,
+  // SUB is even), the last one refills
+  for (int t = 0; t + 1 < nk; t++) {
+#pragma unroll
+    for (int s = 0; s < SUB; s += 2) {
+      inner_step(SUB * t + s, F0, F1);
+      if (s + 2 < SUB) inner_step(SUB * t + s + 1, F1, F0);
+      else last_step(SUB * t + s + 1, F1, F0);
+    }
+  }
+  {  // the last stage: no refill, and its final sub-step reads nothing
+    const int u = SUB * (nk - 1);
+#pragma unroll
+    for (int s = 0; s + 2 < SUB; s += 2) {
+      inner_step(u + s, F0, F1);
+      inner_step(u + s + 1, F1, F0);
+    }
+    inner_step(u + SUB - 2, F0, F1);
+    mfmas(F1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no DMA left in flight into this block's LDS
+
+  // Epilogue
+  const int P = (EPI == GEMM_QKV) ? *p.pos : 0;
+  const int ecol = lane % 32, erow = (lane / 32) * 4;
+  const bool out_split = p.c_lo != nullptr;
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+#pragma unroll
+    for (int j = 0; j < (DUAL ? NT / 2 : NT); j++) {
+      const int n = DUAL ? n0 + wn * (WN / 2) + j * 32 + ecol : n0 + wn * WN + j * 32 + ecol;
+      if (n >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int m = m0 + wm * WM + i * 32 + 8 * (e / 4) + erow + (e % 4);
+        if (m >= M) continue;
+        const float v = acc[i][j][e];
+        if (EPI == GEMM_STORE) {
+          p.c[(size_t)m * p.ldc + n] = v;
+        } else if (EPI == GEMM_RESIDUAL) {
+          p.c[(size_t)m * p.ldc + n] += v;
+        } else if (EPI == GEMM_PARTIAL) {
+          p.c[((size_t)blockIdx.z * M + m) * p.ldc + n] = v;
+        } else if (EPI == GEMM_SWIGLU) {
+          store_split(p.c_hi, p.c_lo, (size_t)m * p.ldc + n, silu_mul(v, acc[i][j + NT / 2][e]),
+                      out_split);
+        } else {  // GEMM_QKV
+          if (n < p.q_dim) {
+            p.q[(size_t)m * p.q_dim + n] = v;
+          } else {
+            const int kv = n - p.q_dim;
+            float* cache = kv < p.kv_dim ? p.kcache : p.vcache;
+            const int j2 = kv < p.kv_dim ? kv : kv - p.kv_dim;
+            const int head = j2 / p.head_dim, h = j2 % p.head_dim;
+            cache[((size_t)head * p.ctx + P + m) * p.head_dim + h] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int NS, int EPI, int PREC, int NW, int KS, int OCC = 1>
+void launch3(const GemmParams& p, int splits, hipStream_t s) {
+  const int cols = EPI == GEMM_SWIGLU ? BN / 2 : BN;
+  const int tiles = ((p.N + cols - 1) / cols) * ((p.M + BM - 1) / BM);
+  constexpr size_t shm = (size_t)NS * (BM * (PREC == GEMM_SPLIT2 ? 2 : 1) + BN) * 2 * KS;
+  static_assert(shm <= 160 * 1024, "GEMM stages exceed LDS");
+  static bool attr = false;
+  if (!attr) {
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemm3_kernel<BM, BN, NS, EPI, PREC, NW, KS, OCC>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
+    attr = true;
+  }
+  hipLaunchKernelGGL((gemm3_kernel<BM, BN, NS, EPI, PREC, NW, KS, OCC>), dim3(tiles, 1, splits),
+                     dim3(NW * WAVE), shm, s, p);
+}
+
+template <int BM, int BN, int NS, int EPI, int PREC, int OCC = 0, int KS = 32, int WD = 0, int NW = 4>
 void launch(const GemmParams& p, int splits, hipStream_t s) {
   const int cols = EPI == GEMM_SWIGLU ? BN / 2 : BN;
   const int tiles = ((p.N + cols - 1) / cols) * ((p.M + BM - 1) / BM);
@@ -395,36 +609,43 @@ void launch(const GemmParams& p, int splits, hipStream_t s) {
   static_assert(shm <= 160 * 1024, "GEMM stages exceed LDS");
   static bool attr = false;
   if (!attr) {
-    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD, NW>,
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemm_kernel<BM, BN, NS, EPI, PREC, OCC, KS, WD, NW>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
     attr = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC, PIPE, OCC, KS, WD, NW>), dim3(tiles, 1, splits),
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, NS, EPI, PREC, OCC, KS, WD, NW>), dim3(tiles, 1, splits),
                      dim3(NW * WAVE), shm, s, p);
 }
 
-// Tile shape forced by STRASGPT_GEMM_TILE ("128x256", "128x128",
+// Tile shape forced by STRASGPT_GEMM_TILE ("256x256", "128x256", "128x128",
 // "64x128x64", "64x128x64s4", "64x128", "64x64"), for tests that run every
 // shape on small models; 0 = by size.
 int forced_tile() {
   const char* v = getenv("STRASGPT_GEMM_TILE");
   if (!v || !*v) return 0;
+  if (!strcmp(v, "256x256")) return 7;
   if (!strcmp(v, "128x256")) return 4;
   if (!strcmp(v, "128x128")) return 3;
   if (!strcmp(v, "64x128x64")) return 5;
   if (!strcmp(v, "64x128x64s4")) return 6;
   if (!strcmp(v, "64x128")) return 2;
   if (!strcmp(v, "64x64")) return 1;
-  ST_DIE("STRASGPT_GEMM_TILE must be 128x256, 128x128, 64x128x64, 64x128x64s4, 64x128 or 64x64");
+  ST_DIE("STRASGPT_GEMM_TILE must be 256x256, 128x256, 128x128, 64x128x64, 64x128x64s4, 64x128 or 64x64");
 }
 
 template <int EPI, int PREC>
 void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
   // Measured on MI355X, bf16x2, with the weights coming from HBM (caches
   // evicted before each launch, as in a prefill pass):
-  // * from about 4 blocks of 128 x 256 per CU (M >= 2048 prefill shapes),
-  //   128 x 256 with 32-deep stages and two blocks per CU reaches ~50% of
-  //   the MFMA rate (fewest stage bytes per MFMA);
+  // * from 192 tiles of 256 x 256 (3/4 of the CUs; M >= 2048 on the
+  //   d = 5120 projections, M >= 512 on the wide FFN ones), the 32x32x16
+  //   kernel with eight wavefronts (two per SIMD) is 5-25% faster than the
+  //   16x16x32 tiles (Mistral-Small-24B shapes at M = 2048: gate/up 23.4%
+  //   of the bf16 peak in algorithmic flops, QKV 21.2%); with fewer tiles,
+  //   or a last round of blocks that leaves more than a quarter of the CUs
+  //   idle (320 blocks = 1.25 rounds), part of the chip idles and it loses;
+  // * from about 4 blocks of 128 x 256 per CU, 128 x 256 with 32-deep
+  //   stages and two blocks per CU (fewest stage bytes per MFMA);
   // * below that, 64 x 128 tiles with 64-deep stages: 128-byte row segments
   //   per DMA lane group move ~1.8x the bytes per cycle of 64-byte ones.
   //   With more than one block per CU: two blocks per CU, a 2-stage A ring
@@ -437,18 +658,22 @@ void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
   const long big = (long)((p.N + cols - 1) / cols) * ((p.M + 127) / 128) * splits;
   const long wide = (long)((p.N + 2 * cols - 1) / (2 * cols)) * ((p.M + 127) / 128) * splits;
   const long small = (long)((p.N + cols - 1) / cols) * ((p.M + 63) / 64) * splits;
+  const long huge = (long)((p.N + 2 * cols - 1) / (2 * cols)) * ((p.M + 255) / 256) * splits;
   int shape = forced_tile();
   if ((shape == 5 || shape == 6) && p.K % 64) shape = 2;
   if (!shape) {
-    if (wide >= 1024) shape = 4;
+    const long rounds = (huge + 255) / 256;  // rounds of one 256 x 256 block per CU
+    if (huge >= 192 && 4 * huge >= 3 * 256 * rounds) shape = 7;
+    else if (wide >= 1024) shape = 4;
     else if (p.K % 64 == 0 && small > 256) shape = 5;
     else if (p.K % 64 == 0 && small >= 64) shape = 6;
     else shape = big >= 512 ? 3 : big >= 192 ? 2 : 1;
   }
   switch (shape) {
-    case 4: launch<128, 256, 2, EPI, PREC, false, 2>(p, splits, s); break;
-    case 5: launch<64, 128, 2, EPI, PREC, false, 2, 64, 1>(p, splits, s); break;
-    case 6: launch<64, 128, 4, EPI, PREC, false, 1, 64>(p, splits, s); break;
+    case 7: launch3<256, 256, 3, EPI, PREC, 8, 32, 2>(p, splits, s); break;
+    case 4: launch<128, 256, 2, EPI, PREC, 2>(p, splits, s); break;
+    case 5: launch<64, 128, 2, EPI, PREC, 2, 64, 1>(p, splits, s); break;
+    case 6: launch<64, 128, 4, EPI, PREC, 1, 64>(p, splits, s); break;
     case 3: launch<128, 128, 2, EPI, PREC>(p, splits, s); break;
     case 2: launch<64, 128, 4, EPI, PREC>(p, splits, s); break;
     default: launch<64, 64, 4, EPI, PREC>(p, splits, s); break;
@@ -499,73 +724,6 @@ void gemm(const GemmParams& p, int epi, int prec, int splits, hipStream_t s) {
   if (prec == GEMM_SPLIT2) dispatch<GEMM_SPLIT2>(p, epi, splits, s);
   else if (prec == GEMM_BF16) dispatch<GEMM_BF16>(p, epi, splits, s);
   else ST_DIE("unknown GEMM precision");
-  HIP_CHECK(hipGetLastError());
-}
-
-int gemm_variant_count() { return 30; }
-
-void gemm_variant(const GemmParams& p, int prec, int v, hipStream_t s) {
-  check(p, GEMM_STORE, prec, 1);
-#define GP(BM, BN, NS)                                                                \
-  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, true>(p, 1, s); \
-  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, true>(p, 1, s);                      \
-  break;
-#define GO(BM, BN, NS, PIPE, OCC)                                                          \
-  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, PIPE, OCC>(p, 1, s); \
-  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, PIPE, OCC>(p, 1, s);                      \
-  break;
-#define GK(BM, BN, NS, OCC)                                                                \
-  if (p.K % 64) ST_DIE("64-deep GEMM stages need K to be a multiple of 64");               \
-  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, false, OCC, 64>(p, 1, s); \
-  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, false, OCC, 64>(p, 1, s);                      \
-  break;
-#define GW(BM, BN, NS, OCC, KS)                                                                \
-  if (p.K % KS) ST_DIE("GEMM stages need K to be a multiple of the stage depth");                \
-  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2, false, OCC, KS, 1>(p, 1, s); \
-  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16, false, OCC, KS, 1>(p, 1, s);                      \
-  break;
-#define G(BM, BN, NS)                                                        \
-  if (prec == GEMM_SPLIT2) launch<BM, BN, NS, GEMM_STORE, GEMM_SPLIT2>(p, 1, s); \
-  else launch<BM, BN, NS, GEMM_STORE, GEMM_BF16>(p, 1, s);                   \
-  break;
-  switch (v) {
-    case 0: G(128, 128, 4)
-    case 1: G(128, 128, 3)
-    case 2: G(64, 64, 4)
-    case 3: G(128, 64, 4)
-    case 4: G(64, 128, 4)
-    case 5: G(128, 128, 2)
-    case 6: G(128, 256, 2)
-    case 7: G(128, 256, 3)
-    case 8: G(64, 256, 3)
-    case 9: GP(128, 128, 3)
-    case 10: GP(128, 128, 4)
-    case 11: GP(64, 128, 4)
-    case 12: GP(128, 256, 3)
-    case 13: GP(64, 128, 3)
-    case 14: GO(128, 256, 2, false, 2)
-    case 15: GO(128, 128, 2, false, 3)
-    case 16: GO(128, 256, 3, true, 1)
-    case 17: GO(128, 128, 3, false, 2)
-    case 18: GO(256, 128, 2, false, 2)
-    case 19: GO(128, 256, 4, true, 1)
-    case 20: GK(128, 128, 3, 1)
-    case 21: GK(128, 128, 2, 1)
-    case 22: GK(128, 256, 2, 1)
-    case 23: GK(64, 128, 4, 1)
-    case 24: GK(64, 128, 2, 2)
-    case 25: GK(256, 128, 2, 1)
-    case 26: GW(64, 128, 2, 2, 64)
-    case 27: GW(64, 128, 3, 1, 64)
-    case 28: GW(128, 128, 2, 1, 64)
-    case 29: GW(64, 128, 3, 2, 32)
-    default: ST_DIE("unknown GEMM variant");
-  }
-#undef G
-#undef GP
-#undef GO
-#undef GK
-#undef GW
   HIP_CHECK(hipGetLastError());
 }
 
