@@ -179,6 +179,9 @@ def main():
     ap.add_argument("--probe-traffic", action="store_true",
                     help="only launch the kernels an HBM-counter run needs (a 256 MiB copy, "
                          "then a 16-token prefill and 4 eager decode steps); prints nothing")
+    ap.add_argument("--probe-prefill", action="store_true",
+                    help="only run two prefills of the workload's prompt (for MFMA counter "
+                         "runs of the prefill GEMMs); prints nothing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU runs are "
@@ -198,6 +201,12 @@ def main():
 
     if args.probe_traffic:
         probe_traffic(t, prompt)
+        return
+    if args.probe_prefill:
+        for i in range(2):  # the first one also warms the clocks up
+            t.reset()
+            t.predict(prompt)
+            log(f"probe prefill {i + 1}/2 done")
         return
 
     for i in range(args.warmup):

@@ -708,6 +708,18 @@ void check(const GemmParams& p, int epi, int prec, int splits) {
 }  // namespace
 
 int gemm_splits(int M, int N, int K) {
+  // Long reductions (K >= 16384) over many rows: the fewest splits that give
+  // the 256 x 256 kernel whole rounds of blocks (at least 3/4 of the last
+  // one used). Its tiles re-read the activations a quarter as often as
+  // 64 x 128 ones: on the Mistral-Small-24B down projection (M = 2048,
+  // K = 32768) the 64 x 128 tiles moved 12x the algorithmic HBM bytes.
+  if (K >= 16384) {
+    const long t256 = (long)((N + 255) / 256) * ((M + 255) / 256);
+    for (int s = 1; s <= 8 && K / (BK * s) >= 4; s++) {
+      const long blocks = t256 * s, rounds = (blocks + 255) / 256;
+      if (blocks >= 192 && 4 * blocks >= 3 * 256 * rounds) return s;
+    }
+  }
   // Enough blocks for the 256 CUs on the N = embedding_dim projections;
   // long reductions (K >= 16384: a 1024-step K loop and more) split until
   // there are about four 128 x 128 tiles per CU.

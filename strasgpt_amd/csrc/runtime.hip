@@ -1100,8 +1100,10 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->att_lo = dalloc<uint16_t>(T * D->qd);
   D->act_hi = dalloc<uint16_t>(T * H);
   D->act_lo = dalloc<uint16_t>(T * H);
+  // split-K workspace: up to 8 splits of a 512-row chunk, 4 of a full chunk
+  // (long reductions such as a 32768-wide down projection split 3 ways)
   D->ws_splits = 8;
-  D->ws_rows = TRANSFORMER_CHUNK_MAX_LEN;  // split-K only pays on short chunks
+  D->ws_rows = std::max<size_t>(TRANSFORMER_CHUNK_MAX_LEN, T / 2);
   D->ws = dalloc<float>((size_t)D->ws_splits * D->ws_rows * d);
   const size_t cache = (size_t)D->L * D->kvh * D->ctx * hd;
   D->kc = dalloc<float>(cache);
