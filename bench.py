@@ -176,6 +176,8 @@ def main():
     ap.add_argument("--cpu-decode-tokens", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--precision", type=int, default=0, help="prefill GEMM: 0 bf16x2, 1 bf16")
+    ap.add_argument("--kv-cache", choices=["fp32", "bf16"], default="fp32",
+                    help="KV-cache storage format (fp32: the reference's)")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="only launch the kernels an HBM-counter run needs (a 256 MiB copy, "
                          "then a 16-token prefill and 4 eager decode steps); prints nothing")
@@ -197,6 +199,7 @@ def main():
     t0 = time.time()
     t = runtime.Transformer(d)
     t.set_prefill_precision(args.precision)
+    t.set_kv_cache_format(runtime.KV_BF16 if args.kv_cache == "bf16" else runtime.KV_FP32)
     log(f"loaded into HBM in {time.time() - t0:.1f}s; {runtime.version()}")
 
     if args.probe_traffic:
@@ -293,7 +296,7 @@ def main():
         "config": {"workload": f"{shp.name}-shaped decoder: {shp.prompt_len}-token prefill + "
                                f"{shp.decode_len} greedy decode tokens, batch 1",
                    "global_batch": 1, "seq_len": shp.prompt_len + shp.decode_len,
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU", "kv_cache": args.kv_cache},
         "prefill_tok_s": round(prefill_tok_s, 1),
         "decode_ms_per_token": round(decode_s / decode_n * 1e3, 4),
         "decode_effective_gbs": round(decode_bytes / ntok / (decode_s / decode_n) / 1e9, 1),

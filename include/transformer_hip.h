@@ -81,6 +81,25 @@ enum transformer_decode_mode {
 };
 int transformer_set_decode_mode(transformer_t* transformer, int mode);
 
+/* KV-cache storage format (no reference counterpart: the reference cache
+ * is fp32, include/transformer.h:76-77, written at
+ * source/transformer.c:1271-1291). TRANSFORMER_KV_BF16 stores every key
+ * (after its norm and RoPE) and value rounded to the nearest bf16, in the
+ * same [layer][kv_head][position][head_dim] layout: half the cache memory
+ * and half the bytes decode attention reads. Attention reads the stored
+ * values exactly, so results differ from the fp32 cache by that rounding
+ * only. The initial format is fp32, or bf16 when the environment variable
+ * STRASGPT_KV_CACHE=bf16 is set at load time. The format can change only
+ * while the cache is empty (before the first token or right after
+ * transformer_reset); it dies otherwise. Returns the previous format. The
+ * fp32 prefill attention kernel (STRASGPT_PREFILL_ATTN=fp32) needs the fp32
+ * cache. */
+enum transformer_kv_format {
+  TRANSFORMER_KV_FP32 = 0,
+  TRANSFORMER_KV_BF16 = 1
+};
+int transformer_set_kv_cache_format(transformer_t* transformer, int format);
+
 /* Measurement hooks (no reference counterpart; the reference only times
  * whole predict calls, source/strasgpt.c:206-274). While enabled, every
  * kernel launch of the forward pass is bracketed by HIP events on the

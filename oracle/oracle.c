@@ -25,6 +25,7 @@ struct oracle_model {
   /* KV cache [L][kvh][ctx][hd] and RoPE table [ctx][hd] */
   float *kc, *vc, *rope;
   size_t cached;
+  int kv_format; /* ORACLE_KV_*: rounding of the values written to kc, vc */
   float *cap, *cap_final;
 };
 
@@ -41,6 +42,46 @@ static inline float bf16f(uint16_t w) {
 }
 
 float oracle_bf16_to_f32(uint16_t w) { return bf16f(w); }
+
+/* Round to the nearest bf16 value, ties to even (the top 16 bits of the
+ * fp32 pattern after adding half an ulp of the kept part, plus one when the
+ * kept part is odd); infinities stay, NaNs stay NaN. No reference
+ * counterpart: the reference cache is fp32. */
+float oracle_round_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    u |= 0x00400000u; /* quiet NaN */
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+  }
+  u &= 0xffff0000u;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/* Round to the nearest OCP FP8 E4M3 value (bias 7, largest 448, subnormal
+ * spacing 2^-9), ties to even, magnitudes past 448 saturating to 448; NaN
+ * stays NaN. The spacing of the binade of |x| is a power of two, so the
+ * quotient below is exact and rintf (round to nearest even, the default
+ * mode) does the rounding. No reference counterpart. */
+float oracle_round_fp8_e4m3(float x) {
+  if (isnan(x)) return x;
+  float a = fabsf(x);
+  if (a >= 448.0f) return copysignf(448.0f, x);
+  int e;
+  frexpf(a, &e);                       /* a = f 2^e, f in [0.5, 1) */
+  int q = (a < 0.015625f ? -6 : e - 1) - 3;  /* log2 of the spacing */
+  float r = ldexpf(rintf(ldexpf(a, -q)), q);
+  if (r > 448.0f) r = 448.0f;
+  return copysignf(r, x);
+}
+
+void oracle_set_kv_format(oracle_model_t* m, int fmt) { m->kv_format = fmt; }
+
+static float round_kv(int fmt, float v) {
+  return fmt == ORACLE_KV_BF16 ? oracle_round_bf16(v) : fmt == ORACLE_KV_FP8_E4M3 ? oracle_round_fp8_e4m3(v) : v;
+}
 void oracle_bf16_to_f32_array(const uint16_t* w, size_t n, float* out) {
   for (size_t i = 0; i < n; i++) out[i] = bf16f(w[i]);
 }
@@ -535,6 +576,14 @@ static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc
         if (c->qk_norm) oracle_rmsnorm(hd, kr, kr, W(m, ORACLE_K_NORM, l), eps);
         rope_apply(hd, c->rope_interleaved, kr, m->rope + (P + t) * hd);
       }
+    }
+    /* cache storage format: the new rows as the cache holds them */
+    if (m->kv_format != ORACLE_KV_F32) {
+      for (size_t head = 0; head < kvh; head++)
+        for (size_t i = (head * ctx + P) * hd; i < (head * ctx + P + T) * hd; i++) {
+          kc[i] = round_kv(m->kv_format, kc[i]);
+          vc[i] = round_kv(m->kv_format, vc[i]);
+        }
     }
     /* Q projection, Q-norm, RoPE (source/transformer.c:1327-1373) */
     {

@@ -77,6 +77,15 @@ int oracle_predict(oracle_model_t* m, size_t token_count, const int* token,
  * stream after every layer [L][T][d] and final-norm output [T][d]. */
 void oracle_capture_hidden(oracle_model_t* m, float* out, float* out_final);
 
+/* KV-cache storage formats (no reference counterpart: the reference cache
+ * is fp32): every key and value row written to the cache (keys after their
+ * norm and RoPE) is rounded to the format, round to nearest even, and read
+ * back exactly by attention. */
+enum { ORACLE_KV_F32 = 0, ORACLE_KV_BF16 = 1, ORACLE_KV_FP8_E4M3 = 2 };
+void oracle_set_kv_format(oracle_model_t* m, int fmt);
+float oracle_round_bf16(float x);
+float oracle_round_fp8_e4m3(float x);
+
 /* Reference sample_argmax (source/sampler.c:92-102). */
 size_t oracle_argmax(const float* x, size_t n);
 

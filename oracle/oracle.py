@@ -114,6 +114,11 @@ def load_lib():
     lib.oracle_rope_table.argtypes = [sz, sz, ctypes.c_float, ctypes.c_int, fp]
     lib.oracle_attention_row.argtypes = [sz, sz, fp, fp, fp, fp]
     lib.oracle_topk_softmax.argtypes = [sz, fp, sz, ip, fp]
+    lib.oracle_set_kv_format.argtypes = [P, ctypes.c_int]
+    lib.oracle_round_bf16.argtypes = [ctypes.c_float]
+    lib.oracle_round_bf16.restype = ctypes.c_float
+    lib.oracle_round_fp8_e4m3.argtypes = [ctypes.c_float]
+    lib.oracle_round_fp8_e4m3.restype = ctypes.c_float
     _LIB = lib
     return lib
 
@@ -163,10 +168,14 @@ def classify(name: str):
     return None, None
 
 
+# KV-cache storage formats (oracle.h ORACLE_KV_*)
+KV_F32, KV_BF16, KV_FP8_E4M3 = 0, 1, 2
+
+
 class OracleModel:
     """The reference forward pass on the CPU, loaded from a model directory."""
 
-    def __init__(self, model_dir: str, threads: Optional[int] = None):
+    def __init__(self, model_dir: str, threads: Optional[int] = None, kv_format: int = KV_F32):
         self.lib = load_lib()
         if threads:
             self.lib.oracle_set_threads(int(threads))
@@ -209,6 +218,7 @@ class OracleModel:
         missing = self.lib.oracle_finalize(self.handle)
         if missing:
             raise ValueError(f"oracle: {missing} tensors missing")
+        self.lib.oracle_set_kv_format(self.handle, int(kv_format))
 
     def close(self):
         if self.handle:

@@ -87,6 +87,10 @@ int transformer_set_decode_mode(transformer_t* transformer, int mode) {
   return transformer ? sg_set_decode_mode(transformer, mode) : -1;
 }
 
+int transformer_set_kv_cache_format(transformer_t* transformer, int format) {
+  return transformer ? sg_set_kv_cache_format(transformer, format) : -1;
+}
+
 void transformer_profile(transformer_t* transformer, int enable) {
   if (transformer) sg_profile(transformer, enable);
 }

@@ -31,6 +31,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// The same rounding for every value: NaNs stay NaN (quieted), infinities
+// stay (the KV-cache bf16 format).
+__device__ __forceinline__ uint16_t f32_to_bf16_any(float f) {
+  uint32_t u = __float_as_uint(f);
+  u = (u & 0x7FFFFFFFu) > 0x7F800000u ? u | 0x00400000u : u + 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
 // MXFP4 (OCP MX v1.0) E2M1 element: sign bit 3, exponent bits 2..1,
 // mantissa bit 0. Magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6 built directly as
 // fp32 bit patterns: exponent e >= 1 gives 2^(e-1) * (1 + m/2).

@@ -265,7 +265,24 @@ __device__ __forceinline__ int x3_vswz(int d) { return (0 - (d >> 2)) & 3; }
 // Cache rows [r0, r1) of one kv head (blockIdx.y) into the bf16 planes:
 // 32 rows per block. K keeps its row layout; V goes through LDS and is
 // written transposed, 64 contiguous bytes (32 keys) per dim and plane.
-template <int HD>
+// A bf16 cache (B16) holds rows that are bf16 already: their split is the
+// row itself and a zero lo plane.
+template <int HD, bool B16>
+__device__ __forceinline__ float2 cache_pair(const float* c, size_t i) {
+  if constexpr (B16) {
+    const uint32_t u = *(const uint32_t*)((const uint16_t*)c + i);
+    return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xFFFF0000u));
+  } else {
+    return *(const float2*)(c + i);
+  }
+}
+template <bool B16>
+__device__ __forceinline__ float cache_at(const float* c, size_t i) {
+  if constexpr (B16) return bf16_to_f32(((const uint16_t*)c)[i]);
+  else return c[i];
+}
+
+template <int HD, bool B16>
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* kc, const float* vc, uint16_t* khi,
                                                          uint16_t* klo, uint16_t* vthi, uint16_t* vtlo,
                                                          int ctx, int ctx_pad, int r0, int r1) {
@@ -276,7 +293,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* kc, const 
   for (int i = tid; i < 32 * HD / 2; i += 256) {
     const int r = rb + (2 * i) / HD, dd = (2 * i) % HD;
     if (r < r1) {
-      const float2 x = *(const float2*)(kc + kbase + (size_t)r * HD + dd);
+      const float2 x = cache_pair<HD, B16>(kc, kbase + (size_t)r * HD + dd);
       uint32_t hi, lo;
       split2(x.x, x.y, hi, lo);
       *(uint32_t*)(khi + kbase + (size_t)r * HD + dd) = hi;
@@ -285,7 +302,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* kc, const 
   }
   for (int i = tid; i < 32 * HD; i += 256) {
     const int r = rb + i / HD, dd = i % HD;
-    vs[i / HD][dd] = r < r1 ? vc[kbase + (size_t)r * HD + dd] : 0.0f;
+    vs[i / HD][dd] = r < r1 ? cache_at<B16>(vc, kbase + (size_t)r * HD + dd) : 0.0f;
   }
   __syncthreads();
   const size_t vbase = (size_t)h * HD * ctx_pad;
@@ -498,11 +515,15 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
 // LDS layout of the decode kernel (floats). K rows are padded to HD + 4
 // floats: the lanes of a wave read one key row each, and with the padding
 // eight consecutive rows start in eight different bank groups.
-template <int HD>
+// With a bf16 cache (B16) the tiles hold bf16 rows: K rows of HD + 8
+// elements (the same 16-byte padding), V rows of HD; sizes below stay in
+// 4-byte units.
+template <int HD, bool B16 = false>
 struct DecLds {
-  static constexpr int KROW = HD + 4;
+  static constexpr int KROW = B16 ? HD / 2 + 4 : HD + 4;  // K row stride, 4-byte units
+  static constexpr int VROW = B16 ? HD / 2 : HD;
   static constexpr int KT = kDecTile * KROW;       // K tile
-  static constexpr int VT = kDecTile * HD;         // V tile
+  static constexpr int VT = kDecTile * VROW;       // V tile
   static constexpr int qs = 0;                     // [kDecMaxG][HD] normalised, rotated queries
   static constexpr int kn = qs + kDecMaxG * HD;    // [HD] this step's processed key
   static constexpr int flag = kn + HD;             // [4]
@@ -516,24 +537,25 @@ struct DecLds {
 // K rows one instruction per row (its first HD / 4 lanes) into the padded
 // layout. No registers are held; the caller waits for vector memory
 // operations and syncs the block.
-template <int HD>
+template <int HD, bool B16 = false>
 __device__ __forceinline__ void dma_kv(const float* kb, const float* vb, int t0, int n, float* kt,
                                        float* vt) {
-  constexpr int CPR = HD / 4;  // 16-byte chunks per row
+  constexpr int RB = HD * (B16 ? 2 : 4);  // row bytes
+  constexpr int CPR = RB / 16;            // 16-byte chunks per row
   constexpr int NWAVE = kDecThreads / WAVE;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  const float* ks = kb + (size_t)t0 * HD;
-  const float* vs = vb + (size_t)t0 * HD;
+  const char* ks = (const char*)kb + (size_t)t0 * RB;
+  const char* vs = (const char*)vb + (size_t)t0 * RB;
   const int units = n * CPR;
   for (int u0 = wave * WAVE; u0 < units; u0 += kDecThreads) {
     const int u = u0 + lane;
     if (u < units)
-      __builtin_amdgcn_global_load_lds((const void*)(vs + u * 4), (lds_ptr)(vt + u0 * 4), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vs + u * 16), (lds_ptr)(vt + u0 * 4), 16, 0, 0);
   }
   for (int r = wave; r < n; r += NWAVE) {
     if (lane < CPR)
-      __builtin_amdgcn_global_load_lds((const void*)(ks + r * HD + lane * 4), (lds_ptr)(kt + r * (HD + 4)), 16,
-                                       0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(ks + r * RB + lane * 16),
+                                       (lds_ptr)(kt + r * DecLds<HD, B16>::KROW), 16, 0, 0);
   }
 }
 
@@ -542,7 +564,10 @@ __device__ __forceinline__ void dma_kv(const float* kb, const float* vb, int t0,
 // weights, fr / fi the rotation of the lane's pair (element lane*pst and
 // lane*pst + po, when lane*pst < pb). Result in LDS dst. Same arithmetic as
 // the reference (source/transformer.c:1293-1323).
-template <int HD>
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16_any(x)); }
+
+// B16: the result is rounded to bf16 (a key headed for a bf16 cache).
+template <int HD, bool B16 = false>
 __device__ __forceinline__ void norm_rope_regs(const float* xv, const float* wv, bool norm, float eps,
                                                float fr, float fi, int pb, int po, int pst, float* dst) {
 #pragma clang fp contract(off)
@@ -568,8 +593,17 @@ __device__ __forceinline__ void norm_rope_regs(const float* xv, const float* wv,
   }
   __builtin_amdgcn_wave_barrier();
   if (h < pb) {
-    dst[h] = r0;
-    dst[h + po] = r1;
+    dst[h] = B16 ? round_bf16(r0) : r0;
+    dst[h + po] = B16 ? round_bf16(r1) : r1;
+  }
+  if constexpr (B16) {  // elements outside every rotated pair, rounded too
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int e = lane + i * WAVE;
+      const bool first = e < pb && e % pst == 0, second = e >= po && e - po < pb && (e - po) % pst == 0;
+      if (e < HD && !first && !second) dst[e] = round_bf16(dst[e]);
+    }
   }
 }
 
@@ -594,10 +628,10 @@ __device__ __forceinline__ void norm_rope_regs(const float* xv, const float* wv,
 // (the value row was written by the QKV projection).
 // Two blocks fit per CU (LDS), so at most 2 waves per SIMD: the register
 // budget that lets every K read of a tile be in flight at once.
-template <int HD, int GW>
+template <int HD, int GW, bool B16>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_decode_kernel(
     AttnParams p) {
-  using L = DecLds<HD>;
+  using L = DecLds<HD, B16>;
   constexpr int NW = kDecThreads / WAVE;
   constexpr int PER = (HD + WAVE - 1) / WAVE;
   constexpr int MAXV = (kDecMaxG + 1 + NW - 1) / NW;  // head vectors per wave in the staging
@@ -620,12 +654,13 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
   const int s0 = c * len, s1 = min(total, s0 + len);
   const bool has_new = s1 == total;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-  const float* kb = p.kcache + (size_t)g * p.ctx * HD;
-  const float* vb = p.vcache + (size_t)g * p.ctx * HD;
+  // cache element offsets (a bf16 cache: 2-byte elements)
+  const float* kb = (const float*)((const char*)p.kcache + (size_t)g * p.ctx * HD * (B16 ? 2 : 4));
+  const float* vb = (const float*)((const char*)p.vcache + (size_t)g * p.ctx * HD * (B16 ? 2 : 4));
 
   // Stage 1 loads: the first K/V tile, the raw q (and new k) vectors, their
   // norm weights and the rotation of position P.
-  dma_kv<HD>(kb, vb, s0, min(kDecTile, s1 - s0), tiles, tiles + L::KT);
+  dma_kv<HD, B16>(kb, vb, s0, min(kDecTile, s1 - s0), tiles, tiles + L::KT);
   const float* cs = p.rope + (size_t)P * HD;
   const int nvec = G + (has_new ? 1 : 0);
   const int hp = lane * p.pair_stride;
@@ -652,9 +687,12 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
 #pragma unroll
   for (int j = 0; j < MAXV; j++) {
     const int v = wave + j * NW;
-    if (v < nvec)
-      norm_rope_regs<HD>(xv[j], wv[j], (v == G ? p.kn : p.qn) != nullptr, p.eps, fr[j], fi[j],
-                         p.pair_bound, p.pair_offset, p.pair_stride, v == G ? kn : qs + v * HD);
+    if (v == G)  // this step's key, rounded as the cache will hold it
+      norm_rope_regs<HD, B16>(xv[j], wv[j], p.kn != nullptr, p.eps, fr[j], fi[j], p.pair_bound,
+                              p.pair_offset, p.pair_stride, kn);
+    else if (v < nvec)
+      norm_rope_regs<HD>(xv[j], wv[j], p.qn != nullptr, p.eps, fr[j], fi[j], p.pair_bound, p.pair_offset,
+                         p.pair_stride, qs + v * HD);
   }
 
   const float scale = sqrtf((float)HD);
@@ -677,7 +715,7 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     __syncthreads();                // ... for every wave; previous tile consumed
     if (t0 + kDecTile < s1) {
       float* nk = tiles + (buf ^ 1) * (L::KT + L::VT);
-      dma_kv<HD>(kb, vb, t0 + kDecTile, min(kDecTile, s1 - t0 - kDecTile), nk, nk + L::KT);
+      dma_kv<HD, B16>(kb, vb, t0 + kDecTile, min(kDecTile, s1 - t0 - kDecTile), nk, nk + L::KT);
     }
     if (!active) continue;
     if (t0 == s0) {  // this wave's queries, the lane's half of each
@@ -697,13 +735,26 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     // scores: key t0 + kl, dims [half * HALF, (half + 1) * HALF)
     const bool valid = kl < n;
     const bool is_new = has_new && t0 + kl == P;
-    const float* krow = (is_new ? kn : kt + kl * L::KROW) + half * HALF;
     float s[GW];
 #pragma unroll
     for (int j = 0; j < GW; j++) s[j] = 0.0f;
     float4 kv[HALF / 4];  // every read of the row issued before the first product
+    if (!B16 || is_new) {
+      const float* krow = (is_new ? kn : kt + kl * L::KROW) + half * HALF;
 #pragma unroll
-    for (int i = 0; i < HALF / 4; i++) kv[i] = *(const float4*)(krow + 4 * i);
+      for (int i = 0; i < HALF / 4; i++) kv[i] = *(const float4*)(krow + 4 * i);
+    } else {
+      typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+      const u32x4v* krow = (const u32x4v*)((const uint16_t*)(kt + kl * L::KROW) + half * HALF);
+#pragma unroll
+      for (int i = 0; i < HALF / 8; i++) {
+        const u32x4v u = krow[i];
+        kv[2 * i] = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u),
+                                __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xFFFF0000u));
+        kv[2 * i + 1] = make_float4(__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xFFFF0000u),
+                                    __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xFFFF0000u));
+      }
+    }
 #pragma unroll
     for (int i = 0; i < HALF / 4; i++) {
 #pragma unroll
@@ -736,6 +787,18 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
       float v[8][DPL];
 #pragma unroll
       for (int kk = 0; kk < 8; kk++) {
+        if constexpr (B16) {
+          const uint16_t* vr = (const uint16_t*)vt + min(k0 + kk, n - 1) * HD + dd;
+          if constexpr (DPL == 2) {
+            const uint32_t u = *(const uint32_t*)vr;
+            v[kk][0] = __uint_as_float(u << 16);
+            v[kk][1] = __uint_as_float(u & 0xFFFF0000u);
+          } else {
+#pragma unroll
+            for (int d = 0; d < DPL; d++) v[kk][d] = bf16_to_f32(vr[d]);
+          }
+          continue;
+        }
         const float* vr = vt + min(k0 + kk, n - 1) * HD + dd;
         if constexpr (DPL == 2) {
           const float2 f = *(const float2*)vr;
@@ -775,8 +838,11 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     }
   }
   if (has_new) {  // cache row P of kv head g, read by later steps
-    float* kc = p.kcache_w + ((size_t)g * p.ctx + P) * HD;
-    for (int e = tid; e < HD; e += kDecThreads) kc[e] = kn[e];
+    const size_t at = ((size_t)g * p.ctx + P) * HD;
+    for (int e = tid; e < HD; e += kDecThreads) {
+      if (B16) ((uint16_t*)p.kcache_w)[at + e] = f32_to_bf16_any(kn[e]);  // exact: kn is rounded
+      else p.kcache_w[at + e] = kn[e];
+    }
   }
   // Hand-off to the combining block. Partials are written and read only by
   // agent-scope relaxed atomic accesses (sc1: written through to, and read
@@ -892,9 +958,12 @@ void attention_init() {
   X3_ATTR(128)
 #undef X3_ATTR
 #define DECODE_ATTR(HD, GW)                                                                     \
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<HD, GW>,                        \
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<HD, GW, false>,                 \
                                 hipFuncAttributeMaxDynamicSharedMemorySize,                     \
-                                (int)(DecLds<HD>::total * sizeof(float))));
+                                (int)(DecLds<HD>::total * sizeof(float))));                     \
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<HD, GW, true>,                  \
+                                hipFuncAttributeMaxDynamicSharedMemorySize,                     \
+                                (int)(DecLds<HD, true>::total * sizeof(float))));
   DECODE_ATTR(16, 1)
   DECODE_ATTR(16, 2)
   DECODE_ATTR(32, 1)
@@ -904,16 +973,6 @@ void attention_init() {
   DECODE_ATTR(128, 1)
   DECODE_ATTR(128, 2)
 #undef DECODE_ATTR
-}
-
-size_t attention_decode_lds_bytes(int hd) {
-  switch (hd) {
-    case 16: return DecLds<16>::total * sizeof(float);
-    case 32: return DecLds<32>::total * sizeof(float);
-    case 64: return DecLds<64>::total * sizeof(float);
-    case 128: return DecLds<128>::total * sizeof(float);
-    default: return 0;
-  }
 }
 
 // STRASGPT_PREFILL_ATTN=fp32 selects the fp32 matrix-core kernel; the
@@ -931,7 +990,7 @@ void attention_prefill(const AttnParams& p, hipStream_t s) {
 
 void attention_split_rows(const float* kcache, const float* vcache, uint16_t* khi, uint16_t* klo,
                           uint16_t* vthi, uint16_t* vtlo, int kv_heads, int ctx, int ctx_pad, int hd,
-                          int r0, int r1, hipStream_t s) {
+                          int r0, int r1, int kv_bf16, hipStream_t s) {
   if (r0 % 32 || r0 < 0 || r1 > ctx || ctx_pad % 32 || ctx_pad < ctx)
     ST_DIE("attention_split_rows: rows must start at a multiple of 32 and stay in the cache");
   if (r1 <= r0) return;
@@ -939,8 +998,12 @@ void attention_split_rows(const float* kcache, const float* vcache, uint16_t* kh
   switch (hd) {
 #define SPLIT_CASE(HD)                                                                                \
   case HD:                                                                                            \
-    hipLaunchKernelGGL(split_rows_kernel<HD>, grid, dim3(256), 0, s, kcache, vcache, khi, klo, vthi, \
-                       vtlo, ctx, ctx_pad, r0, r1);                                                   \
+    if (kv_bf16)                                                                                      \
+      hipLaunchKernelGGL((split_rows_kernel<HD, true>), grid, dim3(256), 0, s, kcache, vcache, khi, klo, \
+                         vthi, vtlo, ctx, ctx_pad, r0, r1);                                           \
+    else                                                                                              \
+      hipLaunchKernelGGL((split_rows_kernel<HD, false>), grid, dim3(256), 0, s, kcache, vcache, khi, klo, \
+                         vthi, vtlo, ctx, ctx_pad, r0, r1);                                           \
     break;
     SPLIT_CASE(16)
     SPLIT_CASE(32)
@@ -958,6 +1021,7 @@ void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s) 
   if (variant == 0 && (!p.khi || !p.klo || !p.vthi || !p.vtlo || p.ctx_pad % 32 || p.ctx_pad < p.ctx))
     ST_DIE("split-bf16 prefill attention needs the cache's bf16 planes");
   if (variant != 0 && variant != 1) ST_DIE("prefill attention variant is 0 (split bf16) or 1 (fp32)");
+  if (variant == 1 && p.kv_bf16) ST_DIE("the fp32 prefill attention kernel reads an fp32 KV cache only");
   dim3 grid((p.T + PQ - 1) / PQ, p.q_heads);
   const bool fp32 = variant == 1;
   switch (p.hd) {
@@ -988,19 +1052,29 @@ void attention_decode(const AttnParams& p, hipStream_t s) {
       p.pair_bound - p.pair_stride + p.pair_offset >= p.hd)
     ST_DIE("decode attention: RoPE pairs must fit one per lane within the head");
   const dim3 grid(p.splits, p.kv_heads);
-  const size_t shm = attention_decode_lds_bytes(p.hd);
   const bool two = G > kDecThreads / WAVE;  // two query heads per wave
   switch (p.hd) {
-#define DECODE_CASE(HD)                                                                        \
-  case HD:                                                                                     \
-    if (two) hipLaunchKernelGGL((attn_decode_kernel<HD, 2>), grid, dim3(kDecThreads), shm, s, p); \
-    else hipLaunchKernelGGL((attn_decode_kernel<HD, 1>), grid, dim3(kDecThreads), shm, s, p);     \
+#define DECODE_LAUNCH(HD, GW)                                                                 \
+  if (p.kv_bf16)                                                                              \
+    hipLaunchKernelGGL((attn_decode_kernel<HD, GW, true>), grid, dim3(kDecThreads),           \
+                       (DecLds<HD, true>::total * sizeof(float)), s, p);                      \
+  else                                                                                        \
+    hipLaunchKernelGGL((attn_decode_kernel<HD, GW, false>), grid, dim3(kDecThreads),          \
+                       DecLds<HD>::total * sizeof(float), s, p);
+#define DECODE_CASE(HD)     \
+  case HD:                  \
+    if (two) {              \
+      DECODE_LAUNCH(HD, 2)  \
+    } else {                \
+      DECODE_LAUNCH(HD, 1)  \
+    }                       \
     break;
     DECODE_CASE(16)
     DECODE_CASE(32)
     DECODE_CASE(64)
     DECODE_CASE(128)
 #undef DECODE_CASE
+#undef DECODE_LAUNCH
     default: ST_DIE("attention supports head_dim 16, 32, 64 or 128");
   }
   HIP_CHECK(hipGetLastError());

@@ -123,27 +123,34 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(NormParams p) {
 // One wavefront per (token, head): optional per-head RMSNorm with the
 // layer's q/k norm weight (source/transformer.c:1293-1307, 1340-1356), then
 // the pair rotation v0' = v0 cos - v1 sin, v1' = v0 sin + v1 cos with the
-// host-built table (source/transformer.c:1309-1323, 1358-1373).
+// host-built table (source/transformer.c:1309-1323, 1358-1373). With a bf16
+// cache (kstage given) a key row is read from kstage and the whole result
+// row is stored rounded into the cache.
 __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
     float* q, int q_heads, float* kcache, int ctx, int hd, const int* pos,
     const uint16_t* qn, const uint16_t* kn, float eps, const float* rope,
-    int pair_bound, int pair_offset, int pair_stride) {
+    int pair_bound, int pair_offset, int pair_stride, const float* kstage) {
 #pragma clang fp contract(off)
   __shared__ float v[512];
   const int t = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
   const int P = *pos + t;
+  const bool staged = kstage && head >= q_heads;
   float* row;
+  const float* src;
   const uint16_t* nw;
   if (head < q_heads) {
     row = q + ((size_t)t * q_heads + head) * hd;
+    src = row;
     nw = qn;
   } else {
-    row = kcache + ((size_t)(head - q_heads) * ctx + P) * hd;
+    const int kh = head - q_heads;
+    row = kcache + ((size_t)kh * ctx + P) * hd;  // a bf16 row when staged
+    src = staged ? kstage + ((size_t)t * (gridDim.y - q_heads) + kh) * hd : row;
     nw = kn;
   }
   float ss = 0.0f;
   for (int e = lane; e < hd; e += WAVE) {
-    const float x = row[e];
+    const float x = src[e];
     v[e] = x;
     ss = fmaf(x, x, ss);
   }
@@ -154,13 +161,28 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   }
   __syncthreads();
   const float* cs = rope + (size_t)P * hd;
+  if (!staged) {
+    for (int i = lane; i * pair_stride < pair_bound; i += WAVE) {
+      const int h = i * pair_stride;
+      const float fr = cs[h], fi = cs[h + pair_offset];
+      const float v0 = v[h], v1 = v[h + pair_offset];
+      row[h] = v0 * fr - v1 * fi;
+      row[h + pair_offset] = v0 * fi + v1 * fr;
+    }
+    return;
+  }
+  // staged key: rotate in LDS (each pair read and written by one lane), then
+  // store every element rounded
   for (int i = lane; i * pair_stride < pair_bound; i += WAVE) {
     const int h = i * pair_stride;
     const float fr = cs[h], fi = cs[h + pair_offset];
     const float v0 = v[h], v1 = v[h + pair_offset];
-    row[h] = v0 * fr - v1 * fi;
-    row[h + pair_offset] = v0 * fi + v1 * fr;
+    v[h] = v0 * fr - v1 * fi;
+    v[h + pair_offset] = v0 * fi + v1 * fr;
   }
+  __syncthreads();
+  uint16_t* row16 = (uint16_t*)kcache + ((size_t)(head - q_heads) * ctx + P) * hd;
+  for (int e = lane; e < hd; e += WAVE) row16[e] = f32_to_bf16_any(v[e]);
 }
 
 // ------------------------------------------------------------- argmax --
@@ -274,13 +296,13 @@ void residual_norm(const NormParams& p, hipStream_t s) {
 void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T, const int* pos,
                   int ctx, int hd, const uint16_t* qn, const uint16_t* kn, float eps,
                   const float* rope, int pair_bound, int pair_offset, int pair_stride,
-                  hipStream_t s) {
+                  const float* kstage, hipStream_t s) {
   if (hd > 512 || hd % 2) ST_DIE("head_dim must be even and at most 512");
   if (pair_stride < 1 || pair_bound - pair_stride + pair_offset >= hd)
     ST_DIE("inconsistent RoPE pair geometry");
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(T, q_heads + kv_heads), dim3(64), 0, s, q,
                      q_heads, kcache, ctx, hd, pos, qn, kn, eps, rope, pair_bound,
-                     pair_offset, pair_stride);
+                     pair_offset, pair_stride, kstage);
   HIP_CHECK(hipGetLastError());
 }
 

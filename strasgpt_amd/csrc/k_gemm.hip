@@ -313,7 +313,10 @@ __global__ __launch_bounds__(NW * WAVE, OCC ? OCC : 1) void gemm_kernel(GemmPara
             float* cache = kv < p.kv_dim ? p.kcache : p.vcache;
             const int j2 = kv < p.kv_dim ? kv : kv - p.kv_dim;
             const int head = j2 / p.head_dim, h = j2 % p.head_dim;
-            cache[((size_t)head * p.ctx + P + m) * p.head_dim + h] = v;
+            const size_t at = ((size_t)head * p.ctx + P + m) * p.head_dim + h;
+            if (!p.kv_bf16) cache[at] = v;
+            else if (kv < p.kv_dim) p.kstage[(size_t)m * p.kv_dim + kv] = v;  // rounded after RoPE
+            else ((uint16_t*)cache)[at] = f32_to_bf16_any(v);
           }
         }
       }
@@ -576,7 +579,10 @@ __global__ __launch_bounds__(NW * WAVE, OCC) void gemm3_kernel(GemmParams p) {
             float* cache = kv < p.kv_dim ? p.kcache : p.vcache;
             const int j2 = kv < p.kv_dim ? kv : kv - p.kv_dim;
             const int head = j2 / p.head_dim, h = j2 % p.head_dim;
-            cache[((size_t)head * p.ctx + P + m) * p.head_dim + h] = v;
+            const size_t at = ((size_t)head * p.ctx + P + m) * p.head_dim + h;
+            if (!p.kv_bf16) cache[at] = v;
+            else if (kv < p.kv_dim) p.kstage[(size_t)m * p.kv_dim + kv] = v;  // rounded after RoPE
+            else ((uint16_t*)cache)[at] = f32_to_bf16_any(v);
           }
         }
       }

@@ -157,7 +157,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
           } else {
             const int j = n - p.q_dim - p.kv_dim;
             const int head = j / p.head_dim, h = j % p.head_dim;
-            p.vcache[((size_t)head * p.ctx + *p.pos) * p.head_dim + h] = acc[r];
+            const size_t at = ((size_t)head * p.ctx + *p.pos) * p.head_dim + h;
+            if (p.kv_bf16) ((uint16_t*)p.vcache)[at] = f32_to_bf16_any(acc[r]);
+            else p.vcache[at] = acc[r];
           }
         }
       }
@@ -194,7 +196,9 @@ __device__ __forceinline__ void gemv_store(const GemvParams& p, int n, float a, 
     } else {
       const int j = n - p.q_dim - p.kv_dim;
       const int head = j / p.head_dim, h = j % p.head_dim;
-      p.vcache[((size_t)head * p.ctx + *p.pos) * p.head_dim + h] = a;
+      const size_t at = ((size_t)head * p.ctx + *p.pos) * p.head_dim + h;
+      if (p.kv_bf16) ((uint16_t*)p.vcache)[at] = f32_to_bf16_any(a);
+      else p.vcache[at] = a;
     }
   }
 }

@@ -32,9 +32,10 @@ struct GemvParams {
   // GEMV_QKV destinations
   float* q;        // [q_dim]
   float* kraw;     // [kv_dim]  (pre-norm, pre-RoPE keys of this step)
-  float* vcache;   // this layer's [kv_heads][ctx][head_dim]
+  float* vcache;   // this layer's [kv_heads][ctx][head_dim] (bf16 when kv_bf16)
   const int* pos;  // device: cache position of this step
   int q_dim, kv_dim, head_dim, ctx;
+  int kv_bf16;     // the cache stores bf16 (round to nearest even)
 };
 void gemv(const GemvParams& p, int epilogue, hipStream_t s);
 
@@ -119,6 +120,10 @@ struct GemmParams {
   // GEMM_QKV
   float* q; float* kcache; float* vcache; const int* pos;
   int q_dim, kv_dim, head_dim, ctx;
+  // bf16 cache (kv_bf16): values stored rounded into vcache (as bf16), raw
+  // keys into kstage [M][kv_dim] fp32 (qk_norm_rope rounds them after RoPE)
+  int kv_bf16;
+  float* kstage;
 };
 void gemm(const GemmParams& p, int epilogue, int precision, int splits, hipStream_t s);
 // Split-K factor that fills the CUs for an M x N output (1: no split).
@@ -145,17 +150,21 @@ struct NormParams {
 };
 void residual_norm(const NormParams& p, hipStream_t s);
 // Per-head RMSNorm (if norm weights given) and RoPE, in place, on T rows of
-// q ([T][heads*hd]) and on the T new key rows of one layer's k-cache.
+// q ([T][heads*hd]) and on the T new key rows of one layer's k-cache. With
+// a bf16 cache (kstage given) the raw keys come from kstage [T][kv_heads*hd]
+// and the results are stored rounded into the bf16 cache.
 void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T,
                   const int* pos, int ctx, int hd, const uint16_t* qn,
                   const uint16_t* kn, float eps, const float* rope,
-                  int pair_bound, int pair_offset, int pair_stride, hipStream_t s);
+                  int pair_bound, int pair_offset, int pair_stride, const float* kstage,
+                  hipStream_t s);
 
 // ---------------------------------------------------------- attention --
 struct AttnParams {
   const float* q;        // [T][q_heads*hd]
-  const float* kcache;   // layer base [kv_heads][ctx][hd]
+  const float* kcache;   // layer base [kv_heads][ctx][hd] (bf16 when kv_bf16)
   const float* vcache;
+  int kv_bf16;
   float* out;            // decode: [q_heads*hd] fp32
   uint16_t* out_hi;      // prefill: [T][q_heads*hd] bf16 planes (O-GEMM input)
   uint16_t* out_lo;      //   (out_lo may be null)
@@ -186,9 +195,10 @@ void attention_prefill(const AttnParams& p, hipStream_t s);
 void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s);
 // Cache rows [r0, r1) of every kv head of one layer into the bf16 planes the
 // split-bf16 prefill kernel reads (AttnParams khi .. vtlo).
+// With a bf16 cache (kv_bf16) the rows are bf16 already: hi = the row, lo = 0.
 void attention_split_rows(const float* kcache, const float* vcache, uint16_t* khi, uint16_t* klo,
                           uint16_t* vthi, uint16_t* vtlo, int kv_heads, int ctx, int ctx_pad, int hd,
-                          int r0, int r1, hipStream_t s);
+                          int r0, int r1, int kv_bf16, hipStream_t s);
 void attention_decode(const AttnParams& p, hipStream_t s);
 int attention_decode_chunks(int kv_heads);
 // Sets the decode kernels' LDS limits; called once per device before use.

@@ -30,6 +30,7 @@ void sg_capture_hidden(transformer_t* t, float* out, float* out_final);
 int sg_set_prefill_precision(transformer_t* t, int mode);
 const char* sg_version(void);
 int sg_set_decode_mode(transformer_t* t, int mode);
+int sg_set_kv_cache_format(transformer_t* t, int format);
 void sg_profile(transformer_t* t, int enable);
 int sg_profile_read(transformer_t* t, int kernel_class, transformer_kernel_stat_t* out);
 int sg_kernel_rate(transformer_t* t, int kernel_class, int reps, double* avg_us, double* bytes);

@@ -140,6 +140,12 @@ struct transformer_device {
   bool use_graph = true;  // STRASGPT_DECODE_GRAPH=0: eager decode steps
   int decode_mode = TRANSFORMER_DECODE_GRAPH;
   float *kc = nullptr, *vc = nullptr, *rope = nullptr;
+  // KV-cache format: fp32 (the reference's) or bf16 (kv_bf16: 2-byte
+  // elements in the same [L][kvh][ctx][hd] layout, values rounded to
+  // nearest even); with bf16, prefill stages the raw keys in kstage
+  // [chunk][kvd] fp32 until their norm and RoPE
+  int kv_bf16 = 0;
+  float* kstage = nullptr;
   // The cache rows as bf16 hi/lo planes for the split-bf16 prefill
   // attention: K [L][kvh][ctx][hd], V transposed [L][kvh][hd][ctx_pad];
   // zero-initialised, rows [0, split_pos) converted (every layer).
@@ -195,6 +201,17 @@ T* dalloc(size_t count) {
   if (count == 0) count = 1;
   HIP_CHECK(hipMalloc(&p, count * sizeof(T)));
   return (T*)p;
+}
+
+// The K and V caches (`cache` elements each) in D's format, zeroed, and for
+// a bf16 cache the prefill key staging rows.
+void alloc_kv(Dev* D, size_t cache) {
+  const size_t es = D->kv_bf16 ? 2 : 4;
+  D->kc = (float*)dalloc<char>(cache * es);
+  D->vc = (float*)dalloc<char>(cache * es);
+  HIP_CHECK(hipMemsetAsync(D->kc, 0, cache * es, D->stream));
+  HIP_CHECK(hipMemsetAsync(D->vc, 0, cache * es, D->stream));
+  if (D->kv_bf16) D->kstage = dalloc<float>(D->chunk * D->kvd);
 }
 
 uint16_t* W16(Dev* D, int cls, int layer = 0) {
@@ -451,11 +468,16 @@ void ffn_moe(Dev* D, int l, int T) {
   }
 }
 
+// Layer l's K and V cache bases (fp32 or bf16 elements).
+float* kv_layer(const Dev* D, float* base, int l) {
+  const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
+  return (float*)((char*)base + l * cache_layer * (D->kv_bf16 ? 2 : 4));
+}
+
 void layer_decode(Dev* D, int l) {
   hipStream_t s = D->stream;
-  const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
-  float* kc = D->kc + l * cache_layer;
-  float* vc = D->vc + l * cache_layer;
+  float* kc = kv_layer(D, D->kc, l);
+  float* vc = kv_layer(D, D->vc, l);
   const double d = D->d;
 
   sg::GemvParams g{};
@@ -473,6 +495,7 @@ void layer_decode(Dev* D, int l) {
   g.kv_dim = D->kvd;
   g.head_dim = D->hd;
   g.ctx = D->ctx;
+  g.kv_bf16 = D->kv_bf16;
   {
     Prof pr(D, K_QKV_GEMV, (double)D->qkv_rows * d * 2, 2.0 * D->qkv_rows * d);
     sg::gemv(g, sg::GEMV_QKV, s);
@@ -491,6 +514,7 @@ void layer_decode(Dev* D, int l) {
   a.ctx = D->ctx;
   a.kraw = D->kraw;
   a.kcache_w = kc;
+  a.kv_bf16 = D->kv_bf16;
   a.qn = D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr;
   a.kn = D->qk_norm ? W16(D, W_K_NORM, l) : nullptr;
   a.eps = D->eps;
@@ -503,7 +527,7 @@ void layer_decode(Dev* D, int l) {
   a.counters = D->attn_cnt;
   {
     const double keys = (double)D->host_pos + 1;
-    Prof pr(D, K_ATT_DEC, 2.0 * D->kvh * keys * D->hd * 4, 4.0 * D->qh * keys * D->hd);
+    Prof pr(D, K_ATT_DEC, 2.0 * D->kvh * keys * D->hd * (D->kv_bf16 ? 2 : 4), 4.0 * D->qh * keys * D->hd);
     sg::attention_decode(a, s);
   }
 
@@ -617,8 +641,8 @@ int attn_rows() {
 void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
   hipStream_t s = D->stream;
   const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
-  float* kc = D->kc + l * cache_layer;
-  float* vc = D->vc + l * cache_layer;
+  float* kc = kv_layer(D, D->kc, l);
+  float* vc = kv_layer(D, D->vc, l);
   const double d = D->d, M = T;
   const bool split = D->precision == sg::GEMM_SPLIT2;
 
@@ -638,6 +662,8 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
   g.kv_dim = D->kvd;
   g.head_dim = D->hd;
   g.ctx = D->ctx;
+  g.kv_bf16 = D->kv_bf16;
+  g.kstage = D->kv_bf16 ? D->kstage : nullptr;
   {
     Prof pr(D, K_QKV_GEMM, (double)D->qkv_rows * d * 2, 2.0 * M * D->qkv_rows * d);
     sg::gemm(g, sg::GEMM_QKV, D->precision, 1, s);
@@ -647,7 +673,7 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
     sg::qk_norm_rope(D->q, D->qh, kc, D->kvh, T, D->pos, D->ctx, D->hd,
                      D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr,
                      D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
-                     D->po, D->pst, s);
+                     D->po, D->pst, D->kv_bf16 ? D->kstage : nullptr, s);
   }
   // cache rows not yet in the bf16 planes: this chunk's, and any written by
   // decode steps since the last prefill (from a multiple of 32)
@@ -658,13 +684,14 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
     Prof pr(D, K_ELEM, 2.0 * (r1 - r0) * D->kvd * 4 * 2, 0);
     sg::attention_split_rows(kc, vc, D->kp_hi + l * cache_layer, D->kp_lo + l * cache_layer,
                              D->vt_hi + l * vt_layer, D->vt_lo + l * vt_layer, D->kvh, D->ctx,
-                             D->ctx_pad, D->hd, r0, r1, s);
+                             D->ctx_pad, D->hd, r0, r1, D->kv_bf16, s);
   }
   if (l == D->L - 1) D->split_pos = P0 + T;
   sg::AttnParams a{};
   a.q = D->q;
   a.kcache = kc;
   a.vcache = vc;
+  a.kv_bf16 = D->kv_bf16;
   a.khi = D->kp_hi + l * cache_layer;
   a.klo = D->kp_lo + l * cache_layer;
   a.vthi = D->vt_hi + l * vt_layer;
@@ -681,7 +708,7 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
   {
     // causal (query, key) pairs: sum over t of (P + t + 1)
     const double pairs = M * (double)D->host_pos + M * (M + 1) / 2;
-    Prof pr(D, K_ATT_PRE, 2.0 * D->kvh * ((double)D->host_pos + M) * D->hd * 4,
+    Prof pr(D, K_ATT_PRE, 2.0 * D->kvh * ((double)D->host_pos + M) * D->hd * (D->kv_bf16 ? 2 : 4),
             4.0 * D->qh * D->hd * pairs);
     // launches of at most attn_rows() queries
     const int rows = attn_rows();
@@ -1106,10 +1133,12 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->ws_rows = std::max<size_t>(TRANSFORMER_CHUNK_MAX_LEN, T / 2);
   D->ws = dalloc<float>((size_t)D->ws_splits * D->ws_rows * d);
   const size_t cache = (size_t)D->L * D->kvh * D->ctx * hd;
-  D->kc = dalloc<float>(cache);
-  D->vc = dalloc<float>(cache);
-  HIP_CHECK(hipMemsetAsync(D->kc, 0, cache * sizeof(float), D->stream));
-  HIP_CHECK(hipMemsetAsync(D->vc, 0, cache * sizeof(float), D->stream));
+  {
+    const char* f = getenv("STRASGPT_KV_CACHE");
+    if (f && *f && strcmp(f, "fp32") && strcmp(f, "bf16")) ST_DIE("STRASGPT_KV_CACHE must be fp32 or bf16");
+    D->kv_bf16 = f && !strcmp(f, "bf16");
+  }
+  alloc_kv(D, cache);
   D->ctx_pad = (D->ctx + 31) / 32 * 32;
   {
     const size_t kn = cache, vn = (size_t)D->L * D->kvh * D->hd * D->ctx_pad;
@@ -1165,7 +1194,7 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   ss->ffn_act = D->act;
   ss->logits = D->logits;
   ss->cached_count = 0;
-  ss->k_cache = D->kc;
+  ss->k_cache = D->kc;  // device memory, bf16 elements when D->kv_bf16
   ss->v_cache = D->vc;
   ss->rope_cos_sin = D->rope;
   return t;
@@ -1189,7 +1218,7 @@ extern "C" void sg_free(transformer_t* t) {
                     D->moe_sel, D->moe_w, D->moe_act, D->moe_logits, D->moe_offs, D->moe_order, D->moe_out,
                     D->moe_ahi, D->moe_alo,
                     D->xn_hi, D->xn_lo,
-                    D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws};
+                    D->att_hi, D->att_lo, D->act_hi, D->act_lo, D->ws, D->kstage};
     for (void* b : bufs)
       if (b) HIP_CHECK(hipFree(b));
     if (D->h_tok) HIP_CHECK(hipHostFree(D->h_tok));
@@ -1344,6 +1373,32 @@ extern "C" int sg_set_prefill_precision(transformer_t* t, int mode) {
   if (mode != sg::GEMM_SPLIT2 && mode != sg::GEMM_BF16) ST_DIE("unknown prefill precision");
   const int old = t->device->precision;
   t->device->precision = mode;
+  return old;
+}
+
+extern "C" int sg_set_kv_cache_format(transformer_t* t, int format) {
+  if (format != TRANSFORMER_KV_FP32 && format != TRANSFORMER_KV_BF16) ST_DIE("unknown KV-cache format");
+  Dev* D = t->device;
+  if (t->state->cached_count != 0)
+    ST_DIE("the KV-cache format can only change while the cache is empty (before the first token or "
+           "after transformer_reset)");
+  const int old = D->kv_bf16 ? TRANSFORMER_KV_BF16 : TRANSFORMER_KV_FP32;
+  if (format == old) return old;
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  if (D->graph) {  // the captured decode step points at the old cache
+    HIP_CHECK(hipGraphExecDestroy(D->graph));
+    D->graph = nullptr;
+  }
+  HIP_CHECK(hipFree(D->kc));
+  HIP_CHECK(hipFree(D->vc));
+  if (D->kstage) HIP_CHECK(hipFree(D->kstage));
+  D->kc = D->vc = D->kstage = nullptr;
+  D->kv_bf16 = format == TRANSFORMER_KV_BF16;
+  alloc_kv(D, (size_t)D->L * D->kvh * D->ctx * D->hd);
+  t->state->k_cache = D->kc;
+  t->state->v_cache = D->vc;
+  D->split_pos = 0;
+  HIP_CHECK(hipStreamSynchronize(D->stream));
   return old;
 }
 

@@ -94,6 +94,8 @@ def lib():
     L.transformer_set_prefill_precision.argtypes = [TP, ctypes.c_int]
     L.transformer_set_decode_mode.restype = ctypes.c_int
     L.transformer_set_decode_mode.argtypes = [TP, ctypes.c_int]
+    L.transformer_set_kv_cache_format.restype = ctypes.c_int
+    L.transformer_set_kv_cache_format.argtypes = [TP, ctypes.c_int]
     dp = ctypes.POINTER(ctypes.c_double)
     L.transformer_hip_version.restype = ctypes.c_char_p
     L.transformer_profile.argtypes = [TP, ctypes.c_int]
@@ -119,6 +121,8 @@ def _ints(seq: Sequence[int]):
 # Kernel classes reported by transformer_profile_read (include/transformer_hip.h).
 # transformer_set_decode_mode (include/transformer_hip.h)
 DECODE_GRAPH, DECODE_EAGER = 1, 2
+# transformer_set_kv_cache_format (include/transformer_hip.h)
+KV_FP32, KV_BF16 = 0, 1
 
 PROFILE_KERNELS = ["qkv_gemv", "attention_decode", "o_gemv", "gate_up_gemv", "down_gemv",
                    "logits_gemv", "argmax", "moe_route", "moe_gate_up", "moe_down",
@@ -200,6 +204,10 @@ class Transformer:
     def set_decode_mode(self, mode: int) -> int:
         """DECODE_GRAPH or DECODE_EAGER; returns the old mode."""
         return int(self._lib.transformer_set_decode_mode(self._t, mode))
+
+    def set_kv_cache_format(self, fmt: int) -> int:
+        """KV_FP32 or KV_BF16, while the cache is empty; returns the old format."""
+        return int(self._lib.transformer_set_kv_cache_format(self._t, fmt))
 
     def profile(self, enable: bool):
         self._lib.transformer_profile(self._t, int(enable))

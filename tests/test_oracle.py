@@ -252,6 +252,111 @@ def test_oracle_chunk_invariance(model_dir):
     np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
 
 
+def _bf16_round_by_definition(x):
+    """The nearer of the two bf16 values around x (same sign: the truncation
+    toward zero and the next bf16 away from it), ties to the even pattern;
+    values past the largest finite bf16 go to infinity as IEEE rounding does."""
+    x = np.float32(x)
+    u = int(np.array(x).view(np.uint32))
+    lo_u = u & 0xFFFF0000
+    hi_u = lo_u + 0x10000
+    lo = float(np.array(lo_u, np.uint32).view(np.float32))
+    # past the largest finite bf16 the next value would be 2^128 (IEEE
+    # rounding overflows to infinity from halfway up)
+    over = (hi_u & 0x7FFFFFFF) == 0x7F800000
+    hi = (2.0 ** 128 if x > 0 else -2.0 ** 128) if over else float(np.array(hi_u, np.uint32).view(np.float32))
+    dl, dh = abs(float(x) - lo), abs(hi - float(x))
+    if dl < dh or (dl == dh and (lo_u >> 16) % 2 == 0):
+        return np.float32(lo)
+    return np.float32(np.copysign(np.inf, x)) if over else np.float32(hi)
+
+
+def test_round_bf16_definition():
+    """oracle_round_bf16 (the bf16 KV-cache format) against the definition
+    of round-to-nearest-even on random patterns, exact ties, and the ends of
+    the range."""
+    L = lib()
+    rng = np.random.default_rng(5)
+    pats = rng.integers(0, 0x7F7F0000, 20000, dtype=np.uint64).astype(np.uint32)
+    ties = (rng.integers(0, 0x7F7F, 2000).astype(np.uint32) << 16) | 0x8000
+    for u in np.concatenate([pats, ties, np.array([0, 1, 0x7F7FFFFF, 0x7F7F7FFF, 0x00008000], np.uint32)]):
+        for sign in (0, 0x80000000):
+            x = float(np.array(int(u) | sign, np.uint32).view(np.float32))
+            got = np.float32(L.oracle_round_bf16(x))
+            want = _bf16_round_by_definition(x)
+            assert got.view(np.uint32) == want.view(np.uint32), hex(int(u) | sign)
+    assert np.isinf(L.oracle_round_bf16(float(np.float32(3.4e38))))
+    assert np.isinf(L.oracle_round_bf16(float("inf")))
+    assert np.isnan(L.oracle_round_bf16(float("nan")))
+
+
+def _e4m3_values():
+    """Every finite OCP FP8 E4M3 value by code (sign, 4-bit exponent with
+    bias 7, 3-bit mantissa; exponent 0 is subnormal; S.1111.111 is NaN)."""
+    out = {}
+    for code in range(256):
+        s, e, m = code >> 7, (code >> 3) & 15, code & 7
+        if e == 15 and m == 7:
+            continue
+        v = (m / 8) * 2.0 ** -6 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+        out[code] = -v if s else v
+    return out
+
+
+def test_round_fp8_e4m3_definition():
+    """oracle_round_fp8_e4m3 against a brute-force nearest search over the
+    256 codes (ties to the even code, saturation at 448); the code table is
+    pinned by the format's known points."""
+    vals = _e4m3_values()
+    assert vals[0x7E] == 448.0 and vals[0x08] == 2.0 ** -6 and vals[0x01] == 2.0 ** -9
+    assert vals[0x38] == 1.0 and vals[0xB8] == -1.0 and len(vals) == 254
+    codes = sorted(vals, key=lambda c: (vals[c], c))
+    table = np.array([vals[c] for c in codes])
+    L = lib()
+    rng = np.random.default_rng(6)
+    xs = np.concatenate([rng.uniform(-460, 460, 4000), rng.uniform(-0.03, 0.03, 4000),
+                         np.array(table[:-1] + np.diff(table) / 2),  # exact midpoints
+                         np.array([0.0, 1e-9, 447.9, 448.0, 463.9, 1000.0, -1000.0])])
+    for x in xs.astype(np.float32):
+        got = L.oracle_round_fp8_e4m3(float(x))
+        if abs(x) >= 448:
+            assert got == np.copysign(448.0, x)
+            continue
+        dist = np.abs(table - float(x))
+        best = np.flatnonzero(dist == dist.min())
+        cand = [codes[i] for i in best]
+        even = [c for c in cand if c % 2 == 0 and (vals[c] != 0 or c == 0 or len(cand) == 1)]
+        want = vals[(even or cand)[0]]
+        assert got == want or (want == 0 and got == 0), (float(x), got, want)
+
+
+def test_oracle_kv_formats(model_dir):
+    """The oracle's KV-cache formats: bf16 moves the logits by a small
+    amount and keeps the greedy tokens on tiny-qwen; every format stays
+    chunk-invariant (rounding happens once per cached row)."""
+    d = model_dir("tiny-qwen")
+    prompt = synth.prompt_tokens(256, 12, 12)
+    ref = orc.OracleModel(d, threads=2)
+    want = ref.predict(prompt)
+    ref.reset()
+    want_tok = ref.generate(prompt, 8)
+    for fmt, tol in ((orc.KV_BF16, 5e-2), (orc.KV_FP8_E4M3, None)):
+        om = orc.OracleModel(d, threads=2, kv_format=fmt)
+        a = om.predict(prompt)
+        om.reset()
+        om.predict(prompt[:5])
+        b = om.predict(prompt[5:])
+        np.testing.assert_array_equal(a, b)
+        err = float(np.abs(a - want).max())
+        print(f"kv format {fmt}: max |logit - fp32 cache| {err:.3g} (largest |logit| {float(np.abs(want).max()):.3g})")
+        assert err > 0
+        if tol is not None:
+            assert err < tol
+            om.reset()
+            assert om.generate(prompt, 8) == want_tok
+        om.close()
+
+
 def test_oracle_moe_float64(model_dir):
     """MoE semantics (no reference counterpart) against a float64 numpy
     restatement on the tiny MoE model."""
