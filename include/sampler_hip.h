@@ -34,6 +34,29 @@ size_t sampler_argmax(const float* probability, size_t n);
 #define SAMPLER_ARGMAX_NOALLOC_MAX 262144
 size_t sampler_argmax_noalloc(const float* probability, size_t n);
 
+/* The reference's sampler (include/sampler.h:19-38, source/sampler.c:14-337)
+ * with its state on the GPU: temperature (0: greedy argmax), top_k (0: off),
+ * top_p (outside (0, 1]: off), the xorshift64* generator seeded with seed
+ * (0: time(NULL), like the reference's seed <= 0), the presence marks and a
+ * presence penalty (0 unless set; the reference never sets it). One coin is
+ * drawn per non-greedy call, as in the reference; draws follow its steps
+ * with its per-element arithmetic and differ only in summation order
+ * (softmax, top-p and multinomial running sums), i.e. only when the coin or
+ * top_p lies within that rounding of a boundary. Equal probabilities rank
+ * by index. The sampler lives on the device that is current when it is
+ * built. */
+typedef struct sampler_hip sampler_hip_t;
+sampler_hip_t* sampler_hip_build(size_t vocabulary_len, float temperature, size_t top_k,
+                                 float top_p, unsigned long long seed);
+void sampler_hip_free(sampler_hip_t* sampler);
+void sampler_hip_set_presence_penalty(sampler_hip_t* sampler, float penalty);
+/* The reference's sampler_sample(sampler, logits, token) on a host array of
+ * vocabulary_len logits (not modified) and the previous token (marked
+ * present; < 0: none). Returns the drawn token. */
+size_t sampler_hip_sample(sampler_hip_t* sampler, const float* logits, int token);
+/* The generator state (after the draws so far). */
+unsigned long long sampler_hip_rng_state(sampler_hip_t* sampler);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,28 @@ size_t transformer_generate_greedy(
     transformer_timing_t* timing
 );
 
+/* transformer_generate_greedy with the reference's stochastic sampler in
+ * place of the argmax (source/strasgpt.c:206-252 with sampler_sample,
+ * source/sampler.c:234-337), every draw on the device: after the prompt,
+ * the sampler draws from the last row's logits with the prompt's last
+ * token as the previous token; each decode step feeds the drawn token and
+ * draws again with it as the previous token. The sampler (sampler_hip.h)
+ * carries the parameters, the generator state and the presence marks
+ * across calls, as the reference's sampler_t does; it must have the
+ * model's vocabulary and live on the same device. A temperature of 0 gives
+ * transformer_generate_greedy's tokens. */
+struct sampler_hip;
+size_t transformer_generate_sampled(
+    transformer_t* transformer,
+    size_t token_count,
+    const int* token,
+    size_t step_count,
+    int eos_token_id,
+    struct sampler_hip* sampler,
+    int* out,
+    transformer_timing_t* timing
+);
+
 /* Forget the KV cache (cached_count = 0) so that one loaded model can
  * serve another sequence. The reference has no reset: it builds a new
  * transformer_t per sequence. */

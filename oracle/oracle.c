@@ -276,6 +276,109 @@ size_t oracle_argmax(const float* x, size_t n) {
 /* MoE router (no reference counterpart): the k largest logits in
  * descending order, ties to the lowest index, then softmax over those k
  * with max subtraction, expf and a sequential sum. */
+/* ---- Stochastic sampler: reference source/sampler.c:79-337 ---- */
+
+/* Xorshift64* (source/sampler.c:79-85): the state update and the 32-bit
+ * output of the published generator. */
+static unsigned int sampler_u32(unsigned long long* s) {
+  *s ^= *s >> 12;
+  *s ^= *s << 25;
+  *s ^= *s >> 27;
+  return (unsigned int)((*s * 0x2545F4914F6CDD1Dull) >> 32);
+}
+/* source/sampler.c:87-90: 24 random bits scaled to [0, 1). */
+static float sampler_f32(unsigned long long* s) { return (sampler_u32(s) >> 8) / 16777216.0f; }
+
+typedef struct {
+  float p;
+  size_t i;
+} prob_index_t;
+/* Descending probability; equal probabilities keep index order (the order
+ * a stable sort of the index-ordered array gives, as glibc's merge-sort
+ * qsort does for source/sampler.c:159-167). */
+static int prob_desc(const void* a_, const void* b_) {
+  const prob_index_t *a = a_, *b = b_;
+  if (a->p > b->p) return -1;
+  if (a->p < b->p) return 1;
+  return a->i < b->i ? -1 : a->i > b->i;
+}
+
+/* One sampler_sample call (source/sampler.c:234-337) on logits[n] (modified
+ * in place like the reference). presence[n] marks tokens seen, prev is the
+ * previous token. Reports the coin and the distance from the coin to the
+ * nearest boundary of the sampled token's cdf interval (margin), which
+ * tells whether a different summation order could pick another token. */
+size_t oracle_sample(oracle_sampler_t* s, float* x, size_t n, unsigned char* presence, int prev,
+                     float* coin_out, double* margin_out) {
+  if (prev >= 0 && (size_t)prev < n) presence[prev] = 1;
+  if (s->presence_penalty != 0.0f)
+    for (size_t i = 0; i < n; i++)
+      if (presence[i]) x[i] -= s->presence_penalty;
+  if (coin_out) *coin_out = -1.0f;
+  if (margin_out) *margin_out = INFINITY;
+  if (s->temperature == 0.0f) return oracle_argmax(x, n);
+  for (size_t i = 0; i < n; i++) x[i] /= s->temperature;
+  /* softmax (source/sampler.c:104-123) */
+  float mx = x[0];
+  for (size_t i = 1; i < n; i++)
+    if (x[i] > mx) mx = x[i];
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; i++) {
+    x[i] = expf(x[i] - mx);
+    sum += x[i];
+  }
+  for (size_t i = 0; i < n; i++) x[i] /= sum;
+  const float coin = sampler_f32(&s->rng_state);
+  if (coin_out) *coin_out = coin;
+  prob_index_t* pi = malloc(n * sizeof(*pi));
+  double cut_margin = INFINITY;
+  if (s->top_k > 0) { /* source/sampler.c:170-193 */
+    for (size_t i = 0; i < n; i++) pi[i] = (prob_index_t){x[i], i};
+    qsort(pi, n, sizeof(*pi), prob_desc);
+    for (size_t r = s->top_k < n ? s->top_k : n; r < n; r++) x[pi[r].i] = 0.0f;
+  }
+  if (s->top_p > 0 && s->top_p <= 1) { /* source/sampler.c:195-229 */
+    for (size_t i = 0; i < n; i++) pi[i] = (prob_index_t){x[i], i};
+    qsort(pi, n, sizeof(*pi), prob_desc);
+    float cum = 0.0f;
+    size_t last = n - 1;
+    for (size_t r = 0; r < n; r++) {
+      const float before = cum;
+      cum += pi[r].p;
+      if (cum >= s->top_p) {
+        last = r;
+        cut_margin = fmin((double)cum - s->top_p, (double)s->top_p - before);
+        break;
+      }
+    }
+    for (size_t r = last + 1; r < n; r++) x[pi[r].i] = 0.0f;
+  }
+  free(pi);
+  /* renormalize (source/sampler.c:139-157) */
+  double dsum = 0.0;
+  for (size_t i = 0; i < n; i++) dsum += (double)x[i];
+  if (dsum <= 0.0) {
+    const float u = 1.0f / (float)n;
+    for (size_t i = 0; i < n; i++) x[i] = u;
+  } else {
+    const float inv = (float)(1.0 / dsum);
+    for (size_t i = 0; i < n; i++) x[i] *= inv;
+  }
+  /* sample_mult (source/sampler.c:125-137) */
+  float cdf = 0.0f;
+  size_t pick = n - 1;
+  for (size_t i = 0; i < n; i++) {
+    const float before = cdf;
+    cdf += x[i];
+    if (coin < cdf) {
+      pick = i;
+      if (margin_out) *margin_out = fmin(fmin((double)cdf - coin, (double)coin - before), cut_margin);
+      break;
+    }
+  }
+  return pick;
+}
+
 void oracle_topk_softmax(size_t n, const float* logits, size_t k, int* index, float* weight) {
   unsigned char taken[1024] = {0};
   for (size_t j = 0; j < k; j++) {

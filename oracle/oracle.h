@@ -86,6 +86,23 @@ void oracle_set_kv_format(oracle_model_t* m, int fmt);
 float oracle_round_bf16(float x);
 float oracle_round_fp8_e4m3(float x);
 
+/* Reference sampler state (source/sampler.c:14-51, include/sampler.h:19-31)
+ * and sampler_sample (source/sampler.c:234-337): presence penalty,
+ * temperature, softmax, top-k, top-p, renormalization, multinomial draw
+ * with the reference's xorshift64* coin. Equal probabilities rank by index
+ * (a stable sort). coin_out gets the coin (-1 when greedy), margin_out the
+ * distance from the coin to the sampled token's cdf interval ends and from
+ * top_p to the top-p cutoff's cumulative sums (INFINITY when greedy). */
+typedef struct {
+  float temperature;
+  size_t top_k;
+  float top_p;
+  float presence_penalty;
+  unsigned long long rng_state;
+} oracle_sampler_t;
+size_t oracle_sample(oracle_sampler_t* s, float* logits, size_t n, unsigned char* presence,
+                     int prev, float* coin_out, double* margin_out);
+
 /* Reference sample_argmax (source/sampler.c:92-102). */
 size_t oracle_argmax(const float* x, size_t n);
 

@@ -115,6 +115,9 @@ def load_lib():
     lib.oracle_attention_row.argtypes = [sz, sz, fp, fp, fp, fp]
     lib.oracle_topk_softmax.argtypes = [sz, fp, sz, ip, fp]
     lib.oracle_set_kv_format.argtypes = [P, ctypes.c_int]
+    lib.oracle_sample.argtypes = [ctypes.POINTER(SamplerState), fp, sz, P, ctypes.c_int,
+                                  fp, ctypes.POINTER(ctypes.c_double)]
+    lib.oracle_sample.restype = sz
     lib.oracle_round_bf16.argtypes = [ctypes.c_float]
     lib.oracle_round_bf16.restype = ctypes.c_float
     lib.oracle_round_fp8_e4m3.argtypes = [ctypes.c_float]
@@ -166,6 +169,41 @@ def classify(name: str):
     if m and m.group(2) in _LAYER:
         return _LAYER[m.group(2)], int(m.group(1))
     return None, None
+
+
+class SamplerState(ctypes.Structure):
+    """oracle_sampler_t (oracle.h)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_size_t),
+                ("top_p", ctypes.c_float), ("presence_penalty", ctypes.c_float),
+                ("rng_state", ctypes.c_ulonglong)]
+
+
+class Sampler:
+    """The reference sampler (source/sampler.c:234-337) on host logits."""
+
+    def __init__(self, vocab: int, temperature: float, top_k: int, top_p: float, seed: int,
+                 presence_penalty: float = 0.0):
+        self.lib = load_lib()
+        self.state = SamplerState(temperature, top_k, top_p, presence_penalty, seed)
+        self.presence = np.zeros(vocab, np.uint8)
+        self.vocab = vocab
+
+    def sample(self, logits, prev: int, probabilities: bool = False):
+        """(token, coin, margin) for one sampler_sample(logits, prev) call,
+        and the final (renormalised) probabilities when asked."""
+        x = np.array(logits, np.float32, copy=True)
+        coin = ctypes.c_float()
+        margin = ctypes.c_double()
+        tok = self.lib.oracle_sample(ctypes.byref(self.state), fptr(x), self.vocab,
+                                     self.presence.ctypes.data_as(ctypes.c_void_p), int(prev),
+                                     ctypes.byref(coin), ctypes.byref(margin))
+        if probabilities:
+            return int(tok), coin.value, margin.value, x
+        return int(tok), coin.value, margin.value
+
+    @property
+    def rng_state(self) -> int:
+        return int(self.state.rng_state)
 
 
 # KV-cache storage formats (oracle.h ORACLE_KV_*)

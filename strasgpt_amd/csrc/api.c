@@ -69,6 +69,15 @@ size_t transformer_generate_greedy(transformer_t* transformer, size_t token_coun
                             out, timing);
 }
 
+size_t transformer_generate_sampled(transformer_t* transformer, size_t token_count,
+                                    const int* token, size_t step_count, int eos_token_id,
+                                    struct sampler_hip* sampler, int* out,
+                                    transformer_timing_t* timing) {
+  if (!transformer || !out || token_count == 0 || step_count == 0) return 0;
+  return sg_generate_sampled(transformer, token_count, token, step_count, eos_token_id, sampler,
+                             out, timing);
+}
+
 void transformer_reset(transformer_t* transformer) {
   if (transformer) sg_reset(transformer);
 }

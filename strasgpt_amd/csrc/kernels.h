@@ -221,6 +221,45 @@ struct ArgmaxParams {
 void argmax(const ArgmaxParams& p, hipStream_t s);
 int argmax_blocks();
 
+// ----------------------------------------------------------- sampling --
+// The reference's sampler_sample (source/sampler.c:234-337) on device
+// logits: presence penalty, temperature 0 (argmax) or softmax, coin, top-k,
+// top-p, renormalisation and the multinomial draw; writes the token like
+// the argmax (out, seq, pos_inc).
+struct SampleParams {
+  const float* logits;
+  int V;
+  float temperature;
+  int top_k;
+  float top_p;
+  float penalty;
+  unsigned char* presence;       // [V] tokens seen (marked before the penalty)
+  const int* prev;               // previous token on the device, or null:
+  int prev_value;                //   then this one (< 0: none)
+  unsigned long long* rng;       // xorshift64* state, advanced once per non-greedy draw
+  // work buffers
+  float* y;                      // [V]
+  float* part;                   // [512]
+  unsigned* keys;                // [V] x 2 and int [V] x 2: the descending sort
+  unsigned* keys_sorted;
+  int* vals;
+  int* vals_sorted;
+  unsigned char* keep;           // [V]
+  void* sort_temp;
+  size_t sort_temp_bytes;        // sample_sort_temp_bytes(V)
+  float* scal;                   // [4]
+  int* nkeep;
+  float* argmax_v;               // [argmax_blocks()]
+  int* argmax_i;
+  // the drawn token
+  int* out;
+  int* seq;
+  int* seq_len;
+  int* pos_inc;
+};
+void sample(const SampleParams& p, hipStream_t s);
+size_t sample_sort_temp_bytes(int V);
+
 // ---------------------------------------------------------------- MoE --
 // Router logits (bf16 GEMV), top-k with lowest-index ties, softmax over
 // the k selected logits.

@@ -25,6 +25,9 @@ int sg_predict_argmax(transformer_t* t, size_t token_count, const int* token);
 size_t sg_generate_greedy(transformer_t* t, size_t token_count, const int* token,
                           size_t step_count, int eos, int* out,
                           transformer_timing_t* timing);
+size_t sg_generate_sampled(transformer_t* t, size_t token_count, const int* token,
+                           size_t step_count, int eos, struct sampler_hip* sampler, int* out,
+                           transformer_timing_t* timing);
 void sg_reset(transformer_t* t);
 void sg_capture_hidden(transformer_t* t, float* out, float* out_final);
 int sg_set_prefill_precision(transformer_t* t, int mode);

@@ -29,6 +29,7 @@
 #include "hip_check.h"
 #include "kernels.h"
 #include "runtime.h"
+#include "sampler_impl.h"
 #include "safetensors.h"
 
 namespace {
@@ -162,7 +163,8 @@ struct transformer_device {
   int* h_tok = nullptr;
   int* h_pos = nullptr;
   int* h_next = nullptr;
-  hipGraphExec_t graph = nullptr;
+  hipGraphExec_t graph = nullptr;       // decode step + argmax
+  hipGraphExec_t graph_body = nullptr;  // decode step alone (the sampled loop)
   int precision = sg::GEMM_SPLIT2;
   float* cap_out = nullptr;
   float* cap_final = nullptr;
@@ -201,6 +203,12 @@ T* dalloc(size_t count) {
   if (count == 0) count = 1;
   HIP_CHECK(hipMalloc(&p, count * sizeof(T)));
   return (T*)p;
+}
+
+void drop_graphs(Dev* D) {
+  if (D->graph) HIP_CHECK(hipGraphExecDestroy(D->graph));
+  if (D->graph_body) HIP_CHECK(hipGraphExecDestroy(D->graph_body));
+  D->graph = D->graph_body = nullptr;
 }
 
 // The K and V caches (`cache` elements each) in D's format, zeroed, and for
@@ -791,9 +799,8 @@ void forward_chunk(Dev* D, const int* tok, int T, int lc) {
 void ensure_logits(Dev* D, int rows) {
   if (rows <= D->logits_rows) return;
   HIP_CHECK(hipStreamSynchronize(D->stream));
-  if (D->graph) {  // the captured decode step points at the old buffer
-    HIP_CHECK(hipGraphExecDestroy(D->graph));
-    D->graph = nullptr;
+  if (D->graph || D->graph_body) {  // the captured decode step points at the old buffer
+    drop_graphs(D);
   }
   if (D->logits) HIP_CHECK(hipFree(D->logits));
   D->logits = dalloc<float>((size_t)rows * D->V);
@@ -870,17 +877,17 @@ void predict_device(transformer_t* t, size_t T, const int* token, size_t lc,
   }
 }
 
-void build_decode_graph(Dev* D) {
-  if (D->graph) return;
+void build_decode_graph(Dev* D, bool with_argmax = true) {
+  if (with_argmax ? D->graph != nullptr : D->graph_body != nullptr) return;
   hipGraph_t g;
   float* cap = D->cap_out;  // hidden-state capture is never part of the graph
   D->cap_out = nullptr;
   HIP_CHECK(hipStreamBeginCapture(D->stream, hipStreamCaptureModeRelaxed));
   forward_chunk(D, D->next, 1, 1);
-  argmax_to(D, D->logits, true, true);
+  if (with_argmax) argmax_to(D, D->logits, true, true);
   HIP_CHECK(hipStreamEndCapture(D->stream, &g));
   D->cap_out = cap;
-  HIP_CHECK(hipGraphInstantiate(&D->graph, g, nullptr, nullptr, 0));
+  HIP_CHECK(hipGraphInstantiate(with_argmax ? &D->graph : &D->graph_body, g, nullptr, nullptr, 0));
   HIP_CHECK(hipGraphDestroy(g));
 }
 
@@ -1207,7 +1214,7 @@ extern "C" void sg_free(transformer_t* t) {
     if (D->stream) HIP_CHECK(hipStreamSynchronize(D->stream));
     harvest(D);
     for (hipEvent_t e : D->event_pool) HIP_CHECK(hipEventDestroy(e));
-    if (D->graph) HIP_CHECK(hipGraphExecDestroy(D->graph));
+    drop_graphs(D);
     for (int k = 0; k < W_COUNT; k++) {
       if (D->w[k] && !(k == W_OUT && D->tied)) HIP_CHECK(hipFree(D->w[k]));
     }
@@ -1346,6 +1353,69 @@ extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* toke
   return produced;
 }
 
+extern "C" size_t sg_generate_sampled(transformer_t* t, size_t T, const int* token, size_t steps,
+                                      int eos, sampler_hip* smp, int* out, transformer_timing_t* timing) {
+  Dev* D = t->device;
+  if (!smp) ST_DIE("transformer_generate_sampled: NULL sampler");
+  if (smp->V != D->V) ST_DIE("transformer_generate_sampled: sampler vocabulary differs from the model's");
+  int dev = 0;
+  HIP_CHECK(hipGetDevice(&dev));
+  if (dev != smp->device) ST_DIE("transformer_generate_sampled: sampler built on another device");
+  if (T == 0 || steps == 0) ST_DIE("transformer_generate_sampled: needs tokens and steps");
+  if (t->state->cached_count + T + (steps - 1) > (size_t)D->ctx) ST_DIE("context length exhausted");
+  HIP_CHECK(hipStreamSynchronize(smp->stream));  // earlier host-array draws are done
+  HIP_CHECK(hipMemsetAsync(D->seq_len, 0, sizeof(int), D->stream));
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  const double t0 = now_s();
+  predict_device(t, T, token, 1, nullptr);
+  sg::sample(sampler_params(smp, D->logits, nullptr, token[T - 1], D->next, D->seq, D->seq_len, nullptr),
+             D->stream);
+  HIP_CHECK(hipStreamSynchronize(D->stream));
+  harvest(D);
+  const double t1 = now_s();
+  size_t produced = 1;
+  bool stop = false;
+  if (eos >= 0) {
+    HIP_CHECK(hipMemcpy(D->h_next, D->next, sizeof(int), hipMemcpyDeviceToHost));
+    stop = *D->h_next == eos;
+  }
+  if (steps > 1 && !stop) {
+    const bool eager = D->prof || !D->use_graph || D->decode_mode == TRANSFORMER_DECODE_EAGER;
+    if (!eager) build_decode_graph(D, false);
+    set_pos(D, t->state->cached_count);
+    for (size_t i = 1; i < steps && !stop; i++) {
+      if (eager) {
+        D->host_pos = t->state->cached_count + produced - 1;
+        forward_chunk(D, D->next, 1, 1);
+      } else {
+        HIP_CHECK(hipGraphLaunch(D->graph_body, D->stream));
+      }
+      // the previous token (the one just fed) is read before the draw overwrites it
+      sg::sample(sampler_params(smp, D->logits, D->next, -1, D->next, D->seq, D->seq_len, D->pos), D->stream);
+      if (eager) {
+        HIP_CHECK(hipStreamSynchronize(D->stream));
+        harvest(D);
+      }
+      produced++;
+      if (eos >= 0) {
+        HIP_CHECK(hipMemcpyAsync(D->h_next, D->next, sizeof(int), hipMemcpyDeviceToHost, D->stream));
+        HIP_CHECK(hipStreamSynchronize(D->stream));
+        stop = *D->h_next == eos;
+      }
+    }
+    HIP_CHECK(hipStreamSynchronize(D->stream));
+    t->state->cached_count += produced - 1;
+  }
+  const double t2 = now_s();
+  HIP_CHECK(hipMemcpy(out, D->seq, produced * sizeof(int), hipMemcpyDeviceToHost));
+  if (timing) {
+    timing->prefill_s = t1 - t0;
+    timing->decode_s = t2 - t1;
+    timing->decode_count = produced - 1;
+  }
+  return produced;
+}
+
 // The bf16 planes of the cache (prefill attention) are valid for rows
 // [0, split_pos) of the current sequence only: a new sequence starts with
 // none converted.
@@ -1385,9 +1455,8 @@ extern "C" int sg_set_kv_cache_format(transformer_t* t, int format) {
   const int old = D->kv_bf16 ? TRANSFORMER_KV_BF16 : TRANSFORMER_KV_FP32;
   if (format == old) return old;
   HIP_CHECK(hipStreamSynchronize(D->stream));
-  if (D->graph) {  // the captured decode step points at the old cache
-    HIP_CHECK(hipGraphExecDestroy(D->graph));
-    D->graph = nullptr;
+  if (D->graph || D->graph_body) {  // the captured decode step points at the old cache
+    drop_graphs(D);
   }
   HIP_CHECK(hipFree(D->kc));
   HIP_CHECK(hipFree(D->vc));

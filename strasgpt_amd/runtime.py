@@ -105,6 +105,18 @@ def lib():
     L.transformer_kernel_rate.argtypes = [TP, ctypes.c_int, ctypes.c_int, dp, dp]
     L.sampler_argmax.restype = sz
     L.sampler_argmax.argtypes = [fp, sz]
+    VP = ctypes.c_void_p
+    L.sampler_hip_build.restype = VP
+    L.sampler_hip_build.argtypes = [sz, ctypes.c_float, sz, ctypes.c_float, ctypes.c_ulonglong]
+    L.sampler_hip_free.argtypes = [VP]
+    L.sampler_hip_set_presence_penalty.argtypes = [VP, ctypes.c_float]
+    L.sampler_hip_sample.restype = sz
+    L.sampler_hip_sample.argtypes = [VP, fp, ctypes.c_int]
+    L.sampler_hip_rng_state.restype = ctypes.c_ulonglong
+    L.sampler_hip_rng_state.argtypes = [VP]
+    L.transformer_generate_sampled.restype = sz
+    L.transformer_generate_sampled.argtypes = [TP, sz, ctypes.POINTER(ctypes.c_int), sz, ctypes.c_int, VP,
+                                               ctypes.POINTER(ctypes.c_int), ctypes.POINTER(Timing)]
     _LIB = L
     return L
 
@@ -198,6 +210,15 @@ class Transformer:
                                                   eos, out, ctypes.byref(tm))
         return [int(out[i]) for i in range(n)], tm
 
+    def generate_sampled(self, prompt: Sequence[int], steps: int, sampler: "Sampler", eos: int = -1
+                         ) -> Tuple[List[int], Timing]:
+        """transformer_generate_sampled: the decode loop with device sampling."""
+        out = (ctypes.c_int * max(steps, 1))()
+        tm = Timing()
+        n = self._lib.transformer_generate_sampled(self._t, len(prompt), _ints(prompt), steps, eos,
+                                                   sampler.handle, out, ctypes.byref(tm))
+        return [int(out[i]) for i in range(n)], tm
+
     def set_prefill_precision(self, mode: int) -> int:
         return int(self._lib.transformer_set_prefill_precision(self._t, mode))
 
@@ -235,6 +256,36 @@ def argmax(values: np.ndarray) -> int:
     """sampler_argmax: the reference's sample_argmax on the device."""
     v = np.ascontiguousarray(values, np.float32)
     return int(lib().sampler_argmax(_fp(v), v.size))
+
+
+class Sampler:
+    """sampler_hip_t: the reference's sampler with its state on the device."""
+
+    def __init__(self, vocab: int, temperature: float, top_k: int, top_p: float, seed: int,
+                 presence_penalty: float = 0.0):
+        self._lib = lib()
+        self.handle = self._lib.sampler_hip_build(vocab, temperature, top_k, top_p, seed)
+        if presence_penalty:
+            self._lib.sampler_hip_set_presence_penalty(self.handle, presence_penalty)
+
+    def sample(self, logits: np.ndarray, prev: int) -> int:
+        v = np.ascontiguousarray(logits, np.float32)
+        return int(self._lib.sampler_hip_sample(self.handle, _fp(v), int(prev)))
+
+    @property
+    def rng_state(self) -> int:
+        return int(self._lib.sampler_hip_rng_state(self.handle))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self._lib.sampler_hip_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def version() -> str:

@@ -473,3 +473,84 @@ def test_oracle_dense_float64(name, model_dir):
     om = orc.OracleModel(d, threads=2)
     prompt = synth.prompt_tokens(shp.vocab, 5, 9)
     np.testing.assert_allclose(om.predict(prompt)[0], numpy_forward(d, prompt), rtol=2e-4, atol=2e-4)
+
+
+def _xorshift_coins(seed, n):
+    """Xorshift64* (the reference's random_u32, source/sampler.c:79-85) in
+    Python integers, and the coin of source/sampler.c:87-90."""
+    s, out = seed, []
+    for _ in range(n):
+        s ^= s >> 12
+        s ^= (s << 25) & (2 ** 64 - 1)
+        s ^= s >> 27
+        u = ((s * 0x2545F4914F6CDD1D) & (2 ** 64 - 1)) >> 32
+        out.append((u >> 8) / 16777216.0)
+    return out, s
+
+
+def test_sampler_coins():
+    """The oracle sampler's coins are the xorshift64* stream (one draw per
+    non-greedy call, none when greedy), uniform on [0, 1) in 2^-24 steps."""
+    x = np.zeros(4, np.float32)
+    s = orc.Sampler(4, 1.0, 0, 0.0, 12345)
+    coins = [s.sample(x, -1)[1] for _ in range(2000)]
+    want, state = _xorshift_coins(12345, 2000)
+    assert coins == [np.float32(c) for c in want] and s.rng_state == state
+    g = orc.Sampler(4, 0.0, 0, 0.0, 12345)
+    assert g.sample(x, -1)[1] == -1 and g.rng_state == 12345
+    big, _ = _xorshift_coins(7, 100000)
+    hist = np.histogram(big, bins=10, range=(0, 1))[0]
+    assert np.all(np.abs(hist - 10000) < 5 * 100)  # 5 sigma
+    assert all(c * 16777216 == int(c * 16777216) for c in big[:1000])
+
+
+def _filtered(logits, temp, top_k, top_p):
+    """The sampling distribution of source/sampler.c:234-337 in float64:
+    softmax at the temperature, the k most likely (index order among equal
+    probabilities), then the shortest descending prefix reaching top_p,
+    renormalized."""
+    z = np.asarray(logits, np.float64) / temp
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    order = sorted(range(len(p)), key=lambda i: (-p[i], i))
+    keep = order[:top_k] if top_k > 0 else order
+    if 0 < top_p <= 1:
+        cum, cut = 0.0, len(keep)
+        for r, i in enumerate(keep):
+            cum += p[i]
+            if cum >= top_p:
+                cut = r + 1
+                break
+        keep = keep[:cut]
+    q = np.zeros_like(p)
+    q[keep] = p[keep]
+    return q / q.sum()
+
+
+@pytest.mark.parametrize("temp,top_k,top_p", [(1.0, 0, 0.0), (0.7, 3, 0.0), (1.3, 0, 0.8),
+                                               (1.0, 4, 0.9)])
+def test_sampler_distribution(temp, top_k, top_p):
+    """Sampled frequencies over 40000 calls match the float64 distribution
+    the reference's steps define (within 5 sigma per token)."""
+    logits = np.array([0.3, -1.2, 1.7, 0.9, 0.9, -0.4, 2.2, -3.0], np.float32)
+    want = _filtered(logits, temp, top_k, top_p)
+    s = orc.Sampler(len(logits), temp, top_k, top_p, 99)
+    n = 40000
+    got = np.bincount([s.sample(logits, -1)[0] for _ in range(n)], minlength=len(logits)) / n
+    sigma = np.sqrt(want * (1 - want) / n) + 1e-9
+    assert np.all(np.abs(got - want) <= 5 * sigma + 1e-12), (got, want)
+    assert np.all(got[want == 0] == 0)
+
+
+def test_sampler_special_cases():
+    """Greedy and degenerate filters give the argmax (ties to the lower
+    index); top-k 1 ignores the coin; a presence penalty removes a seen
+    token."""
+    tie = np.array([0.5, 2.0, -1.0, 2.0], np.float32)
+    assert orc.Sampler(4, 0.0, 0, 0.0, 1).sample(tie, -1)[0] == 1
+    s = orc.Sampler(4, 1.0, 1, 0.0, 3)
+    assert {s.sample(tie, -1)[0] for _ in range(200)} == {1}
+    s = orc.Sampler(4, 1.0, 0, 1e-7, 3)
+    assert {s.sample(tie, -1)[0] for _ in range(200)} == {1}
+    s = orc.Sampler(4, 0.0, 0, 0.0, 3, presence_penalty=100.0)
+    assert s.sample(tie, 1)[0] == 3  # token 1 marked present and penalised
