@@ -151,6 +151,24 @@ def probe_traffic(t, prompt):
     log("probe decode done")
 
 
+def probe_mfma():
+    """strasgpt_kbench_mfma: the bf16 matrix-core rate with constant and with
+    random (toggling) operands, one and two waves per SIMD, for the clock
+    counter runs."""
+    import ctypes
+    from strasgpt_amd import runtime
+    lib = runtime.lib()
+    lib.strasgpt_kbench_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_double)]
+    tf = ctypes.c_double()
+    for rnd in (0, 1):
+        for waves in (1, 2):
+            if lib.strasgpt_kbench_mfma(rnd, waves, 20000 // waves, 4, ctypes.byref(tf)) != 0:
+                raise RuntimeError("strasgpt_kbench_mfma refused its arguments")
+            log(f"mfma probe: {'random' if rnd else 'constant'} operands, {waves} wave(s) per SIMD: "
+                f"{tf.value:.1f} TFLOP/s ({tf.value / 25:.1f}% of 2.5 PF)")
+
+
 def traffic_for(kernel, config):
     """HBM bytes per launch of a decode kernel class from the committed counter
     summary of this workload (FETCH_SIZE + WRITE_SIZE, calibrated on
@@ -181,6 +199,9 @@ def main():
     ap.add_argument("--probe-traffic", action="store_true",
                     help="only launch the kernels an HBM-counter run needs (a 256 MiB copy, "
                          "then a 16-token prefill and 4 eager decode steps); prints nothing")
+    ap.add_argument("--probe-mfma", action="store_true",
+                    help="only run the sustained MFMA rate probe (constant and random operands, "
+                         "one and two waves per SIMD) and log its rates; prints nothing")
     ap.add_argument("--probe-prefill", action="store_true",
                     help="only run two prefills of the workload's prompt (for MFMA counter "
                          "runs of the prefill GEMMs); prints nothing")
@@ -191,6 +212,9 @@ def main():
         sys.exit(2)
 
     from strasgpt_amd import runtime, synth
+    if args.probe_mfma:
+        probe_mfma()
+        return
     shp = synth.shape(args.config)
     d = ensure_model(shp, args.seed)
     prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, 42)

@@ -25,6 +25,17 @@ int strasgpt_kbench_mxfp4_decode(const uint8_t* codes, const uint8_t* scales, in
  * per launch. The calibration kernel for HBM traffic counters. */
 int strasgpt_kbench_copy(size_t bytes, int iters, double* avg_us);
 
+/* Sustained bf16 matrix-core rate: every wave of waves_per_simd (1 or 2) per
+ * SIMD on every CU issues 16 x iters v_mfma_f32_32x32x16_bf16 over 8
+ * independent accumulators, operands cycled over 8 register fragments of
+ * random finite bf16 values (random_operands) or one constant pattern; one
+ * warm-up launch, then `launches` launches between two events; *tflops is
+ * the achieved rate. The reference point for the prefill GEMMs: the rate
+ * and, read with the clock counters, the clock the chip holds when operands
+ * toggle like real data. */
+int strasgpt_kbench_mfma(int random_operands, int waves_per_simd, int iters, int launches,
+                         double* tflops);
+
 #ifdef __cplusplus
 }
 #endif
