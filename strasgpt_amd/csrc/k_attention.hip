@@ -26,24 +26,11 @@ namespace {
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-// Decode: threads per block, keys per LDS tile, query heads per kv head
-// and key chunks per kv head, at most.
+// Decode: threads per block, query heads per kv head and blocks (partial
+// results) per kv head, at most.
 constexpr int kDecThreads = 256;
-constexpr int kDecTile = 32;
 constexpr int kDecMaxG = 8;
 constexpr int kDecMaxChunks = 64;
-constexpr int kDecMinChunk = 32;  // keys per chunk, at least
-
-// Split of `total` keys into nch chunks of len keys (the last may be
-// shorter, none is empty): as many chunks as allowed, each of at least
-// kDecMinChunk keys and a whole number of kDecTile-key tiles (a chunk of 33
-// keys would cost two tile steps for one key more).
-__host__ __device__ inline void attention_decode_split(int total, int max_chunks, int& nch, int& len) {
-  nch = total < max_chunks * kDecMinChunk ? (total + kDecMinChunk - 1) / kDecMinChunk : max_chunks;
-  len = (total + nch - 1) / nch;
-  len = (len + kDecTile - 1) / kDecTile * kDecTile;
-  nch = (total + len - 1) / len;
-}
 
 // Prefill attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32:
 // fp32 products accumulated in fp32, as the reference computes them; only
@@ -512,53 +499,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
   }
 }
 
-// LDS layout of the decode kernel (floats). K rows are padded to HD + 4
-// floats: the lanes of a wave read one key row each, and with the padding
-// eight consecutive rows start in eight different bank groups.
-// With a bf16 cache (B16) the tiles hold bf16 rows: K rows of HD + 8
-// elements (the same 16-byte padding), V rows of HD; sizes below stay in
-// 4-byte units.
-template <int HD, bool B16 = false>
-struct DecLds {
-  static constexpr int KROW = B16 ? HD / 2 + 4 : HD + 4;  // K row stride, 4-byte units
-  static constexpr int VROW = B16 ? HD / 2 : HD;
-  static constexpr int KT = kDecTile * KROW;       // K tile
-  static constexpr int VT = kDecTile * VROW;       // V tile
-  static constexpr int qs = 0;                     // [kDecMaxG][HD] normalised, rotated queries
-  static constexpr int kn = qs + kDecMaxG * HD;    // [HD] this step's processed key
-  static constexpr int flag = kn + HD;             // [4]
-  static constexpr int tiles = flag + 4;           // [2][K tile | V tile]
-  static constexpr int total = tiles + 2 * (KT + VT);
-  static_assert(tiles % 4 == 0 && KT % 4 == 0, "tiles are 16-byte aligned");
-};
-
-// Keys [t0, t0 + n) of a kv head into LDS by the global-to-LDS DMA (16
-// bytes per lane): V rows back to back (each wave instruction fills 1 KiB),
-// K rows one instruction per row (its first HD / 4 lanes) into the padded
-// layout. No registers are held; the caller waits for vector memory
-// operations and syncs the block.
-template <int HD, bool B16 = false>
-__device__ __forceinline__ void dma_kv(const float* kb, const float* vb, int t0, int n, float* kt,
-                                       float* vt) {
-  constexpr int RB = HD * (B16 ? 2 : 4);  // row bytes
-  constexpr int CPR = RB / 16;            // 16-byte chunks per row
-  constexpr int NWAVE = kDecThreads / WAVE;
-  const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  const char* ks = (const char*)kb + (size_t)t0 * RB;
-  const char* vs = (const char*)vb + (size_t)t0 * RB;
-  const int units = n * CPR;
-  for (int u0 = wave * WAVE; u0 < units; u0 += kDecThreads) {
-    const int u = u0 + lane;
-    if (u < units)
-      __builtin_amdgcn_global_load_lds((const void*)(vs + u * 16), (lds_ptr)(vt + u0 * 4), 16, 0, 0);
-  }
-  for (int r = wave; r < n; r += NWAVE) {
-    if (lane < CPR)
-      __builtin_amdgcn_global_load_lds((const void*)(ks + r * RB + lane * 16),
-                                       (lds_ptr)(kt + r * DecLds<HD, B16>::KROW), 16, 0, 0);
-  }
-}
-
 // RMSNorm (when nw is given) and RoPE of one head vector held by a wave:
 // xv / wv are the lane's elements lane + i*64 of the vector and of the norm
 // weights, fr / fi the rotation of the lane's pair (element lane*pst and
@@ -607,67 +547,123 @@ __device__ __forceinline__ void norm_rope_regs(const float* xv, const float* wv,
   }
 }
 
-// Decode attention in one launch. Block (chunk c, kv head g) takes keys
-// [c*len, min(P+1, (c+1)*len)) for the G query heads of kv head g (the K/V
-// rows are read once for the group), in tiles of kDecTile keys brought to
-// LDS by DMA, double-buffered: tile t+1 is in flight while tile t is used.
-// Wave w owns query heads w*GW .. w*GW+GW-1 and keeps their online softmax
-// state (running max m, sum l) and unnormalised output in registers; per
-// tile, lane (key kl = lane % 32, half = lane / 32) forms the score of its
-// key over half of the head dimension (the halves meet by one cross-lane
-// add), the wave updates m and l, and P.V runs with DPL output dimensions
-// per lane, the probabilities broadcast lane by lane. One block barrier per
-// tile. The block stores (m, l, output) per head with agent-coherent
-// stores, then counts itself done on the kv head's counter; the last block
-// of the head combines the chunks (one wave per head, the chunk weights in
-// lanes):
-//   att = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c,  M = max_c m_c,
-// and resets the counter for the next launch. The block holding position
-// P also normalises and rotates this step's key (the lane whose key is P
-// reads it from LDS rather than from the tile) and writes it to the cache
-// (the value row was written by the QKV projection).
-// Two blocks fit per CU (LDS), so at most 2 waves per SIMD: the register
-// budget that lets every K read of a tile be in flight at once.
-template <int HD, int GW, bool B16>
-__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_decode_kernel(
-    AttnParams p) {
-  using L = DecLds<HD, B16>;
-  constexpr int NW = kDecThreads / WAVE;
-  constexpr int PER = (HD + WAVE - 1) / WAVE;
-  constexpr int MAXV = (kDecMaxG + 1 + NW - 1) / NW;  // head vectors per wave in the staging
-  constexpr int HALF = HD / 2;                        // dims per lane in a score
-  constexpr int DPL = HD >= WAVE ? HD / WAVE : 1;     // output dims per lane
-  static_assert(kDecTile == 32 && NW * GW >= 1, "one key per lane pair");
-  static_assert(kDecMaxChunks <= WAVE, "one lane per chunk in the combine");
-  extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* qs = lds + L::qs;
-  float* kn = lds + L::kn;
-  int* flag = (int*)(lds + L::flag);
-  float* tiles = lds + L::tiles;
 
-  const int c = blockIdx.x, g = blockIdx.y;
+// Decode attention on the matrix cores, over the cache's bf16 planes (the
+// operands of the split-bf16 prefill kernel: K [kv][ctx][hd] hi/lo, V
+// transposed [kv][hd][ctx_pad] hi/lo; with a bf16 cache the hi planes hold
+// the rows and lo is not read).
+//
+// Block (b, kv head g) takes tiles [b*tpb, (b+1)*tpb) of 32 keys; wave w
+// takes tiles w, w+4, ... of them (waves without a tile only help with the
+// queries), their operands loaded straight into registers in the MFMA
+// layouts (no LDS), with its own online softmax state for all G query
+// heads at once:
+// * S^T = K Q^T by v_mfma_f32_16x16x32_bf16: the query heads are the 16
+//   B columns (head c < G, the rest zero), A row c of key sub-tile s is key
+//   8 (c / 4) + 4 s + c % 4, so output lane (gq, c) = (lane / 16, lane % 16)
+//   holds keys 8 gq .. 8 gq + 7 of head c: the B operand layout of the P.V
+//   step. Products kh.qh + kh.ql + kl.qh (hi/lo splits, fp32 accumulate).
+// * Softmax in base 2 (scores scaled by log2(e) / sqrt(hd)), reductions
+//   over the four lane groups.
+// * O^T += V^T P^T: one k-step over the tile's keys per 16 dims, A = 16
+//   bytes of a V^T row per plane.
+// The waves' states merge through LDS into the block's (m, l, o) per head,
+// stored agent-coherently for the combining block (the last to arrive on
+// the kv head's counter); a context of one block is written out directly.
+// Key P (this step's) is not in the planes yet: the block holding it
+// normalises and rotates the key (QK-norm, RoPE) and reads the value row
+// from the fp32/bf16 cache, patches them into the operands of the last
+// tile (keys past P zeroed), and writes them to the cache and the planes.
+constexpr int kD2Tile = 32;     // keys per wave step
+// Buffer descriptor word 3 for raw (untyped, unswizzled) buffer loads on
+// gfx9-family GPUs: 32-bit data format, no index/stride.
+constexpr int kRsrcWord3 = 0x00020000;
+// Tiles per block, at least: fewer, larger chunks beat more partial
+// results to combine at short contexts; a context of up to this many tiles
+// is one block per kv head, whose result is the output (no combine).
+constexpr int kD2MinTiles = 2;
+
+// Tiles a wave holds in registers at once (128 VGPRs per tile with the
+// hi and lo planes, 64 with hi only).
+template <bool B16>
+constexpr int kD2Tpw = B16 ? 4 : 2;
+
+// Blocks per kv head (nb <= max_blocks) and tiles per block (tpb) for
+// `total` keys: as many blocks as allowed, each a whole number of tiles.
+__host__ __device__ inline void decode_mfma_split(int total, int max_blocks, int& nb, int& tpb) {
+  const int nt = (total + kD2Tile - 1) / kD2Tile;
+  const int per = (nt + max_blocks - 1) / max_blocks;
+  tpb = per > kD2MinTiles ? per : kD2MinTiles;
+  nb = (nt + tpb - 1) / tpb;
+}
+
+// Lane l's value plus / max with lane l ^ 16 or l ^ 32 (gfx950 lane-swap
+// moves: no LDS round trip), and lane l ^ 8 within a row of 16 (DPP).
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float dpp_ror8(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));  // row_ror:8
+}
+
+__device__ __forceinline__ void split8v(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) split2(x[2 * e], x[2 * e + 1], h[e], l[e]);
+  hi = __builtin_bit_cast(bf16x8, (uint4){h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(bf16x8, (uint4){l[0], l[1], l[2], l[3]});
+}
+
+template <int HD, int GW, bool B16>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParams p) {
+  constexpr int NW = kDecThreads / WAVE;
+  constexpr int NKK = (HD + 31) / 32;  // 32-dim k-steps of S
+  constexpr int DJ = HD / 16;          // 16-dim row blocks of O^T
+  constexpr int PER = (HD + WAVE - 1) / WAVE;
+  constexpr int MAXV = (kDecMaxG + 1 + NW - 1) / NW;  // head vectors per wave in the prologue
+  static_assert(NW == 4 && kD2Tile == 32, "four waves, 32-key tiles");
+  __shared__ __attribute__((aligned(16))) float qs[kDecMaxG * HD];  // normalised, rotated queries
+  __shared__ __attribute__((aligned(16))) float kn[HD];             // this step's key
+  __shared__ float vn[HD];                                          // this step's value
+  __shared__ float mo[NW][kDecMaxG][HD];                            // per-wave outputs
+  __shared__ float ml[NW][kDecMaxG][2];                             // per-wave (m, l)
+  __shared__ int flag;
+
+  const int blk = blockIdx.x, g = blockIdx.y;
   const int G = p.q_heads / p.kv_heads;
   const int P = *p.pos, total = P + 1;
-  int nch, len;
-  attention_decode_split(total, p.splits, nch, len);
-  if (c >= nch) return;  // not counted: the last block waits for nch arrivals
-  const int s0 = c * len, s1 = min(total, s0 + len);
-  const bool has_new = s1 == total;
-  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-  // cache element offsets (a bf16 cache: 2-byte elements)
-  const float* kb = (const float*)((const char*)p.kcache + (size_t)g * p.ctx * HD * (B16 ? 2 : 4));
-  const float* vb = (const float*)((const char*)p.vcache + (size_t)g * p.ctx * HD * (B16 ? 2 : 4));
+  int nb, tpb;
+  decode_mfma_split(total, p.splits, nb, tpb);
+  if (blk >= nb) return;  // not counted: the last block waits for nb arrivals
+  const int nt = (total + kD2Tile - 1) / kD2Tile;
+  const int t0 = blk * tpb, t1 = min(nt, t0 + tpb);
+  const bool has_new = t1 == nt;  // the block holding key P (in tile nt - 1)
+  const int tid = threadIdx.x, lane = tid % WAVE, gq = lane / 16, c = lane % 16;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform: tile choices are scalar
+  const size_t krow0 = (size_t)g * p.ctx * HD;
+  const size_t vrow0 = (size_t)g * HD * p.ctx_pad;
 
-  // Stage 1 loads: the first K/V tile, the raw q (and new k) vectors, their
-  // norm weights and the rotation of position P.
-  dma_kv<HD, B16>(kb, vb, s0, min(kDecTile, s1 - s0), tiles, tiles + L::KT);
+  // Prologue loads, in the order they are needed: the raw q (and new k)
+  // vectors, norm weights and the rotation of position P; the new value;
+  // then the first two tiles of operands. Out-of-range vector loads read a
+  // valid element and are discarded.
   const float* cs = p.rope + (size_t)P * HD;
-  const int nvec = G + (has_new ? 1 : 0);
   const int hp = lane * p.pair_stride;
-  // Loads are unconditional (out-of-range ones read a valid element and are
-  // discarded), so that the compiler issues them all before the first use.
-  float xv[MAXV][PER], wv[MAXV][PER], fr[MAXV], fi[MAXV];
   const int hq = hp < p.pair_bound ? hp : 0;
+  float xv[MAXV][PER], wv[MAXV][PER], fr[MAXV], fi[MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; j++) {
     const int v = wave + j * NW;
@@ -684,166 +680,259 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
     fr[j] = cs[hq];
     fi[j] = cs[hq + p.pair_offset];
   }
+  float vraw = 0.0f;
+  if (has_new && tid < HD) vraw = cache_at<B16>(p.vcache, ((size_t)g * p.ctx + P) * HD + tid);
+
+  // Tile operands, straight from HBM into registers in the MFMA operand
+  // layouts (buffer loads: 32-bit offsets from the kv head's plane base).
+  // A wave holds up to TPW tiles at once; its first TPW tiles are requested
+  // here, before the queries are processed, the rest a round at a time.
+  struct Regs {
+    bf16x8 kh[2][NKK], kl[2][NKK], vh[DJ], vl[DJ];
+  };
+  const unsigned kbytes = (unsigned)((size_t)p.ctx * HD * 2), vbytes = (unsigned)((size_t)HD * p.ctx_pad * 2);
+  const __amdgpu_buffer_rsrc_t rkh = __builtin_amdgcn_make_buffer_rsrc((void*)(p.khi + krow0), 0, kbytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rkl = __builtin_amdgcn_make_buffer_rsrc((void*)(p.klo + krow0), 0, kbytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rvh = __builtin_amdgcn_make_buffer_rsrc((void*)(p.vthi + vrow0), 0, vbytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rvl = __builtin_amdgcn_make_buffer_rsrc((void*)(p.vtlo + vrow0), 0, vbytes, kRsrcWord3);
+  auto ld = [](__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  };
+  auto load = [&](int it, Regs& r) {
+    const int key0 = it * kD2Tile;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      const int key = min(key0 + 8 * (c >> 2) + 4 * s + (c & 3), P);  // rows past P: masked
+#pragma unroll
+      for (int kk = 0; kk < NKK; kk++) {
+        const int d = 32 * kk + 8 * gq;
+        if (HD >= 32 || d < HD) {  // head_dim 16: dims 16..31 of the k-step are zero
+          const unsigned off = (unsigned)(key * HD + d) * 2u;
+          r.kh[s][kk] = ld(rkh, off);
+          if (!B16) r.kl[s][kk] = ld(rkl, off);
+        } else {
+          r.kh[s][kk] = bf16x8{};
+          r.kl[s][kk] = bf16x8{};
+        }
+      }
+    }
+#pragma unroll
+    for (int dj = 0; dj < DJ; dj++) {  // key0 + 32 <= ctx_pad
+      const unsigned off = (unsigned)((16 * dj + c) * p.ctx_pad + key0 + 8 * gq) * 2u;
+      r.vh[dj] = ld(rvh, off);
+      if (!B16) r.vl[dj] = ld(rvl, off);
+    }
+  };
+  constexpr int TPW = kD2Tpw<B16>;
+  const int first = t0 + wave;                                 // tiles first, first + 4, ...
+  const int cnt = first < t1 ? (t1 - first + NW - 1) / NW : 0;  // of this wave
+  Regs r[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; j++)
+    if (j < cnt) load(first + j * NW, r[j]);
+
 #pragma unroll
   for (int j = 0; j < MAXV; j++) {
     const int v = wave + j * NW;
-    if (v == G)  // this step's key, rounded as the cache will hold it
+    if (v == G)  // this step's key, rounded as a bf16 cache holds it
       norm_rope_regs<HD, B16>(xv[j], wv[j], p.kn != nullptr, p.eps, fr[j], fi[j], p.pair_bound,
                               p.pair_offset, p.pair_stride, kn);
-    else if (v < nvec)
+    else if (v < G)
       norm_rope_regs<HD>(xv[j], wv[j], p.qn != nullptr, p.eps, fr[j], fi[j], p.pair_bound, p.pair_offset,
                          p.pair_stride, qs + v * HD);
   }
+  if (has_new && tid < HD) vn[tid] = vraw;
+  __syncthreads();
 
-  const float scale = sqrtf((float)HD);
-  const int kl = lane % 32, half = lane / 32;
-  const bool active = wave * GW < G;  // waves past the group idle (G < 4)
-  float q[GW][HALF], m[GW], l[GW], acc[GW][DPL];
+  // B operands (dims 32 kk + 8 gq .. + 7 of a head): column c < 8 holds
+  // head c's hi part, column c + 8 its lo part (qb); qb2 the hi parts only
+  // (for the K lo plane). Columns of heads >= G are zero.
+  const int hc = c & 7;
+  const bool lo_col = c >= 8;
+  bf16x8 qb[NKK], qb2[NKK];
 #pragma unroll
-  for (int j = 0; j < GW; j++) {
-    m[j] = -INFINITY;
-    l[j] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < DPL; d++) acc[j][d] = 0.0f;
-  }
-
-  for (int t0 = s0, buf = 0; t0 < s1; t0 += kDecTile, buf ^= 1) {
-    const int n = min(kDecTile, s1 - t0);
-    const float* kt = tiles + buf * (L::KT + L::VT);
-    const float* vt = kt + L::KT;
-    __builtin_amdgcn_s_waitcnt(0);  // this tile (and the q/k loads) landed
-    __syncthreads();                // ... for every wave; previous tile consumed
-    if (t0 + kDecTile < s1) {
-      float* nk = tiles + (buf ^ 1) * (L::KT + L::VT);
-      dma_kv<HD, B16>(kb, vb, t0 + kDecTile, min(kDecTile, s1 - t0 - kDecTile), nk, nk + L::KT);
-    }
-    if (!active) continue;
-    if (t0 == s0) {  // this wave's queries, the lane's half of each
-#pragma unroll
-      for (int j = 0; j < GW; j++) {
-        const int h = min(wave * GW + j, G - 1);
-#pragma unroll
-        for (int i = 0; i < HALF; i += 4) {
-          const float4 f = *(const float4*)(qs + h * HD + half * HALF + i);
-          q[j][i] = f.x;
-          q[j][i + 1] = f.y;
-          q[j][i + 2] = f.z;
-          q[j][i + 3] = f.w;
-        }
-      }
-    }
-    // scores: key t0 + kl, dims [half * HALF, (half + 1) * HALF)
-    const bool valid = kl < n;
-    const bool is_new = has_new && t0 + kl == P;
-    float s[GW];
-#pragma unroll
-    for (int j = 0; j < GW; j++) s[j] = 0.0f;
-    float4 kv[HALF / 4];  // every read of the row issued before the first product
-    if (!B16 || is_new) {
-      const float* krow = (is_new ? kn : kt + kl * L::KROW) + half * HALF;
-#pragma unroll
-      for (int i = 0; i < HALF / 4; i++) kv[i] = *(const float4*)(krow + 4 * i);
+  for (int kk = 0; kk < NKK; kk++) {
+    const int d = 32 * kk + 8 * gq;
+    float x[8];
+    if (hc < G && (HD >= 32 || d < HD)) {
+      const f32x4 a = *(const f32x4*)(qs + hc * HD + d), b = *(const f32x4*)(qs + hc * HD + d + 4);
+      x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3]; x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
     } else {
-      typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
-      const u32x4v* krow = (const u32x4v*)((const uint16_t*)(kt + kl * L::KROW) + half * HALF);
 #pragma unroll
-      for (int i = 0; i < HALF / 8; i++) {
-        const u32x4v u = krow[i];
-        kv[2 * i] = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u),
-                                __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xFFFF0000u));
-        kv[2 * i + 1] = make_float4(__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xFFFF0000u),
-                                    __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xFFFF0000u));
-      }
+      for (int e = 0; e < 8; e++) x[e] = 0.0f;
     }
+    bf16x8 h, lo;
+    split8v(x, h, lo);
+    qb[kk] = lo_col ? lo : h;
+    qb2[kk] = lo_col ? bf16x8{} : h;
+  }
+
+  const float sl2 = 1.44269504088896341f / sqrtf((float)HD);
+  float m = -INFINITY, l = 0.0f;
+  f32x4 o[DJ];
 #pragma unroll
-    for (int i = 0; i < HALF / 4; i++) {
+  for (int dj = 0; dj < DJ; dj++) o[dj] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // The last tile's operands get key P (K row, V^T column) and zeros for
+  // the V^T entries of keys past P.
+  auto patch = [&](Regs& r, int key0) {
 #pragma unroll
-      for (int j = 0; j < GW; j++) {
-        s[j] = fmaf(q[j][4 * i], kv[i].x, s[j]);
-        s[j] = fmaf(q[j][4 * i + 1], kv[i].y, s[j]);
-        s[j] = fmaf(q[j][4 * i + 2], kv[i].z, s[j]);
-        s[j] = fmaf(q[j][4 * i + 3], kv[i].w, s[j]);
-      }
-    }
-    float pr[GW];
+    for (int s = 0; s < 2; s++) {
+      if (key0 + 8 * (c >> 2) + 4 * s + (c & 3) == P) {
 #pragma unroll
-    for (int j = 0; j < GW; j++) {
-      const float full = s[j] + __shfl_xor(s[j], 32, WAVE);  // the same sum in both halves
-      const float sc = valid ? full / scale : -INFINITY;
-      const float mn = fmaxf(m[j], wave_peak(sc));
-      const float e = valid ? expf(sc - mn) : 0.0f;
-      const float f = expf(m[j] - mn);
-      l[j] = l[j] * f + wave_total(half == 0 ? e : 0.0f);
-      m[j] = mn;
+        for (int kk = 0; kk < NKK; kk++) {
+          const int d = 32 * kk + 8 * gq;
+          if (HD >= 32 || d < HD) {
+            float x[8];
 #pragma unroll
-      for (int d = 0; d < DPL; d++) acc[j][d] *= f;
-      pr[j] = e;
-    }
-    // P.V: dims lane * DPL .. + DPL (lanes past HD use the last dims and
-    // never store), 8 keys per batch with all their reads in flight; keys
-    // past n read row n - 1 (finite data) with probability 0.
-    const int dd = min(lane * DPL, HD - DPL);
-    for (int k0 = 0; k0 < n; k0 += 8) {
-      float v[8][DPL];
-#pragma unroll
-      for (int kk = 0; kk < 8; kk++) {
-        if constexpr (B16) {
-          const uint16_t* vr = (const uint16_t*)vt + min(k0 + kk, n - 1) * HD + dd;
-          if constexpr (DPL == 2) {
-            const uint32_t u = *(const uint32_t*)vr;
-            v[kk][0] = __uint_as_float(u << 16);
-            v[kk][1] = __uint_as_float(u & 0xFFFF0000u);
-          } else {
-#pragma unroll
-            for (int d = 0; d < DPL; d++) v[kk][d] = bf16_to_f32(vr[d]);
+            for (int e = 0; e < 8; e++) x[e] = kn[d + e];
+            split8v(x, r.kh[s][kk], r.kl[s][kk]);
           }
-          continue;
-        }
-        const float* vr = vt + min(k0 + kk, n - 1) * HD + dd;
-        if constexpr (DPL == 2) {
-          const float2 f = *(const float2*)vr;
-          v[kk][0] = f.x;
-          v[kk][1] = f.y;
-        } else {
-#pragma unroll
-          for (int d = 0; d < DPL; d++) v[kk][d] = vr[d];
-        }
-      }
-#pragma unroll
-      for (int kk = 0; kk < 8; kk++) {
-#pragma unroll
-        for (int j = 0; j < GW; j++) {
-          const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[j]), k0 + kk));
-#pragma unroll
-          for (int d = 0; d < DPL; d++) acc[j][d] = fmaf(pk, v[kk][d], acc[j][d]);
         }
       }
     }
-  }
-  if (active) {
+    const int at = P - key0 - 8 * gq;  // the lane's V^T element holding key P
+    if (at < 8) {  // key P or keys past it among the lane's eight
+      typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 #pragma unroll
-    for (int j = 0; j < GW; j++) {
-      const int h = wave * GW + j;
-      if (h < G) {
-        float* part = p.partial + ((size_t)(g * G + h) * p.splits + c) * (HD + 2);
-        if (lane * DPL < HD) {
+      for (int dj = 0; dj < DJ; dj++) {
+        u16x8 h = __builtin_bit_cast(u16x8, r.vh[dj]), lo = __builtin_bit_cast(u16x8, r.vl[dj]);
+        uint32_t nh, nl;
+        split2(vn[16 * dj + c], 0.0f, nh, nl);
 #pragma unroll
-          for (int d = 0; d < DPL; d++) cstore(part + 2 + lane * DPL + d, acc[j][d]);
+        for (int e = 0; e < 8; e++) {
+          h[e] = e < at ? h[e] : e == at ? (unsigned short)nh : (unsigned short)0;
+          lo[e] = e < at ? lo[e] : e == at ? (unsigned short)nl : (unsigned short)0;
         }
-        if (lane == 0) {
-          cstore(part, m[j]);
-          cstore(part + 1, l[j]);
-        }
+        r.vh[dj] = __builtin_bit_cast(bf16x8, h);
+        r.vl[dj] = __builtin_bit_cast(bf16x8, lo);
       }
     }
+  };
+
+  auto step = [&](Regs& r, int it) {
+    const int key0 = it * kD2Tile;
+    if (it == nt - 1) patch(r, key0);
+    // column c: kh.qh + kl.qh (c < 8) or kh.ql (c >= 8); columns c and
+    // c ^ 8 summed (a rotation by 8 within each row of 16 lanes) give the
+    // score of head c & 7 in both
+    f32x4 sc[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      sc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NKK; kk++) {
+        sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.kh[s][kk], qb[kk], sc[s], 0, 0, 0);
+        if (!B16) sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.kl[s][kk], qb2[kk], sc[s], 0, 0, 0);
+      }
+    }
+    float pv[8];
+    float mx = -INFINITY;
+    const bool full = key0 + kD2Tile - 1 <= P;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float x = sc[j >> 2][j & 3];
+      const float sum = (x + dpp_ror8(x)) * sl2;  // every lane (the DPP reads lane c ^ 8)
+      const float v = full || key0 + 8 * gq + j <= P ? sum : -INFINITY;
+      pv[j] = v;
+      mx = fmaxf(mx, v);
+    }
+    mx = fmaxf(mx, xor16_max(mx));
+    mx = fmaxf(mx, xor32_max(mx));
+    const float mn = fmaxf(m, mx);  // finite: key key0 <= P is in every tile
+    const float corr = __builtin_amdgcn_exp2f(m - mn);
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float e = __builtin_amdgcn_exp2f(pv[j] - mn);
+      pv[j] = e;
+      rs += e;
+    }
+    rs = xor16_sum(rs);
+    rs = xor32_sum(rs);
+    l = l * corr + rs;
+    m = mn;
+    // P^T columns as the queries': hi in c < 8, lo in c >= 8 (pb), hi only
+    // for the V lo plane (pb2); column c ^ 8 is folded in after the loop
+    bf16x8 ph, pl;
+    split8v(pv, ph, pl);
+    const bf16x8 pb = lo_col ? pl : ph, pb2 = lo_col ? bf16x8{} : ph;
+#pragma unroll
+    for (int dj = 0; dj < DJ; dj++) {
+      o[dj] *= corr;
+      o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.vh[dj], pb, o[dj], 0, 0, 0);
+      if (!B16) o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.vl[dj], pb2, o[dj], 0, 0, 0);
+    }
+  };
+
+  for (int b = 0; b < cnt; b += TPW) {
+    if (b > 0) {
+#pragma unroll
+      for (int j = 0; j < TPW; j++)
+        if (b + j < cnt) load(first + (b + j) * NW, r[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < TPW; j++)
+      if (b + j < cnt) step(r[j], first + (b + j) * NW);
   }
-  if (has_new) {  // cache row P of kv head g, read by later steps
-    const size_t at = ((size_t)g * p.ctx + P) * HD;
-    for (int e = tid; e < HD; e += kDecThreads) {
-      if (B16) ((uint16_t*)p.kcache_w)[at + e] = f32_to_bf16_any(kn[e]);  // exact: kn is rounded
-      else p.kcache_w[at + e] = kn[e];
+
+  // Merge the waves (a wave without tiles has m = -inf, l = 0, o = 0);
+  // head c's output is the sum of columns c and c + 8.
+#pragma unroll
+  for (int dj = 0; dj < DJ; dj++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[dj][e] += dpp_ror8(o[dj][e]);
+  if (c < G) {
+#pragma unroll
+    for (int dj = 0; dj < DJ; dj++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) mo[wave][c][16 * dj + 4 * gq + e] = o[dj][e];
+    if (gq == 0) {
+      ml[wave][c][0] = m;
+      ml[wave][c][1] = l;
     }
   }
+  __syncthreads();
+  for (int i = tid; i < G * HD; i += kDecThreads) {
+    const int h = i / HD, d = i % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; w++) M = fmaxf(M, ml[w][h][0]);
+    float O = 0.0f, Lb = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      const float f = __builtin_amdgcn_exp2f(ml[w][h][0] - M);
+      O = fmaf(f, mo[w][h][d], O);
+      Lb = fmaf(f, ml[w][h][1], Lb);
+    }
+    if (nb == 1) {  // the whole context: the block's result is the output
+      p.out[(size_t)(g * G + h) * HD + d] = O / Lb;
+      continue;
+    }
+    float* part = p.partial + ((size_t)(g * G + h) * p.splits + blk) * (HD + 2);
+    cstore(part + 2 + d, O);
+    if (d == 0) {
+      cstore(part, M);
+      cstore(part + 1, Lb);
+    }
+  }
+  if (has_new && tid < HD) {  // row P of the cache and its planes, read by later steps
+    const size_t at = ((size_t)g * p.ctx + P) * HD + tid;
+    const float k = kn[tid], v = vn[tid];
+    if (B16) ((uint16_t*)p.kcache_w)[at] = f32_to_bf16_any(k);  // exact: kn is rounded
+    else p.kcache_w[at] = k;
+    uint32_t hk, lk, hv, lv;
+    split2(k, 0.0f, hk, lk);
+    split2(v, 0.0f, hv, lv);
+    // the planes are this kernel's operands (read-only above); row P is
+    // read by no block of this launch
+    ((uint16_t*)p.khi)[at] = (uint16_t)hk;
+    ((uint16_t*)p.klo)[at] = (uint16_t)lk;
+    const size_t vt = vrow0 + (size_t)tid * p.ctx_pad + P;
+    ((uint16_t*)p.vthi)[vt] = (uint16_t)hv;
+    ((uint16_t*)p.vtlo)[vt] = (uint16_t)lv;
+  }
+  if (nb == 1) return;
   // Hand-off to the combining block. Partials are written and read only by
   // agent-scope relaxed atomic accesses (sc1: written through to, and read
   // from, the agent's coherence point, never from a non-coherent L2 line),
@@ -858,19 +947,23 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
   if (tid == 0) {
     const unsigned done = __hip_atomic_fetch_add(p.counters + g, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
-    flag[0] = done == (unsigned)(nch - 1);
+    flag = done == (unsigned)(nb - 1);
   }
   __syncthreads();
-  if (!flag[0]) return;
+  if (!flag) return;
 
-  // Last block of kv head g: wave w combines heads w*GW.., lane c holding
-  // chunk c's weight. Every chunk partial of the lane's output dims (of all
-  // the wave's heads when they fit in registers) is loaded before the first
-  // is used, 8 chunks per batch up to nch, then summed in chunk order.
-  constexpr int CB = 8;                          // chunks per load batch
-  constexpr int HB = GW * DPL <= 2 ? GW : 1;     // heads loaded together
+  // Last block of kv head g: wave w combines heads w*GW .., lane c holding
+  // block c's weight (scores in base 2). Every block partial of the lane's
+  // output dims (of all the wave's heads when they fit in registers) is
+  // loaded before the first is used, 8 blocks per batch up to nb, then
+  // summed in block order:
+  //   att = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c,  M = max_c m_c,
+  // and the counter is reset for the next launch.
+  constexpr int DPL = HD >= WAVE ? HD / WAVE : 1;
+  constexpr int CB = 8;
+  constexpr int HB = GW * DPL <= 2 ? GW : 1;
   const int dd = min(lane * DPL, HD - DPL);
-  const bool ok = lane < nch;
+  const bool ok = lane < nb;
 #pragma unroll
   for (int j0 = 0; j0 < GW; j0 += HB) {
     if (wave * GW + j0 >= G) break;
@@ -886,12 +979,12 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
       const float* base = p.partial + (size_t)(g * G + min(wave * GW + j0 + j, G - 1)) * p.splits * (HD + 2);
 #pragma unroll
       for (int b = 0; b < kDecMaxChunks / CB; b++) {
-        if (b * CB < nch) {
+        if (b * CB < nb) {
 #pragma unroll
           for (int i = 0; i < CB; i++) {
-            const float* src = base + (size_t)min(b * CB + i, nch - 1) * (HD + 2) + 2 + dd;
+            const float* src = base + (size_t)min(b * CB + i, nb - 1) * (HD + 2) + 2 + dd;
             if constexpr (DPL == 2) {
-              const float2 f = cload2(src);  // 8-byte aligned: HD + 2 and dd are even
+              const float2 f = cload2(src);
               x[j][b * CB + i][0] = f.x;
               x[j][b * CB + i][1] = f.y;
             } else {
@@ -907,25 +1000,25 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
       const int h = wave * GW + j0 + j;
       if (h >= G) break;
       const float M = wave_peak(mc[j]);
-      const float w = ok ? expf(mc[j] - M) : 0.0f;
+      const float w = ok ? __builtin_amdgcn_exp2f(mc[j] - M) : 0.0f;
       const float W = wave_total(w * lc[j]);
-      float o[DPL];
+      float oo[DPL];
 #pragma unroll
-      for (int d = 0; d < DPL; d++) o[d] = 0.0f;
+      for (int d = 0; d < DPL; d++) oo[d] = 0.0f;
 #pragma unroll
       for (int b = 0; b < kDecMaxChunks / CB; b++) {
-        if (b * CB < nch) {
+        if (b * CB < nb) {
 #pragma unroll
           for (int i = 0; i < CB; i++) {
-            const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b * CB + i));  // 0 past nch
+            const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b * CB + i));
 #pragma unroll
-            for (int d = 0; d < DPL; d++) o[d] = fmaf(wc, x[j][b * CB + i][d], o[d]);
+            for (int d = 0; d < DPL; d++) oo[d] = fmaf(wc, x[j][b * CB + i][d], oo[d]);
           }
         }
       }
       if (lane * DPL < HD) {
 #pragma unroll
-        for (int d = 0; d < DPL; d++) p.out[(size_t)(g * G + h) * HD + lane * DPL + d] = o[d] / W;
+        for (int d = 0; d < DPL; d++) p.out[(size_t)(g * G + h) * HD + lane * DPL + d] = oo[d] / W;
       }
     }
   }
@@ -934,9 +1027,10 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(1, 
 
 }  // namespace
 
-// Chunks per kv head: up to 512 blocks (two per CU fit at once).
+// Blocks per kv head, at most: up to 256 blocks, one per CU (a block holds
+// each SIMD's register file), and at most one combine lane each.
 int attention_decode_chunks(int kv_heads) {
-  return std::max(1, std::min(kDecMaxChunks, 512 / std::max(1, kv_heads)));
+  return std::max(1, std::min(kDecMaxChunks, 256 / std::max(1, kv_heads)));
 }
 
 void attention_init() {
@@ -957,22 +1051,6 @@ void attention_init() {
   X3_ATTR(64)
   X3_ATTR(128)
 #undef X3_ATTR
-#define DECODE_ATTR(HD, GW)                                                                     \
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<HD, GW, false>,                 \
-                                hipFuncAttributeMaxDynamicSharedMemorySize,                     \
-                                (int)(DecLds<HD>::total * sizeof(float))));                     \
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_decode_kernel<HD, GW, true>,                  \
-                                hipFuncAttributeMaxDynamicSharedMemorySize,                     \
-                                (int)(DecLds<HD, true>::total * sizeof(float))));
-  DECODE_ATTR(16, 1)
-  DECODE_ATTR(16, 2)
-  DECODE_ATTR(32, 1)
-  DECODE_ATTR(32, 2)
-  DECODE_ATTR(64, 1)
-  DECODE_ATTR(64, 2)
-  DECODE_ATTR(128, 1)
-  DECODE_ATTR(128, 2)
-#undef DECODE_ATTR
 }
 
 // STRASGPT_PREFILL_ATTN=fp32 selects the fp32 matrix-core kernel; the
@@ -1048,33 +1126,33 @@ void attention_decode(const AttnParams& p, hipStream_t s) {
   if (G > kDecMaxG) ST_DIE("decode attention supports at most 8 query heads per kv head");
   if (p.splits < 1 || p.splits > kDecMaxChunks) ST_DIE("decode attention chunk count out of range");
   if (!p.counters || !p.partial) ST_DIE("decode attention needs its partial buffer and counters");
+  if (!p.khi || !p.klo || !p.vthi || !p.vtlo || p.ctx_pad % 32 || p.ctx_pad < p.ctx)
+    ST_DIE("decode attention needs the cache's bf16 planes");
   if (p.pair_stride < 1 || (p.pair_bound + p.pair_stride - 1) / p.pair_stride > WAVE ||
       p.pair_bound - p.pair_stride + p.pair_offset >= p.hd)
     ST_DIE("decode attention: RoPE pairs must fit one per lane within the head");
   const dim3 grid(p.splits, p.kv_heads);
-  const bool two = G > kDecThreads / WAVE;  // two query heads per wave
+  const bool two = G > kDecThreads / WAVE;  // the combine: two query heads per wave
   switch (p.hd) {
-#define DECODE_LAUNCH(HD, GW)                                                                 \
-  if (p.kv_bf16)                                                                              \
-    hipLaunchKernelGGL((attn_decode_kernel<HD, GW, true>), grid, dim3(kDecThreads),           \
-                       (DecLds<HD, true>::total * sizeof(float)), s, p);                      \
-  else                                                                                        \
-    hipLaunchKernelGGL((attn_decode_kernel<HD, GW, false>), grid, dim3(kDecThreads),          \
-                       DecLds<HD>::total * sizeof(float), s, p);
-#define DECODE_CASE(HD)     \
-  case HD:                  \
-    if (two) {              \
-      DECODE_LAUNCH(HD, 2)  \
-    } else {                \
-      DECODE_LAUNCH(HD, 1)  \
-    }                       \
+#define DECODE2_LAUNCH(HD, GW)                                                                     \
+  if (p.kv_bf16)                                                                                   \
+    hipLaunchKernelGGL((attn_decode_mfma_kernel<HD, GW, true>), grid, dim3(kDecThreads), 0, s, p); \
+  else                                                                                             \
+    hipLaunchKernelGGL((attn_decode_mfma_kernel<HD, GW, false>), grid, dim3(kDecThreads), 0, s, p);
+#define DECODE2_CASE(HD)     \
+  case HD:                   \
+    if (two) {               \
+      DECODE2_LAUNCH(HD, 2)  \
+    } else {                 \
+      DECODE2_LAUNCH(HD, 1)  \
+    }                        \
     break;
-    DECODE_CASE(16)
-    DECODE_CASE(32)
-    DECODE_CASE(64)
-    DECODE_CASE(128)
-#undef DECODE_CASE
-#undef DECODE_LAUNCH
+    DECODE2_CASE(16)
+    DECODE2_CASE(32)
+    DECODE2_CASE(64)
+    DECODE2_CASE(128)
+#undef DECODE2_CASE
+#undef DECODE2_LAUNCH
     default: ST_DIE("attention supports head_dim 16, 32, 64 or 128");
   }
   HIP_CHECK(hipGetLastError());

@@ -179,15 +179,16 @@ struct AttnParams {
   float eps;
   const float* rope;
   int pair_bound, pair_offset, pair_stride;
-  // prefill, split-bf16 kernel: the layer's cache rows as bf16 planes,
-  // K [kv_heads][ctx][hd] (hi, lo) and V transposed [kv_heads][hd][ctx_pad]
+  // the layer's cache rows as bf16 planes (the split-bf16 prefill kernel's
+  // and the decode kernel's operands), K [kv_heads][ctx][hd] (hi, lo) and
+  // V transposed [kv_heads][hd][ctx_pad]; decode writes row P into them
   const uint16_t* khi;
   const uint16_t* klo;
   const uint16_t* vthi;
   const uint16_t* vtlo;
   int ctx_pad;           // ctx rounded up to a multiple of 32
   float* partial;        // [q_heads][splits][hd + 2]
-  int splits;            // key chunks per kv head, at most (attention_decode_chunks)
+  int splits;            // decode: blocks per kv head, at most (attention_decode_chunks)
   unsigned* counters;    // [kv_heads], zero between launches
 };
 void attention_prefill(const AttnParams& p, hipStream_t s);

@@ -147,12 +147,11 @@ struct transformer_device {
   // [chunk][kvd] fp32 until their norm and RoPE
   int kv_bf16 = 0;
   float* kstage = nullptr;
-  // The cache rows as bf16 hi/lo planes for the split-bf16 prefill
-  // attention: K [L][kvh][ctx][hd], V transposed [L][kvh][hd][ctx_pad];
-  // zero-initialised, rows [0, split_pos) converted (every layer).
+  // The cache rows as bf16 hi/lo planes, the operands of the attention
+  // kernels: K [L][kvh][ctx][hd], V transposed [L][kvh][hd][ctx_pad];
+  // zero-initialised; rows [0, cached_count) valid (every layer).
   uint16_t *kp_hi = nullptr, *kp_lo = nullptr, *vt_hi = nullptr, *vt_lo = nullptr;
   int ctx_pad = 0;
-  size_t split_pos = 0;
   int *tok = nullptr, *pos = nullptr, *next = nullptr, *seq = nullptr, *seq_len = nullptr;
   int seq_cap = 0;
   float* attn_part = nullptr;
@@ -530,6 +529,15 @@ void layer_decode(Dev* D, int l) {
   a.pair_bound = D->pb;
   a.pair_offset = D->po;
   a.pair_stride = D->pst;
+  {
+    const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
+    const size_t vt_layer = (size_t)D->kvh * D->hd * D->ctx_pad;
+    a.khi = D->kp_hi + l * cache_layer;
+    a.klo = D->kp_lo + l * cache_layer;
+    a.vthi = D->vt_hi + l * vt_layer;
+    a.vtlo = D->vt_lo + l * vt_layer;
+    a.ctx_pad = D->ctx_pad;
+  }
   a.partial = D->attn_part;
   a.splits = D->attn_splits;
   a.counters = D->attn_cnt;
@@ -683,18 +691,17 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
                      D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
                      D->po, D->pst, D->kv_bf16 ? D->kstage : nullptr, s);
   }
-  // cache rows not yet in the bf16 planes: this chunk's, and any written by
-  // decode steps since the last prefill (from a multiple of 32)
+  // this chunk's cache rows into the bf16 planes (from a multiple of 32;
+  // decode steps write their rows into the planes themselves)
   const size_t P0 = D->host_pos;
   const size_t vt_layer = (size_t)D->kvh * D->hd * D->ctx_pad;
   {
-    const int r0 = (int)(std::min(D->split_pos, P0) / 32 * 32), r1 = (int)(P0 + T);
+    const int r0 = (int)(P0 / 32 * 32), r1 = (int)(P0 + T);
     Prof pr(D, K_ELEM, 2.0 * (r1 - r0) * D->kvd * 4 * 2, 0);
     sg::attention_split_rows(kc, vc, D->kp_hi + l * cache_layer, D->kp_lo + l * cache_layer,
                              D->vt_hi + l * vt_layer, D->vt_lo + l * vt_layer, D->kvh, D->ctx,
                              D->ctx_pad, D->hd, r0, r1, D->kv_bf16, s);
   }
-  if (l == D->L - 1) D->split_pos = P0 + T;
   sg::AttnParams a{};
   a.q = D->q;
   a.kcache = kc;
@@ -1416,12 +1423,10 @@ extern "C" size_t sg_generate_sampled(transformer_t* t, size_t T, const int* tok
   return produced;
 }
 
-// The bf16 planes of the cache (prefill attention) are valid for rows
-// [0, split_pos) of the current sequence only: a new sequence starts with
-// none converted.
+// The bf16 planes of the cache hold rows [0, cached_count) of the current
+// sequence (prefill chunks and decode steps write them).
 extern "C" void sg_reset(transformer_t* t) {
   t->state->cached_count = 0;
-  t->device->split_pos = 0;
 }
 
 extern "C" void sg_capture_hidden(transformer_t* t, float* out, float* out_final) {
@@ -1466,7 +1471,6 @@ extern "C" int sg_set_kv_cache_format(transformer_t* t, int format) {
   alloc_kv(D, (size_t)D->L * D->kvh * D->ctx * D->hd);
   t->state->k_cache = D->kc;
   t->state->v_cache = D->vc;
-  D->split_pos = 0;
   HIP_CHECK(hipStreamSynchronize(D->stream));
   return old;
 }
