@@ -19,6 +19,13 @@ extern "C" {
 int strasgpt_kbench_mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks,
                                  float* out);
 
+/* The same blocks through the grouped prefill GEMM's conversion (MXFP4 to
+ * packed bf16 pairs, as it fills the matrix-core tiles), widened back to
+ * fp32: equal to the fp32 decode wherever the value fits bf16 (all of them:
+ * two significant bits). */
+int strasgpt_kbench_mxfp4_decode_bf16(const uint8_t* codes, const uint8_t* scales, int nblocks,
+                                      float* out);
+
 /* Copy of `bytes` (multiple of 16) between two device buffers: one warm-up
  * launch of copy_probe_kernel (reads and writes exactly `bytes`), then
  * `iters` launches back to back between two events; *avg_us is the average

@@ -134,8 +134,8 @@ extern "C" int strasgpt_kbench_mfma(int random_operands, int waves_per_simd, int
   return 0;
 }
 
-extern "C" int strasgpt_kbench_mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks,
-                                            float* out) {
+static int mxfp4_decode_hook(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out,
+                             int bf16_tiles) {
   if (nblocks <= 0 || !codes || !scales || !out) return -1;
   uint8_t *dc, *ds;
   float* dout;
@@ -144,10 +144,20 @@ extern "C" int strasgpt_kbench_mxfp4_decode(const uint8_t* codes, const uint8_t*
   HIP_CHECK(hipMalloc(&dout, (size_t)nblocks * 32 * sizeof(float)));
   HIP_CHECK(hipMemcpy(dc, codes, (size_t)nblocks * 16, hipMemcpyHostToDevice));
   HIP_CHECK(hipMemcpy(ds, scales, (size_t)nblocks, hipMemcpyHostToDevice));
-  sg::mxfp4_decode(dc, ds, nblocks, dout, 0);
+  sg::mxfp4_decode(dc, ds, nblocks, dout, bf16_tiles, 0);
   HIP_CHECK(hipMemcpy(out, dout, (size_t)nblocks * 32 * sizeof(float), hipMemcpyDeviceToHost));
   HIP_CHECK(hipFree(dc));
   HIP_CHECK(hipFree(ds));
   HIP_CHECK(hipFree(dout));
   return 0;
+}
+
+extern "C" int strasgpt_kbench_mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks,
+                                            float* out) {
+  return mxfp4_decode_hook(codes, scales, nblocks, out, 0);
+}
+
+extern "C" int strasgpt_kbench_mxfp4_decode_bf16(const uint8_t* codes, const uint8_t* scales, int nblocks,
+                                                 float* out) {
+  return mxfp4_decode_hook(codes, scales, nblocks, out, 1);
 }

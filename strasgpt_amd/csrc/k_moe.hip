@@ -38,6 +38,21 @@ __device__ __forceinline__ float2v fp4_pair(uint32_t w, float sc) {
   return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, sc, B);
 }
 
+// A 32-value block (four code words) times `sc` as 16 packed bf16 pairs,
+// element 2j in the low half of o[j]: one conversion per pair, exact (an
+// E2M1 value times a power of two has at most two significant bits, inside
+// bf16's exponent range, subnormals included).
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void fp4_block_bf16(const uint32_t (&w)[4], float sc, uint32_t (&o)[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    o[4 * i + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[i], sc, 0));
+    o[4 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[i], sc, 1));
+    o[4 * i + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[i], sc, 2));
+    o[4 * i + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[i], sc, 3));
+  }
+}
+
 // Activation rows in LDS: rows of K values back to back, each 32-value
 // block (8 chunks of 16 bytes) with chunk c stored at position c ^ (b & 7)
 // of block b. Lanes that take consecutive blocks then read the same
@@ -550,13 +565,24 @@ __global__ __launch_bounds__(kThreads) void down_kernel(MoeGemvParams p) {
 }
 
 // The decode of mx_block_dot, written out: out[32 b + i] = value i of block b.
-__global__ void mxfp4_decode_kernel(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out) {
+__global__ void mxfp4_decode_kernel(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out,
+                                    int bf16_tiles) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblocks) return;
   const uint4 q = *(const uint4*)(codes + (size_t)b * 16);
   const float sc = e8m0_scale(scales[b]);
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
   float* o = out + (size_t)b * 32;
+  if (bf16_tiles) {  // the grouped prefill GEMM's conversion, widened back
+    uint32_t t[16];
+    fp4_block_bf16(w, sc, t);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      o[2 * j] = __uint_as_float(t[j] << 16);
+      o[2 * j + 1] = __uint_as_float(t[j] & 0xFFFF0000u);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const float2v v0 = fp4_pair<0>(w[i], sc), v1 = fp4_pair<1>(w[i], sc);
@@ -895,16 +921,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     const float sc = e8m0_scale(ql[QLds::sc + srow + 2 * t + dk]);
     const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
     uint32_t o[16];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float2v v0 = fp4_pair<0>(ww[i], sc), v1 = fp4_pair<1>(ww[i], sc);
-      const float2v v2 = fp4_pair<2>(ww[i], sc), v3 = fp4_pair<3>(ww[i], sc);
-      // exact in bf16 (E2M1 value x power of two): keep the high halves
-      o[4 * i + 0] = (__float_as_uint(v0.x) >> 16) | (__float_as_uint(v0.y) & 0xFFFF0000u);
-      o[4 * i + 1] = (__float_as_uint(v1.x) >> 16) | (__float_as_uint(v1.y) & 0xFFFF0000u);
-      o[4 * i + 2] = (__float_as_uint(v2.x) >> 16) | (__float_as_uint(v2.y) & 0xFFFF0000u);
-      o[4 * i + 3] = (__float_as_uint(v3.x) >> 16) | (__float_as_uint(v3.y) & 0xFFFF0000u);
-    }
+    fp4_block_bf16(ww, sc, o);
     unsigned char* bt = ql + QLds::tile + (t & 1) * QLds::bt + dr * 128;
 #pragma unroll
     for (int c = 0; c < 4; c++)  // logical chunks 4 dk + c (8 values each)
@@ -1082,10 +1099,11 @@ void moe_gemv_swiglu(const MoeGemvParams& p, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
-void mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out, hipStream_t s) {
+void mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out, int bf16_tiles,
+                  hipStream_t s) {
   if (nblocks <= 0 || (uintptr_t)codes % 16) ST_DIE("MXFP4 decode needs aligned blocks");
   hipLaunchKernelGGL(mxfp4_decode_kernel, dim3((nblocks + 255) / 256), dim3(256), 0, s, codes, scales,
-                     nblocks, out);
+                     nblocks, out, bf16_tiles);
   HIP_CHECK(hipGetLastError());
 }
 

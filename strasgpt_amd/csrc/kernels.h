@@ -90,8 +90,10 @@ bool moe_group_gemm2_ok(const MoeGemmParams& p);
 // x[t][n] += sum_j in top-k order fmaf(w[t k + j], out[t k + j][n], .)
 void moe_combine(const float* out, const float* w, int T, int k, int N, float* x, hipStream_t s);
 // The device MXFP4 decode of the expert kernels on `nblocks` blocks of 32
-// values (16 code bytes + 1 E8M0 scale each): out[32 b + i] (test hook).
-void mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out, hipStream_t s);
+// values (16 code bytes + 1 E8M0 scale each): out[32 b + i] (test hook);
+// bf16_tiles: the grouped prefill GEMM's bf16 conversion, widened back.
+void mxfp4_decode(const uint8_t* codes, const uint8_t* scales, int nblocks, float* out, int bf16_tiles,
+                  hipStream_t s);
 
 // ---------------------------------------------------------------- GEMM --
 // C[M][N] = A[M][K] x W[N][K]^T (bf16 weights) on MFMA. A is given as two

@@ -355,11 +355,13 @@ def test_strasgpt_host_loop_openmp_team(model_dir):
         assert "Prompt processing (prefill)" in r.stderr
 
 
-def test_mxfp4_device_decode_exact():
+@pytest.mark.parametrize("hook", ["strasgpt_kbench_mxfp4_decode", "strasgpt_kbench_mxfp4_decode_bf16"])
+def test_mxfp4_device_decode_exact(hook):
     """The expert kernels' device MXFP4 decode (hardware E2M1 conversion
-    scaled by the E8M0 exponent) equals the oracle's dequantisation bit for
-    bit on every (code, scale) pair: 16 codes in both nibble positions x
-    256 scales (scale 255 decodes to NaN in both)."""
+    scaled by the E8M0 exponent: to fp32 pairs in the GEMVs, to packed bf16
+    pairs in the grouped prefill GEMM's tiles) equals the oracle's
+    dequantisation bit for bit on every (code, scale) pair: 16 codes in both
+    nibble positions x 256 scales (scale 255 decodes to NaN in both)."""
     import ctypes
     from oracle import oracle as orc
     rt = runtime()
@@ -371,7 +373,7 @@ def test_mxfp4_device_decode_exact():
         codes[:, i] = i | ((15 - i) << 4)
     scales = np.arange(256, dtype=np.uint8)
     got = np.zeros(nblocks * 32, np.float32)
-    fn = L.strasgpt_kbench_mxfp4_decode
+    fn = getattr(L, hook)
     fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
     assert fn(codes.ctypes.data, scales.ctypes.data, nblocks, orc.fptr(got)) == 0
     want = np.zeros(nblocks * 32, np.float32)
