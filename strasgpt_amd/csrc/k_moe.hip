@@ -787,21 +787,28 @@ __global__ __launch_bounds__(256) void group_gemm_kernel(MoeGemmParams p) {
 //   to LDS by the global-to-LDS DMA in 128-byte row segments (K steps of
 //   64), 3-stage ring;
 // * the MXFP4 code bytes of the tile's 128 weight rows (gate 64 + up 64, or
-//   128 rows of one matrix, 4 KiB per step) stream through a 3-stage DMA
-//   ring, codes of step t + QNB - QNA + 1 issued with the A rows of step t;
-//   the rows' E8M0 scales are DMA'd once per block;
-// * per step every thread decodes one 32-value block (hardware FP4
-//   conversion, exact in bf16) into the next bf16 B tile while the waves
-//   multiply the current one: 32 slots (experts average about 32 slots per
-//   chunk: 64-slot tiles would be half empty) x 128 rows x 64 K, 16 MFMAs
-//   per wave (2 x 2 waves: 16 slots x 32 output columns of each matrix);
-//   80 KiB of LDS at K = 2880, two blocks per CU (a second wave per SIMD
-//   overlaps each step's decode and LDS round trips).
+//   128 rows of one matrix, 4 KiB per step) go with the A rows of the same
+//   step into the same slot of a 3-stage DMA ring; the rows' E8M0 scales
+//   are DMA'd once per block;
+// * each wave converts the codes of its own weight rows straight into its
+//   MFMA B operands (hardware FP4 conversion to packed bf16 pairs, exact),
+//   so no decoded tile goes through LDS: 32 slots (experts average about 32
+//   slots per chunk: 64-slot tiles would be half empty) x 128 rows x 64 K
+//   per step, 16 MFMAs per wave (each wave: all 32 slots x 16 output
+//   columns of both matrices, or x 32 columns of one); ~50 KiB of LDS at
+//   K = 2880, two blocks per CU.
 // Each step issues exactly QAI A + 1 code DMA instructions per wave
 // (indexes past the last step are clamped to it and never read), so the
 // wait before a step is a constant: the groups of the QNA - 2 later steps
 // may stay in flight.
 constexpr int QBM = 32, QKS = 64, QBR = 128;  // slots, K per step, weight rows per block
+constexpr int kXcds = 8;                      // XCDs of an MI355X (round-robin block dispatch)
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int off = WAVE / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
 constexpr int QNA = 3, QNB = 3;              // A ring, code ring stages
 constexpr int QAI = 2 * QBM * QKS * 2 / 1024 / 4;  // A DMA instructions per wave and step
 constexpr int kQMaxNb = 256;                  // K / 32 <= 256 (scales per row)
@@ -813,12 +820,12 @@ __host__ __device__ constexpr int q_scale_run(int rows, int nb) { return (rows *
 struct QLds {
   static constexpr int a_stage = 2 * QBM * QKS * 2;  // hi + lo rows of 128 bytes
   static constexpr int b_stage = QBR * 32;           // 2 code blocks per row
-  static constexpr int bt = QBR * QKS * 2;           // bf16 B tile
   static constexpr int a = 0;
   static constexpr int b = a + QNA * a_stage;
-  static constexpr int tile = b + QNB * b_stage;
-  static constexpr int sc = tile + 2 * bt;           // scales: QBR rows x nb bytes
+  static constexpr int info = b + QNB * b_stage;     // the tile lookup result
+  static constexpr int sc = info + 1024;             // scales: QBR rows x nb bytes
 };
+static_assert(QNA == QNB, "one ring slot per step for the A rows and the codes");
 
 __device__ __forceinline__ int q_swz(int r) { return (r >> 1) & 7; }  // 128-byte rows
 
@@ -830,45 +837,63 @@ typedef unsigned q_u32x4 __attribute__((ext_vector_type(4)));
 template <bool DUAL>
 __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   // one LDS object (a second one makes the compiler wait for every LDS DMA
-  // before any LDS read); the tile lookup result sits in the B tile area,
-  // which is first written after it has been read
+  // before any LDS read)
   extern __shared__ __attribute__((aligned(1024))) unsigned char ql[];
-  int* tile_info = (int*)(ql + QLds::tile);
+  int* tile_info = (int*)(ql + QLds::info);
   const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
-  const int wm = wave / 2, wn = wave % 2;
+  // Tile of this block. The (slot tile, column tile) grid is laid out per
+  // XCD (blocks are dispatched to the 8 XCDs round-robin by linear id): XCD
+  // x takes a contiguous run of the slot tiles (about an eighth of the
+  // experts) and walks the column tiles in its outer loop, so the A rows of
+  // its tiles stay in its L2 across column tiles and the slot tiles of one
+  // expert, run side by side, share each column tile's codes.
   if (wave == 0) {
-    int e_found = -1, m0 = 0, base = 0;
-    for (int e0 = 0; e0 < p.E && e_found < 0; e0 += WAVE) {
+    // total slot tiles (experts in order, ceil(count / QBM) each)
+    int tr = 0;
+    for (int e0 = 0; e0 < p.E; e0 += WAVE) {
       const int e = e0 + lane;
       const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
-      int tiles = (c + QBM - 1) / QBM, incl = tiles;
+      tr += wave_sum_int((c + QBM - 1) / QBM);
+    }
+    const int lin = (int)(blockIdx.x + blockIdx.y * gridDim.x);
+    const int xcd = lin % kXcds, j = lin / kXcds, ny = (int)gridDim.y;
+    const int lo = xcd * tr / kXcds, nt = (xcd + 1) * tr / kXcds - lo;
+    int e_found = -1, m0 = 0, y = 0;
+    if (nt > 0 && j < nt * ny) {
+      y = j / nt;
+      const int T = lo + j % nt;
+      int base = 0;
+      for (int e0 = 0; e0 < p.E && e_found < 0; e0 += WAVE) {
+        const int e = e0 + lane;
+        const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
+        int tiles = (c + QBM - 1) / QBM, incl = tiles;
 #pragma unroll
-      for (int off = 1; off < WAVE; off <<= 1) {
-        const int v = __shfl_up(incl, off, WAVE);
-        if (lane >= off) incl += v;
+        for (int off = 1; off < WAVE; off <<= 1) {
+          const int v = __shfl_up(incl, off, WAVE);
+          if (lane >= off) incl += v;
+        }
+        const int excl = base + incl - tiles;
+        const unsigned long long m = __ballot(T >= excl && T < excl + tiles);
+        if (m) {
+          const int src = __ffsll((long long)m) - 1;
+          e_found = __shfl(e0 + lane, src, WAVE);
+          m0 = (T - __shfl(excl, src, WAVE)) * QBM;
+        }
+        base += __shfl(incl, WAVE - 1, WAVE);
       }
-      const int excl = base + incl - tiles;
-      const bool mine = (int)blockIdx.x >= excl && (int)blockIdx.x < excl + tiles;
-      const unsigned long long m = __ballot(mine);
-      if (m) {
-        const int src = __ffsll((long long)m) - 1;
-        e_found = __shfl(e0 + lane, src, WAVE);
-        m0 = ((int)blockIdx.x - __shfl(excl, src, WAVE)) * QBM;
-      }
-      base += __shfl(incl, WAVE - 1, WAVE);
     }
     if (lane == 0) {
       tile_info[0] = e_found;
       tile_info[1] = m0;
+      tile_info[2] = y;
     }
   }
   __syncthreads();
   const int e = tile_info[0], m0 = tile_info[1];
-  __syncthreads();  // every thread has read tile_info before decode(0) writes the B tile
   if (e < 0) return;  // past the last tile (the grid is an upper bound)
   const int rbeg = p.offs[e], cnt = p.offs[e + 1] - rbeg;
   const int cols = DUAL ? QBR / 2 : QBR;  // output columns per block
-  const int n0 = blockIdx.y * cols;
+  const int n0 = tile_info[2] * cols;
   const int K = p.K, nb = K / 32, nk = K / QKS;
 
   // --- DMA sources (per lane) ---
@@ -911,104 +936,116 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
       }
     }
   }
-  // decode of step t's codes (stage t % QNB) into B tile buffer t % 2:
-  // thread -> weight row tid / 2, block tid % 2 of the step
-  const int dr = tid / 2, dk = tid % 2;
-  const int srow = DUAL ? (dr / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (dr % (QBR / 2)) * nb : dr * nb;
-  auto decode = [&](int t) {  // codes of step t, into B tile buffer t % 2
-    const unsigned char* bs = ql + QLds::b + (t % QNB) * QLds::b_stage;
-    const q_u32x4 w = *(const q_u32x4*)(bs + dr * 32 + dk * 16);
-    const float sc = e8m0_scale(ql[QLds::sc + srow + 2 * t + dk]);
-    const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
-    uint32_t o[16];
-    fp4_block_bf16(ww, sc, o);
-    unsigned char* bt = ql + QLds::tile + (t & 1) * QLds::bt + dr * 128;
+  // B operands straight from the code stage: wave w takes two fragments of
+  // 16 weight rows (DUAL: gate rows 16 w + c and up rows 64 + 16 w + c, the
+  // block's output columns 16 w + c; otherwise rows 32 w + 16 f + c). Lane
+  // (g, c) = (lane / 16, lane % 16) takes, for MFMA k-step kk of a 64-value
+  // step (= MX block kk of its row), values 8 g .. 8 g + 7: code bytes
+  // 4 g .. 4 g + 3 of the block and the block's scale, converted in
+  // registers. The A operand of lane (g, c): chunk 4 kk + g of its slot
+  // row, the same K values.
+  const int g = lane / 16, c = lane % 16;
+  int brow[2], srow[2];
 #pragma unroll
-    for (int c = 0; c < 4; c++)  // logical chunks 4 dk + c (8 values each)
-      *(q_u32x4*)(bt + (((4 * dk + c) ^ q_swz(dr)) << 4)) = (q_u32x4){o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
-  };
-  auto frag = [&](const unsigned char* base, int r, int j) -> bf16x8 {
-    const int c = 4 * j + lane / 16;
-    return *(const bf16x8*)(base + r * 128 + ((c ^ q_swz(r)) << 4));
-  };
-  // weight row of B fragment j of this wave
-  auto brow = [&](int j) -> int {
-    if (DUAL) return (j < 2 ? 0 : QBR / 2) + 32 * wn + 16 * (j % 2);
-    return 64 * wn + 16 * j;
+  for (int f = 0; f < 2; f++) {
+    brow[f] = DUAL ? (f == 0 ? 16 * wave + c : QBR / 2 + 16 * wave + c) : 32 * wave + 16 * f + c;
+    srow[f] = DUAL ? (brow[f] / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (brow[f] % (QBR / 2)) * nb
+                   : brow[f] * nb;
+  }
+  auto achunk = [&](const unsigned char* as, int r, int ch) -> bf16x8 {
+    return *(const bf16x8*)(as + r * 128 + ((ch ^ q_swz(r)) << 4));
   };
 
-  constexpr int MI = QBM / 32;  // 16-slot sub-tiles per wave
-  f32x4 acc[MI][4];
+  f32x4 acc[2][2];  // [16-slot sub-tile][fragment]
 #pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int fr = lane % 16;
+  for (int i = 0; i < 2; i++) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // prologue: scales, codes(0 .. QNB - QNA), then groups
-  // [A(t), codes(t + QNB - QNA + 1)] for t < QNA - 1
-  auto issue_codes = [&](int c) {
-    const int tb = min(c, nk - 1);
-    unsigned char* bs = ql + QLds::b + (c % QNB) * QLds::b_stage;
-    __builtin_amdgcn_global_load_lds((const void*)(bsrc + (size_t)tb * 32), (lds_ptr)(bs + wave * 1024), 16, 0,
-                                     0);
-  };
-  auto issue_group = [&](int t) {  // A(t) then codes(t + QNB - QNA + 1), indexes clamped
+  // step t: A rows and codes into ring slot t % QNA (indexes past the last
+  // step clamped to it: read, never used)
+  auto issue_group = [&](int t) {
     const int tc = min(t, nk - 1);
     unsigned char* as = ql + QLds::a + (t % QNA) * QLds::a_stage;
 #pragma unroll
     for (int i = 0; i < QAI; i++)
       __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + tc * QKS),
                                        (lds_ptr)(as + (QAI * wave + i) * 1024), 16, 0, 0);
-    issue_codes(t + QNB - QNA + 1);
+    unsigned char* bs = ql + QLds::b + (t % QNB) * QLds::b_stage;
+    __builtin_amdgcn_global_load_lds((const void*)(bsrc + (size_t)tc * 32), (lds_ptr)(bs + wave * 1024), 16, 0,
+                                     0);
   };
-  for (int c = 0; c <= QNB - QNA; c++) issue_codes(c);
   for (int t = 0; t < QNA - 1; t++) issue_group(t);
-  wait_dma_behind<(QAI + 1) * (QNA - 1)>();  // scales and codes(0) landed
-  __syncthreads();
-  decode(0);
+  // the scales (a per-shape number of DMA instructions) and the first
+  // groups: waited for here, so that the loop's waits are exact counts
+  wait_dma_behind<0>();
   for (int kt = 0; kt < nk; kt++) {
-    // A(kt) was issued in the group of step kt - QNA + 1 (codes(kt + 1)
-    // earlier); the QNA - 2 later groups may stay in flight
+    // this wave's scales and groups up to kt landed (the QNA - 2 later
+    // groups may stay in flight); the barrier extends that to every wave's
+    // and frees the slot of step kt - 1
     wait_dma_behind<(QAI + 1) * (QNA - 2)>();
-    __syncthreads();  // B tile kt decoded by every thread; slots of step kt - 1 free
-    // group [A(kt + QNA - 1), codes(kt + QNB)]: A slot (kt - 1) % QNA (read
-    // at step kt - 1), code slot kt % QNB (decoded at step kt - 1)
-    issue_group(kt + QNA - 1);
-    if (kt + 1 < nk) decode(kt + 1);  // into the other B tile buffer
+    __syncthreads();
+    // every operand of step kt from LDS first, then the next group's DMA
+    // (into the slot of step kt - 1)
     const unsigned char* as = ql + QLds::a + (kt % QNA) * QLds::a_stage;
-    const unsigned char* bt = ql + QLds::tile + (kt & 1) * QLds::bt;
+    const unsigned char* bs = ql + QLds::b + (kt % QNB) * QLds::b_stage;
+    unsigned w[2][2];  // [fragment][k-step]: 8 codes
+    float sc[2][2];
 #pragma unroll
-    for (int ks = 0; ks < QKS / 32; ks++) {
-      bf16x8 b[4];
+    for (int f = 0; f < 2; f++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = frag(bt, brow(j) + fr, ks);
-#pragma unroll
-      for (int mi = 0; mi < MI; mi++) {
-        const int r = (QBM / 2) * wm + 16 * mi + fr;
-        const bf16x8 ah = frag(as, r, ks), al = frag(as, QBM + r, ks);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          acc[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[j], acc[mi][j], 0, 0, 0);
-          acc[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[j], acc[mi][j], 0, 0, 0);
-        }
+      for (int kk = 0; kk < 2; kk++) {
+        w[f][kk] = *(const unsigned*)(bs + brow[f] * 32 + kk * 16 + 4 * g);
+        sc[f][kk] = e8m0_scale(ql[QLds::sc + srow[f] + 2 * kt + kk]);
       }
+    bf16x8 ah[2][2], al[2][2];  // [k-step][16-slot sub-tile]
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++) {
+        const int ch = 4 * kk + g, r = 16 * mi + c;
+        ah[kk][mi] = achunk(as, r, ch);
+        al[kk][mi] = achunk(as, QBM + r, ch);
+      }
+    issue_group(kt + QNA - 1);
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      bf16x8 b[2];
+#pragma unroll
+      for (int f = 0; f < 2; f++) {
+        const unsigned x = w[f][kk];
+        const float y = sc[f][kk];
+        const uint4 v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, y, 0)),
+                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, y, 1)),
+                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, y, 2)),
+                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, y, 3))};
+        b[f] = __builtin_bit_cast(bf16x8, v);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+          acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kk][mi], b[f], acc[mi][f], 0, 0, 0);
+          acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[kk][mi], b[f], acc[mi][f], 0, 0, 0);
+        }
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // the clamped tail loads land before the wave ends
   // lane holds C[4 (lane / 16) + i][lane % 16] of each 16 x 16 tile
 #pragma unroll
-  for (int mi = 0; mi < MI; mi++)
+  for (int mi = 0; mi < 2; mi++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int r = (QBM / 2) * wm + 16 * mi + (lane / 16) * 4 + i;
+      const int r = 16 * mi + 4 * g + i;
       if (m0 + r >= cnt) continue;
       const int s2 = p.order[rbeg + m0 + r];
+      if (DUAL) {
+        const int n = n0 + 16 * wave + c;
+        if (n < p.N) p.y[(size_t)s2 * p.N + n] = silu_mul(acc[mi][0][i], acc[mi][1][i]);
+      } else {
 #pragma unroll
-      for (int j = 0; j < (DUAL ? 2 : 4); j++) {
-        const int n = n0 + (DUAL ? 32 * wn : 64 * wn) + 16 * j + lane % 16;
-        if (n >= p.N) continue;
-        p.y[(size_t)s2 * p.N + n] = DUAL ? silu_mul(acc[mi][j][i], acc[mi][j + 2][i]) : acc[mi][j][i];
+        for (int f = 0; f < 2; f++) {
+          const int n = n0 + 32 * wave + 16 * f + c;
+          if (n < p.N) p.y[(size_t)s2 * p.N + n] = acc[mi][f][i];
+        }
       }
     }
 }
@@ -1159,7 +1196,10 @@ void moe_group_gemm(const MoeGemmParams& p, hipStream_t s) {
     const int nb = p.K / 32, runs = dual ? 2 : 1;
     const size_t shm = QLds::sc + (size_t)runs * q_scale_run(QBR / runs, nb);
     const int cols = dual ? QBR / 2 : QBR;
-    const dim3 grid((p.slots + QBM - 1) / QBM + p.E, (p.N + cols - 1) / cols);
+    // slot tiles: an upper bound (the counts are on the device), rounded to
+    // whole rounds of the XCDs (the kernel's per-XCD layout)
+    const int tmax = ((p.slots + QBM - 1) / QBM + p.E + kXcds - 1) / kXcds * kXcds;
+    const dim3 grid(tmax, (p.N + cols - 1) / cols);
     if (dual) {
       set_lds(group_gemm2_kernel<true>, shm);
       hipLaunchKernelGGL(group_gemm2_kernel<true>, grid, dim3(256), shm, s, p);
