@@ -823,7 +823,8 @@ struct QLds {
   static constexpr int a = 0;
   static constexpr int b = a + QNA * a_stage;
   static constexpr int info = b + QNB * b_stage;     // the tile lookup result
-  static constexpr int sc = info + 1024;             // scales: QBR rows x nb bytes
+  static constexpr int fsc = info + 256;             // [2][QBR rows][2 blocks] fp32 scales of a step
+  static constexpr int sc = info + 3072;             // scales: QBR rows x nb bytes
 };
 static_assert(QNA == QNB, "one ring slot per step for the A rows and the codes");
 
@@ -945,13 +946,10 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   // registers. The A operand of lane (g, c): chunk 4 kk + g of its slot
   // row, the same K values.
   const int g = lane / 16, c = lane % 16;
-  int brow[2], srow[2];
+  int brow[2];
 #pragma unroll
-  for (int f = 0; f < 2; f++) {
+  for (int f = 0; f < 2; f++)
     brow[f] = DUAL ? (f == 0 ? 16 * wave + c : QBR / 2 + 16 * wave + c) : 32 * wave + 16 * f + c;
-    srow[f] = DUAL ? (brow[f] / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (brow[f] % (QBR / 2)) * nb
-                   : brow[f] * nb;
-  }
   auto achunk = [&](const unsigned char* as, int r, int ch) -> bf16x8 {
     return *(const bf16x8*)(as + r * 128 + ((ch ^ q_swz(r)) << 4));
   };
@@ -977,6 +975,14 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   // the scales (a per-shape number of DMA instructions) and the first
   // groups: waited for here, so that the loop's waits are exact counts
   wait_dma_behind<0>();
+  __syncthreads();
+  // the E8M0 scales of a step as fp32, one per thread (row tid / 2, block
+  // tid % 2), a step ahead of their use
+  float* fsc = (float*)(ql + QLds::fsc);
+  const int crow = tid / 2;
+  const int csrc = QLds::sc + (DUAL ? (crow / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (crow % (QBR / 2)) * nb
+                                    : crow * nb) + tid % 2;
+  fsc[tid] = e8m0_scale(ql[csrc]);
   for (int kt = 0; kt < nk; kt++) {
     // this wave's scales and groups up to kt landed (the QNA - 2 later
     // groups may stay in flight); the barrier extends that to every wave's
@@ -990,12 +996,14 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     unsigned w[2][2];  // [fragment][k-step]: 8 codes
     float sc[2][2];
 #pragma unroll
-    for (int f = 0; f < 2; f++)
+    for (int f = 0; f < 2; f++) {
+      const float2v s2 = *(const float2v*)(fsc + (kt & 1) * 2 * QBR + 2 * brow[f]);
+      sc[f][0] = s2[0];
+      sc[f][1] = s2[1];
 #pragma unroll
-      for (int kk = 0; kk < 2; kk++) {
-        w[f][kk] = *(const unsigned*)(bs + brow[f] * 32 + kk * 16 + 4 * g);
-        sc[f][kk] = e8m0_scale(ql[QLds::sc + srow[f] + 2 * kt + kk]);
-      }
+      for (int kk = 0; kk < 2; kk++) w[f][kk] = *(const unsigned*)(bs + brow[f] * 32 + kk * 16 + 4 * g);
+    }
+    if (kt + 1 < nk) fsc[((kt + 1) & 1) * 2 * QBR + tid] = e8m0_scale(ql[csrc + 2 * (kt + 1)]);
     bf16x8 ah[2][2], al[2][2];  // [k-step][16-slot sub-tile]
 #pragma unroll
     for (int kk = 0; kk < 2; kk++)
