@@ -786,22 +786,30 @@ __global__ __launch_bounds__(256) void group_gemm_kernel(MoeGemmParams p) {
 //   expert order (moe_gather_split), so a tile's rows are contiguous and go
 //   to LDS by the global-to-LDS DMA in 128-byte row segments (K steps of
 //   64), 3-stage ring;
-// * the MXFP4 code bytes of the tile's 128 weight rows (gate 64 + up 64, or
-//   128 rows of one matrix, 4 KiB per step) go with the A rows of the same
-//   step into the same slot of a 3-stage DMA ring; the rows' E8M0 scales
-//   are DMA'd once per block;
+// * the MXFP4 code bytes of the tile's QBR weight rows (half gate, half up,
+//   or QBR rows of one matrix; QBR x 32 bytes per step) go with the A rows
+//   of the same step into the same slot of a 3-stage DMA ring; the rows'
+//   E8M0 scales are DMA'd once per block and converted to fp32 a step ahead;
 // * each wave converts the codes of its own weight rows straight into its
 //   MFMA B operands (hardware FP4 conversion to packed bf16 pairs, exact),
 //   so no decoded tile goes through LDS: 32 slots (experts average about 32
-//   slots per chunk: 64-slot tiles would be half empty) x 128 rows x 64 K
-//   per step, 16 MFMAs per wave (each wave: all 32 slots x 16 output
-//   columns of both matrices, or x 32 columns of one); ~50 KiB of LDS at
-//   K = 2880, two blocks per CU.
-// Each step issues exactly QAI A + 1 code DMA instructions per wave
+//   slots per chunk: 64-slot tiles would be half empty) x QBR rows x 64 K
+//   per step, 8 QFR MFMAs per wave (each wave: all 32 slots x QFR 16-row
+//   fragments). Every wave reads the whole A stage, so wider blocks read A
+//   less often per product: QBR = 256 takes 1.2x the time of 128 for twice
+//   the work, but its grid of half as many blocks (at two per CU, 75 KiB of
+//   LDS) leaves a partial last round at the 256-token prefill and loses
+//   there (228 vs 193 us for the gate/up pair); it wins at 2048 tokens
+//   (927 vs 1018 us). QBR = 128: ~50 KiB of LDS at K = 2880, three blocks
+//   per CU.
+// * the grid is laid out per XCD (see the kernel).
+// Each step issues exactly QAI A + QBI code DMA instructions per wave
 // (indexes past the last step are clamped to it and never read), so the
 // wait before a step is a constant: the groups of the QNA - 2 later steps
 // may stay in flight.
 constexpr int QBM = 32, QKS = 64, QBR = 128;  // slots, K per step, weight rows per block
+constexpr int QFR = QBR / 64;                  // 16-row B fragments per wave
+constexpr int QBI = QBR / 128;                 // code DMA instructions per wave and step
 constexpr int kXcds = 8;                      // XCDs of an MI355X (round-robin block dispatch)
 
 __device__ __forceinline__ int wave_sum_int(int v) {
@@ -824,7 +832,7 @@ struct QLds {
   static constexpr int b = a + QNA * a_stage;
   static constexpr int info = b + QNB * b_stage;     // the tile lookup result
   static constexpr int fsc = info + 256;             // [2][QBR rows][2 blocks] fp32 scales of a step
-  static constexpr int sc = info + 3072;             // scales: QBR rows x nb bytes
+  static constexpr int sc = (fsc + 2 * QBR * 2 * 4 + 1023) / 1024 * 1024;  // scales: QBR rows x nb bytes
 };
 static_assert(QNA == QNB, "one ring slot per step for the A rows and the codes");
 
@@ -910,14 +918,15 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     const int grow = rbeg + min(m0 + r, cnt - 1);  // rows past the tile load its last row
     asrc[i] = (row < QBM ? p.a_hi : p.a_lo) + (size_t)grow * K + 8 * c;
   }
-  // codes: instruction of wave w covers weight rows 32 w .. 32 w + 31, lane
-  // -> row 32 w + lane / 2, block lane % 2 of the step
-  const uint8_t* bsrc;
-  {
-    const int br = 32 * wave + lane / 2;
+  // codes: instruction i of wave w covers weight rows 32 (QBI w + i) ..
+  // + 31, lane -> row + lane / 2, block lane % 2 of the step
+  const uint8_t* bsrc[QBI];
+#pragma unroll
+  for (int i = 0; i < QBI; i++) {
+    const int br = 32 * (QBI * wave + i) + lane / 2;
     const bool up = DUAL && br >= QBR / 2;
     const int n = min(n0 + (DUAL ? br % (QBR / 2) : br), p.N - 1);
-    bsrc = (up ? p.blocks2 : p.blocks) + ((size_t)e * p.N + n) * nb * 16 + (lane % 2) * 16;
+    bsrc[i] = (up ? p.blocks2 : p.blocks) + ((size_t)e * p.N + n) * nb * 16 + (lane % 2) * 16;
   }
 
   // scales of the block's rows: per matrix a contiguous run of rows x nb
@@ -937,26 +946,31 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
       }
     }
   }
-  // B operands straight from the code stage: wave w takes two fragments of
-  // 16 weight rows (DUAL: gate rows 16 w + c and up rows 64 + 16 w + c, the
-  // block's output columns 16 w + c; otherwise rows 32 w + 16 f + c). Lane
+  // B operands straight from the code stage: wave w takes QFR fragments of
+  // 16 weight rows (DUAL: the gate and up rows of its QFR / 2 16-column
+  // groups of the block's output columns; otherwise QFR 16-column groups of
+  // one matrix). Lane
   // (g, c) = (lane / 16, lane % 16) takes, for MFMA k-step kk of a 64-value
   // step (= MX block kk of its row), values 8 g .. 8 g + 7: code bytes
   // 4 g .. 4 g + 3 of the block and the block's scale, converted in
   // registers. The A operand of lane (g, c): chunk 4 kk + g of its slot
   // row, the same K values.
   const int g = lane / 16, c = lane % 16;
-  int brow[2];
+  constexpr int HF = QFR / 2;  // DUAL: column groups per wave
+  int brow[QFR];
 #pragma unroll
-  for (int f = 0; f < 2; f++)
-    brow[f] = DUAL ? (f == 0 ? 16 * wave + c : QBR / 2 + 16 * wave + c) : 32 * wave + 16 * f + c;
+  for (int f = 0; f < QFR; f++)
+    brow[f] = DUAL ? (f < HF ? 16 * HF * wave + 16 * f + c : QBR / 2 + 16 * HF * wave + 16 * (f - HF) + c)
+                   : 16 * QFR * wave + 16 * f + c;
   auto achunk = [&](const unsigned char* as, int r, int ch) -> bf16x8 {
     return *(const bf16x8*)(as + r * 128 + ((ch ^ q_swz(r)) << 4));
   };
 
-  f32x4 acc[2][2];  // [16-slot sub-tile][fragment]
+  f32x4 acc[2][QFR];  // [16-slot sub-tile][fragment]
 #pragma unroll
-  for (int i = 0; i < 2; i++) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int f = 0; f < QFR; f++) acc[i][f] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // step t: A rows and codes into ring slot t % QNA (indexes past the last
   // step clamped to it: read, never used)
@@ -968,42 +982,52 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
       __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + tc * QKS),
                                        (lds_ptr)(as + (QAI * wave + i) * 1024), 16, 0, 0);
     unsigned char* bs = ql + QLds::b + (t % QNB) * QLds::b_stage;
-    __builtin_amdgcn_global_load_lds((const void*)(bsrc + (size_t)tc * 32), (lds_ptr)(bs + wave * 1024), 16, 0,
-                                     0);
+#pragma unroll
+    for (int i = 0; i < QBI; i++)
+      __builtin_amdgcn_global_load_lds((const void*)(bsrc[i] + (size_t)tc * 32),
+                                       (lds_ptr)(bs + (QBI * wave + i) * 1024), 16, 0, 0);
   };
   for (int t = 0; t < QNA - 1; t++) issue_group(t);
   // the scales (a per-shape number of DMA instructions) and the first
   // groups: waited for here, so that the loop's waits are exact counts
   wait_dma_behind<0>();
   __syncthreads();
-  // the E8M0 scales of a step as fp32, one per thread (row tid / 2, block
-  // tid % 2), a step ahead of their use
+  // the E8M0 scales of a step as fp32 (row q / 2, block q % 2 for q = tid,
+  // tid + 256, ..), a step ahead of their use
   float* fsc = (float*)(ql + QLds::fsc);
-  const int crow = tid / 2;
-  const int csrc = QLds::sc + (DUAL ? (crow / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (crow % (QBR / 2)) * nb
-                                    : crow * nb) + tid % 2;
-  fsc[tid] = e8m0_scale(ql[csrc]);
+  constexpr int NCS = 2 * QBR / 256;  // scales per thread and step
+  int csrc[NCS];
+#pragma unroll
+  for (int i = 0; i < NCS; i++) {
+    const int q = tid + 256 * i, crow = q / 2;
+    csrc[i] = QLds::sc + (DUAL ? (crow / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (crow % (QBR / 2)) * nb
+                               : crow * nb) + q % 2;
+    fsc[q] = e8m0_scale(ql[csrc[i]]);
+  }
   for (int kt = 0; kt < nk; kt++) {
     // this wave's scales and groups up to kt landed (the QNA - 2 later
     // groups may stay in flight); the barrier extends that to every wave's
     // and frees the slot of step kt - 1
-    wait_dma_behind<(QAI + 1) * (QNA - 2)>();
+    wait_dma_behind<(QAI + QBI) * (QNA - 2)>();
     __syncthreads();
     // every operand of step kt from LDS first, then the next group's DMA
     // (into the slot of step kt - 1)
     const unsigned char* as = ql + QLds::a + (kt % QNA) * QLds::a_stage;
     const unsigned char* bs = ql + QLds::b + (kt % QNB) * QLds::b_stage;
-    unsigned w[2][2];  // [fragment][k-step]: 8 codes
-    float sc[2][2];
+    unsigned w[QFR][2];  // [fragment][k-step]: 8 codes
+    float sc[QFR][2];
 #pragma unroll
-    for (int f = 0; f < 2; f++) {
+    for (int f = 0; f < QFR; f++) {
       const float2v s2 = *(const float2v*)(fsc + (kt & 1) * 2 * QBR + 2 * brow[f]);
       sc[f][0] = s2[0];
       sc[f][1] = s2[1];
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) w[f][kk] = *(const unsigned*)(bs + brow[f] * 32 + kk * 16 + 4 * g);
     }
-    if (kt + 1 < nk) fsc[((kt + 1) & 1) * 2 * QBR + tid] = e8m0_scale(ql[csrc + 2 * (kt + 1)]);
+    if (kt + 1 < nk) {
+#pragma unroll
+      for (int i = 0; i < NCS; i++) fsc[((kt + 1) & 1) * 2 * QBR + tid + 256 * i] = e8m0_scale(ql[csrc[i] + 2 * (kt + 1)]);
+    }
     bf16x8 ah[2][2], al[2][2];  // [k-step][16-slot sub-tile]
 #pragma unroll
     for (int kk = 0; kk < 2; kk++)
@@ -1016,9 +1040,9 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     issue_group(kt + QNA - 1);
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
-      bf16x8 b[2];
+      bf16x8 b[QFR];
 #pragma unroll
-      for (int f = 0; f < 2; f++) {
+      for (int f = 0; f < QFR; f++) {
         const unsigned x = w[f][kk];
         const float y = sc[f][kk];
         const uint4 v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, y, 0)),
@@ -1030,7 +1054,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
 #pragma unroll
       for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int f = 0; f < 2; f++) {
+        for (int f = 0; f < QFR; f++) {
           acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kk][mi], b[f], acc[mi][f], 0, 0, 0);
           acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[kk][mi], b[f], acc[mi][f], 0, 0, 0);
         }
@@ -1046,12 +1070,15 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
       if (m0 + r >= cnt) continue;
       const int s2 = p.order[rbeg + m0 + r];
       if (DUAL) {
-        const int n = n0 + 16 * wave + c;
-        if (n < p.N) p.y[(size_t)s2 * p.N + n] = silu_mul(acc[mi][0][i], acc[mi][1][i]);
+#pragma unroll
+        for (int j = 0; j < HF; j++) {
+          const int n = n0 + 16 * HF * wave + 16 * j + c;
+          if (n < p.N) p.y[(size_t)s2 * p.N + n] = silu_mul(acc[mi][j][i], acc[mi][HF + j][i]);
+        }
       } else {
 #pragma unroll
-        for (int f = 0; f < 2; f++) {
-          const int n = n0 + 32 * wave + 16 * f + c;
+        for (int f = 0; f < QFR; f++) {
+          const int n = n0 + 16 * QFR * wave + 16 * f + c;
           if (n < p.N) p.y[(size_t)s2 * p.N + n] = acc[mi][f][i];
         }
       }
