@@ -99,10 +99,11 @@ def test_bf16_cache_against_oracle(name, model_dir):
 
 
 def test_bf16_cache_prefill_after_decode_steps(model_dir):
-    """Rows written by decode steps into the bf16 cache are converted to the
-    prefill attention's planes like fp32 rows: a prompt as one prefill, and
-    as a prefill, 11 single-token steps and one chunk of the rest, give the
-    same last-row logits (within 2e-3 of their largest magnitude)."""
+    """Rows written by decode steps with a bf16 cache go into the attention
+    kernels' planes as the prefill writes them: a prompt as one prefill, and
+    as a prefill, 40 single-token steps and one chunk of the rest (which
+    reads rows 37-63 from the decode steps), give the same last-row logits
+    (within 2e-3 of their largest magnitude)."""
     rt = runtime()
     prompt = synth.prompt_tokens(128, 600, 23)
     with rt.Transformer(model_dir("tiny-long")) as t:
@@ -110,9 +111,9 @@ def test_bf16_cache_prefill_after_decode_steps(model_dir):
         whole = t.predict(prompt)[0]
         t.reset()
         t.predict(prompt[:37])
-        for tok in prompt[37:48]:
+        for tok in prompt[37:77]:
             t.predict([tok])
-        parts = t.predict(prompt[48:])[0]
+        parts = t.predict(prompt[77:])[0]
     err = np.abs(parts - whole).max()
     scale = max(1.0, float(np.abs(whole).max()))
     log(f"tiny-long: max |logit difference| {err:.3g} (largest |logit| {scale:.3g})")

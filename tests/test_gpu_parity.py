@@ -180,22 +180,22 @@ def test_predict_host_loop_equals_device_loop(model_dir):
 @pytest.mark.parametrize("name", ["tiny-chunk", "tiny-long"])
 def test_prefill_after_decode_steps(name, model_dir):
     """A prompt fed as one prefill, and as a prefill of its first 37 tokens,
-    then 11 single-token steps (the decode path, which writes cache rows
-    without converting them to the prefill attention's bf16 planes), then
-    one chunk of the rest: the second prefill converts the rows the decode
-    steps wrote (from a multiple of 32) before attending to them. Last-row
-    logits agree within 2e-3 of their largest magnitude (different kernels
-    and summation orders; rows left out of the planes read as zero and move
-    the logits by orders of magnitude more)."""
+    then 40 single-token steps (the decode path, which writes each row into
+    the cache and into the attention kernels' bf16 planes), then one chunk
+    of the rest: the second prefill converts its own rows from row 64 (a
+    multiple of 32) and attends to rows 37-63 as the decode steps wrote
+    them. Last-row logits agree within 2e-3 of their largest magnitude
+    (different kernels and summation orders; a row missing from the planes
+    moves the logits by orders of magnitude more)."""
     rt = runtime()
     prompt = synth.prompt_tokens(128, 300 if name == "tiny-chunk" else 600, 23)
     with rt.Transformer(model_dir(name)) as t:
         whole = t.predict(prompt)[0]
         t.reset()
         t.predict(prompt[:37])
-        for tok in prompt[37:48]:
+        for tok in prompt[37:77]:
             t.predict([tok])
-        parts = t.predict(prompt[48:])[0]
+        parts = t.predict(prompt[77:])[0]
     err = np.abs(parts - whole).max()
     scale = max(1.0, float(np.abs(whole).max()))
     log(f"{name}: max |logit difference| {err:.3g} (largest |logit| {scale:.3g})")
@@ -262,11 +262,11 @@ def test_decode_step_logits(name, model_dir):
 
 
 def test_reset_starts_a_new_sequence(model_dir):
-    """After transformer_reset, a new sequence that starts with single-token
-    steps (which write cache rows but not the prefill attention's bf16
-    planes) and then prefills the rest attends to its own rows, not to the
-    previous sequence's: last-row logits agree with the oracle on the new
-    sequence alone."""
+    """After transformer_reset, a new sequence that starts with 45
+    single-token steps (their rows go into the cache and its bf16 planes)
+    and then prefills the rest attends to its own rows, not to the previous
+    sequence's (rows 0-31 are read as the decode steps wrote them): last-row
+    logits agree with the oracle on the new sequence alone."""
     rt = runtime()
     d = model_dir("tiny-chunk")
     a = synth.prompt_tokens(128, 300, 41)
