@@ -220,6 +220,28 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnParams p) {
 //   B operand straight from the scores a lane holds; the A operand is one
 //   16-byte read of V^T (row 16 dj + c, keys 8 g ..) per plane.
 // head_dim 16 pads the 32-dim k-step of S with zeros (lanes g >= 2).
+// Lane l's value plus / max with lane l ^ 16 or l ^ 32 (gfx950 lane-swap
+// moves: no LDS round trip), and lane l ^ 8 within a row of 16 (DPP).
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float dpp_ror8(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));  // row_ror:8
+}
+
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 
@@ -312,33 +334,42 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* kc, const 
   }
 }
 
-template <int HD>
+// QS query sub-tiles of 16 per wave (PQ = 64 QS queries per block): the K
+// and V fragments a wave reads from LDS for a tile serve all of them, so
+// QS = 2 halves the LDS reads per product (the kernel is bound by them).
+template <int HD, int QS>
 __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
   constexpr int KT = kX3Keys;              // keys per tile
   constexpr int NKK = (HD + 31) / 32;      // 32-dim k-steps of S
   constexpr int DJ = HD / 16;              // 16-dim sub-tiles of O
+  constexpr int PQB = PQ * QS;             // queries per block
   using L = X3Lds<HD>;
   static_assert(L::KP % 512 == 0 && L::VP % 512 == 0, "planes split into 1 KiB DMA instructions");
   constexpr int NKI = L::KP / 512, NVI = L::VP / 512;  // 1 KiB instructions per plane
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
   const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, g = lane / 16, c = lane % 16;
-  const int nqb = (p.T + PQ - 1) / PQ;
+  const int nqb = (p.T + PQB - 1) / PQB;
   const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
   const int head = blockIdx.y;
   const int G = p.q_heads / p.kv_heads, kvh = head / G;
   const int P = *p.pos + p.q0, T = p.T;
   const int qd = p.q_heads * HD;
-  const int t = qb * PQ + wave * 16 + c;  // this lane's query
+  int t[QS];  // this lane's queries
+#pragma unroll
+  for (int q = 0; q < QS; q++) t[q] = qb * PQB + wave * 16 * QS + 16 * q + c;
   const uint16_t* khg = p.khi + (size_t)kvh * p.ctx * HD;
   const uint16_t* klg = p.klo + (size_t)kvh * p.ctx * HD;
   const uint16_t* vhg = p.vthi + (size_t)kvh * HD * p.ctx_pad;
   const uint16_t* vlg = p.vtlo + (size_t)kvh * HD * p.ctx_pad;
-  const int kv_end = P + min(qb * PQ + PQ, T);  // keys visible to the block's last query
+  const int kv_end = P + min(qb * PQB + PQB, T);  // keys visible to the block's last query
   const int ntiles = (kv_end + KT - 1) / KT;
   // scores in the base-2 domain: s * log2(e) / sqrt(HD)
   const float sl2 = 1.44269504088896341f / sqrtf((float)HD);
-  // last key visible to this lane's query, and to every query of the block
-  const int vis = min(P + t, kv_end - 1), vis_all = min(P + qb * PQ, kv_end - 1);
+  // last key visible to each of this lane's queries, and to every query of the block
+  int vis[QS];
+#pragma unroll
+  for (int q = 0; q < QS; q++) vis[q] = min(P + t[q], kv_end - 1);
+  const int vis_all = min(P + qb * PQB, kv_end - 1);
 
   auto split8 = [](const float (&x)[8], bf16x8& hi, bf16x8& lo) {
     uint32_t h[4], l[4];
@@ -372,10 +403,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
   };
 
   dma_tile(0, xl);
-  // Q^T operand: lane (g, c) holds q[t][32 kk + 8 g .. + 7], split.
-  bf16x8 qh[NKK], ql[NKK];
-  {
-    const float* qr = p.q + (size_t)min(t, T - 1) * qd + head * HD;
+  // Q^T operands: lane (g, c) holds q[t][32 kk + 8 g .. + 7], split.
+  bf16x8 qh[QS][NKK], ql[QS][NKK];
+#pragma unroll
+  for (int q = 0; q < QS; q++) {
+    const float* qr = p.q + (size_t)min(t[q], T - 1) * qd + head * HD;
 #pragma unroll
     for (int kk = 0; kk < NKK; kk++) {
       float x[8];
@@ -387,14 +419,19 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
 #pragma unroll
         for (int e = 0; e < 8; e++) x[e] = 0.0f;
       }
-      split8(x, qh[kk], ql[kk]);
+      split8(x, qh[q][kk], ql[q][kk]);
     }
   }
 
-  f32x4 o[DJ];
+  f32x4 o[QS][DJ];
+  float m[QS], l[QS];
 #pragma unroll
-  for (int j = 0; j < DJ; j++) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.0f;
+  for (int q = 0; q < QS; q++) {
+#pragma unroll
+    for (int j = 0; j < DJ; j++) o[q][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m[q] = -INFINITY;
+    l[q] = 0.0f;
+  }
   // Per-lane parts of the LDS addresses (elements).
   int krow[2], kx[2];
 #pragma unroll
@@ -415,10 +452,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
     const uint16_t* vhi = buf + 2 * L::KP;
     const uint16_t* vlo = vhi + L::VP;
     const int kv0 = it * KT;
-    f32x4 sc[2];
+    f32x4 sc[QS][2];
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-      sc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < QS; q++) sc[q][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < NKK; kk++) {
         // dims past HD (head_dim 16: lane groups 2, 3) are zero in both
@@ -429,66 +467,70 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
           kh = *(const bf16x8*)(khi + off);
           kl = *(const bf16x8*)(klo + off);
         }
-        sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[kk], sc[s], 0, 0, 0);
-        sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[kk], sc[s], 0, 0, 0);
-        sc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[kk], sc[s], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < QS; q++) {
+          sc[q][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[q][kk], sc[q][s], 0, 0, 0);
+          sc[q][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[q][kk], sc[q][s], 0, 0, 0);
+          sc[q][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[q][kk], sc[q][s], 0, 0, 0);
+        }
       }
     }
-    // Causal mask and online softmax of query t (base 2; lane groups g hold
-    // keys 8 g .. 8 g + 7 of the tile).
-    float pv[8];
-    float mx = -INFINITY;
-    if (kv0 + KT - 1 <= vis_all) {  // every key of the tile visible to every query of the block
+    // Causal mask and online softmax of each query (base 2; lane groups g
+    // hold keys 8 g .. 8 g + 7 of the tile).
+    bf16x8 ph[QS], pl[QS];
+    const bool full = kv0 + KT - 1 <= vis_all;  // every key of the tile visible to every query of the block
+#pragma unroll
+    for (int q = 0; q < QS; q++) {
+      float pv[8];
+      float mx = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        pv[j] = sc[j >> 2][j & 3] * sl2;
-        mx = fmaxf(mx, pv[j]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float v = kv0 + 8 * g + j <= vis ? sc[j >> 2][j & 3] * sl2 : -INFINITY;
+        const float v = full || kv0 + 8 * g + j <= vis[q] ? sc[q][j >> 2][j & 3] * sl2 : -INFINITY;
         pv[j] = v;
         mx = fmaxf(mx, v);
       }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-    const float mn = fmaxf(m, mx);
-    const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
-    float rs = 0.0f;
+      mx = fmaxf(mx, xor16_max(mx));
+      mx = fmaxf(mx, xor32_max(mx));
+      const float mn = fmaxf(m[q], mx);
+      const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[q] - mn);
+      float rs = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const float e = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pv[j] - mn);
-      pv[j] = e;
-      rs += e;
-    }
-    rs += __shfl_xor(rs, 16, WAVE);
-    rs += __shfl_xor(rs, 32, WAVE);
-    l = l * corr + rs;
-    m = mn;
+      for (int j = 0; j < 8; j++) {
+        const float e = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pv[j] - mn);
+        pv[j] = e;
+        rs += e;
+      }
+      rs = xor16_sum(rs);
+      rs = xor32_sum(rs);
+      l[q] = l[q] * corr + rs;
+      m[q] = mn;
 #pragma unroll
-    for (int j = 0; j < DJ; j++) o[j] *= corr;
-    bf16x8 ph, pl;
-    split8(pv, ph, pl);
+      for (int j = 0; j < DJ; j++) o[q][j] *= corr;
+      split8(pv, ph[q], pl[q]);
+    }
 #pragma unroll
     for (int dj = 0; dj < DJ; dj++) {
       const bf16x8 vh = *(const bf16x8*)(vhi + vrow + 16 * dj * KT);
       const bf16x8 vl = *(const bf16x8*)(vlo + vrow + 16 * dj * KT);
-      o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[dj], 0, 0, 0);
-      o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[dj], 0, 0, 0);
-      o[dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[dj], 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < QS; q++) {
+        o[q][dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[q], o[q][dj], 0, 0, 0);
+        o[q][dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[q], o[q][dj], 0, 0, 0);
+        o[q][dj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[q], o[q][dj], 0, 0, 0);
+      }
     }
   }
   // lane (g, c) holds O^T[16 dj + 4 g + e][t]: out[t][head*HD + 16 dj + 4 g + e]
-  if (t < T) {
+#pragma unroll
+  for (int q = 0; q < QS; q++) {
+    if (t[q] >= T) continue;
 #pragma unroll
     for (int j = 0; j < DJ; j++) {
-      const size_t idx = (size_t)t * qd + head * HD + 16 * j + 4 * g;
+      const size_t idx = (size_t)t[q] * qd + head * HD + 16 * j + 4 * g;
       uint16_t hi[4], lo[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const float v = o[j][e] / l;
+        const float v = o[q][j][e] / l[q];
         hi[e] = f32_to_bf16_rne(v);
         lo[e] = f32_to_bf16_rne(v - bf16_to_f32(hi[e]));
       }
@@ -595,28 +637,6 @@ __host__ __device__ inline void decode_mfma_split(int total, int max_blocks, int
   const int per = (nt + max_blocks - 1) / max_blocks;
   tpb = per > kD2MinTiles ? per : kD2MinTiles;
   nb = (nt + tpb - 1) / tpb;
-}
-
-// Lane l's value plus / max with lane l ^ 16 or l ^ 32 (gfx950 lane-swap
-// moves: no LDS round trip), and lane l ^ 8 within a row of 16 (DPP).
-__device__ __forceinline__ float xor16_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xor32_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xor16_max(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor32_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float dpp_ror8(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));  // row_ror:8
 }
 
 __device__ __forceinline__ void split8v(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
@@ -1043,7 +1063,10 @@ void attention_init() {
   HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_mfma_kernel<128>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 4 * PK * 128 * (int)sizeof(float)));
 #define X3_ATTR(HD)                                                                  \
-  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_x3_kernel<HD>,             \
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_x3_kernel<HD, 1>,          \
+                                hipFuncAttributeMaxDynamicSharedMemorySize,          \
+                                X3Lds<HD>::bytes));                                  \
+  HIP_CHECK(hipFuncSetAttribute((const void*)attn_prefill_x3_kernel<HD, 2>,          \
                                 hipFuncAttributeMaxDynamicSharedMemorySize,          \
                                 X3Lds<HD>::bytes));
   X3_ATTR(16)
@@ -1054,16 +1077,20 @@ void attention_init() {
 }
 
 // STRASGPT_PREFILL_ATTN=fp32 selects the fp32 matrix-core kernel; the
-// default is the split bf16 one (about 3x faster at long contexts).
-bool prefill_attn_fp32() {
+// default is the split bf16 one (about 3x faster at long contexts), with 32
+// queries per wavefront where the grid of 128-query blocks still fills two
+// blocks per CU, else 16 (x3-16 / x3-32 force one of them).
+int prefill_attn_mode() {
   const char* e = getenv("STRASGPT_PREFILL_ATTN");
-  if (!e || !*e || !strcmp(e, "x3")) return false;
-  if (!strcmp(e, "fp32")) return true;
-  ST_DIE("STRASGPT_PREFILL_ATTN must be x3 or fp32");
+  if (!e || !*e || !strcmp(e, "x3")) return 0;
+  if (!strcmp(e, "fp32")) return 1;
+  if (!strcmp(e, "x3-16")) return 2;
+  if (!strcmp(e, "x3-32")) return 3;
+  ST_DIE("STRASGPT_PREFILL_ATTN must be x3, x3-16, x3-32 or fp32");
 }
 
 void attention_prefill(const AttnParams& p, hipStream_t s) {
-  attention_prefill_variant(p, prefill_attn_fp32() ? 1 : 0, s);
+  attention_prefill_variant(p, prefill_attn_mode(), s);
 }
 
 void attention_split_rows(const float* kcache, const float* vcache, uint16_t* khi, uint16_t* klo,
@@ -1098,17 +1125,21 @@ void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s) 
   if (!p.out_hi) ST_DIE("prefill attention writes bf16 planes");
   if (variant == 0 && (!p.khi || !p.klo || !p.vthi || !p.vtlo || p.ctx_pad % 32 || p.ctx_pad < p.ctx))
     ST_DIE("split-bf16 prefill attention needs the cache's bf16 planes");
-  if (variant != 0 && variant != 1) ST_DIE("prefill attention variant is 0 (split bf16) or 1 (fp32)");
+  if (variant < 0 || variant > 3) ST_DIE("prefill attention variant is 0 (split bf16), 1 (fp32), 2 or 3");
   if (variant == 1 && p.kv_bf16) ST_DIE("the fp32 prefill attention kernel reads an fp32 KV cache only");
-  dim3 grid((p.T + PQ - 1) / PQ, p.q_heads);
   const bool fp32 = variant == 1;
+  // split bf16: 32 queries per wave when 128-query blocks give 2 per CU
+  const bool wide = variant == 3 || (variant == 0 && (long)((p.T + 2 * PQ - 1) / (2 * PQ)) * p.q_heads >= 512);
+  const dim3 grid((p.T + (wide ? 2 * PQ : PQ) - 1) / (wide ? 2 * PQ : PQ), p.q_heads);
   switch (p.hd) {
 #define PREFILL_CASE(HD)                                                                         \
   case HD:                                                                                       \
     if (fp32)                                                                                    \
       hipLaunchKernelGGL(attn_prefill_mfma_kernel<HD>, grid, dim3(256), 4 * PK * HD * sizeof(float), s, p); \
+    else if (wide)                                                                               \
+      hipLaunchKernelGGL((attn_prefill_x3_kernel<HD, 2>), grid, dim3(256), X3Lds<HD>::bytes, s, p); \
     else                                                                                         \
-      hipLaunchKernelGGL(attn_prefill_x3_kernel<HD>, grid, dim3(256), X3Lds<HD>::bytes, s, p); \
+      hipLaunchKernelGGL((attn_prefill_x3_kernel<HD, 1>), grid, dim3(256), X3Lds<HD>::bytes, s, p); \
     break;
     PREFILL_CASE(16)
     PREFILL_CASE(32)

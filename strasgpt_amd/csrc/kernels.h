@@ -194,7 +194,8 @@ struct AttnParams {
   unsigned* counters;    // [kv_heads], zero between launches
 };
 void attention_prefill(const AttnParams& p, hipStream_t s);
-// variant 0: split-bf16 matrix cores, 1: fp32 matrix cores
+// variant 0: split-bf16 matrix cores (16 or 32 queries per wavefront by the
+// grid size), 1: fp32 matrix cores, 2 / 3: split bf16 with 16 / 32 queries
 void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s);
 // Cache rows [r0, r1) of every kv head of one layer into the bf16 planes the
 // split-bf16 prefill kernel reads (AttnParams khi .. vtlo).

@@ -83,14 +83,16 @@ def test_gemm_tile_shapes(name, tile, model_dir, monkeypatch):
         assert tokens == [int(v) for v in g["generated"]]
 
 
-@pytest.mark.parametrize("kernel", ["x3", "fp32"])
+@pytest.mark.parametrize("kernel", ["x3", "x3-16", "x3-32", "fp32"])
 @pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk"])
 def test_prefill_attention_kernels(name, kernel, model_dir, monkeypatch):
     """Both prefill attention kernels (STRASGPT_PREFILL_ATTN): split-bf16
-    matrix-core products (x3, the default; head_dim 16 pads the 32-dim
-    k-step with zeros) and fp32 matrix-core products, over head_dim 16
-    (tiny-llama) and 32 (tiny-qwen; tiny-chunk: 520 queries, several
-    query blocks and key tiles). Logits and tokens as in test_tiny_golden."""
+    matrix-core products (x3, the default, with 16 or 32 queries per
+    wavefront by the grid size, x3-16 / x3-32 forcing one; head_dim 16 pads
+    the 32-dim k-step with zeros) and fp32 matrix-core products, over
+    head_dim 16 (tiny-llama) and 32 (tiny-qwen; tiny-chunk: 520 queries,
+    several query blocks, a partial last one, and key tiles). Logits and
+    tokens as in test_tiny_golden."""
     rt = runtime()
     g = np.load(os.path.join(GOLDEN_DIR, f"{name}.npz"))
     prompt = [int(v) for v in g["prompt"]]
