@@ -650,6 +650,10 @@ void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
   //   of the bf16 peak in algorithmic flops, QKV 21.2%); with fewer tiles,
   //   or a last round of blocks that leaves more than a quarter of the CUs
   //   idle (320 blocks = 1.25 rounds), part of the chip idles and it loses;
+  //   the gate/up SwiGLU GEMM is the exception from 128 tiles (half the CUs
+  //   in one round): Qwen3-4B shape at M = 512 (152 tiles), 110 us against
+  //   118 for the best 16x16x32 tiles; QKV, O and down at 20-48 tiles lose
+  //   by 1.3-2.1x;
   // * from about 4 blocks of 128 x 256 per CU, 128 x 256 with 32-deep
   //   stages and two blocks per CU (fewest stage bytes per MFMA);
   // * below that, 64 x 128 tiles with 64-deep stages: 128-byte row segments
@@ -670,6 +674,7 @@ void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
   if (!shape) {
     const long rounds = (huge + 255) / 256;  // rounds of one 256 x 256 block per CU
     if (huge >= 192 && 4 * huge >= 3 * 256 * rounds) shape = 7;
+    else if (EPI == GEMM_SWIGLU && huge >= 128 && huge <= 256) shape = 7;
     else if (wide >= 1024) shape = 4;
     else if (p.K % 64 == 0 && small > 256) shape = 5;
     else if (p.K % 64 == 0 && small >= 64) shape = 6;
