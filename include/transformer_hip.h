@@ -31,8 +31,9 @@ typedef struct transformer_timing {
  * next token never leaves HBM between steps. By default the step's
  * kernels are replayed from a captured HIP graph (see
  * transformer_set_decode_mode). Writes step_count token ids to out. Stops
- * early (like the reference) when eos_token_id >= 0 is produced; returns
- * the number of ids written. timing may be NULL. Environment:
+ * early, like the reference, when a decode step produces eos_token_id >= 0
+ * (the token predicted from the prompt is not tested, as in
+ * source/strasgpt.c:217-248); returns the number of ids written. timing may be NULL. Environment:
  * STRASGPT_DECODE_GRAPH=0 launches the step's kernels eagerly instead (for
  * tools that do not follow graph launches). */
 size_t transformer_generate_greedy(

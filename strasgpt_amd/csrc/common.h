@@ -23,4 +23,22 @@
     exit(EXIT_FAILURE);                                                      \
   } while (0)
 
+/* Leading fields of the reference driver's options_t (reference
+ * include/options.h:18-23): the readers taking the driver's options only
+ * need model_dir. */
+#include <stdbool.h>
+struct options_prefix {
+  bool use_prompt_file;
+  char* prompt_file;
+  char* prompt_string;
+  bool pre_tokenized;
+  char* model_dir;
+};
+
+/* tokenizer.json reader of the JSON front-end (safetensors.c): appends the
+ * model.vocab entries of `path` to t; dies if the file is missing or
+ * malformed. */
+struct tokenizer;
+void st_read_tokenizer_json(const char* path, struct tokenizer* t);
+
 #endif

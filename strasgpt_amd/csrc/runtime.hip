@@ -1309,6 +1309,7 @@ extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* toke
                                      size_t steps, int eos, int* out,
                                      transformer_timing_t* timing) {
   Dev* D = t->device;
+  if (T == 0 || steps == 0) ST_DIE("transformer_generate_greedy: needs tokens and steps");
   if (t->state->cached_count + T + (steps - 1) > (size_t)D->ctx)
     ST_DIE("context length exhausted");
   HIP_CHECK(hipMemsetAsync(D->seq_len, 0, sizeof(int), D->stream));
@@ -1319,13 +1320,12 @@ extern "C" size_t sg_generate_greedy(transformer_t* t, size_t T, const int* toke
   HIP_CHECK(hipStreamSynchronize(D->stream));
   harvest(D);
   const double t1 = now_s();
+  // The token predicted from the prompt never ends the loop: the reference
+  // tests only the decode steps' tokens against EOS (source/strasgpt.c:
+  // 217-248).
   size_t produced = 1;
   bool stop = false;
-  if (eos >= 0) {
-    HIP_CHECK(hipMemcpy(D->h_next, D->next, sizeof(int), hipMemcpyDeviceToHost));
-    stop = *D->h_next == eos;
-  }
-  if (steps > 1 && !stop) {
+  if (steps > 1) {
     const bool eager = D->prof || !D->use_graph || D->decode_mode == TRANSFORMER_DECODE_EAGER;
     if (!eager) build_decode_graph(D);
     set_pos(D, t->state->cached_count);
@@ -1380,13 +1380,12 @@ extern "C" size_t sg_generate_sampled(transformer_t* t, size_t T, const int* tok
   HIP_CHECK(hipStreamSynchronize(D->stream));
   harvest(D);
   const double t1 = now_s();
+  // The token predicted from the prompt never ends the loop: the reference
+  // tests only the decode steps' tokens against EOS (source/strasgpt.c:
+  // 217-248).
   size_t produced = 1;
   bool stop = false;
-  if (eos >= 0) {
-    HIP_CHECK(hipMemcpy(D->h_next, D->next, sizeof(int), hipMemcpyDeviceToHost));
-    stop = *D->h_next == eos;
-  }
-  if (steps > 1 && !stop) {
+  if (steps > 1) {
     const bool eager = D->prof || !D->use_graph || D->decode_mode == TRANSFORMER_DECODE_EAGER;
     if (!eager) build_decode_graph(D, false);
     set_pos(D, t->state->cached_count);

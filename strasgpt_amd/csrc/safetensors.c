@@ -16,6 +16,9 @@
  *    (json_parser.y:327-338);
  *  - head_dim defaults to hidden_size / num_attention_heads
  *    (json_parser.y:616-619).
+ * tokenizer.json (json_parser.y:380-446, 626-648): the entries of the
+ * top-level "model" object's "vocab" object, key bytes as written and the
+ * number as a float score, in file order; other members are skipped.
  * Differences, all additive: dtype "U8" is accepted (MXFP4 tensors),
  * num_local_experts / num_experts_per_tok are read, and an array-valued
  * bos/eos_token_id takes its first element (the reference rejects arrays).
@@ -29,18 +32,9 @@
 #include <string.h>
 
 #include "common.h"
+#include "tokenizer.h"
 
 const char* safetensors_type_str[] = {"F16", "BF16", "F32", "U8"};
-
-/* Leading fields of the reference driver's options_t (reference
- * include/options.h:18-23): safetensors_read only needs model_dir. */
-struct options_prefix {
-  bool use_prompt_file;
-  char* prompt_file;
-  char* prompt_string;
-  bool pre_tokenized;
-  char* model_dir;
-};
 
 safetensors_t* safetensors_malloc(void) {
   safetensors_t* s = calloc(1, sizeof(safetensors_t));
@@ -55,6 +49,9 @@ void safetensors_free(safetensors_t* s) {
   for (size_t i = 0; i < s->tensor_count; i++) free(s->tensor[i].name);
   free(s);
 }
+
+static char* read_file(const char* path, size_t* len, bool required);
+static char* read_file_optional(const char* path, size_t* len) { return read_file(path, len, false); }
 
 /* ------------------------------------------------------------------------ */
 /* Minimal JSON reader                                                       */
@@ -396,6 +393,52 @@ static void header_member(json_t* j, const char* key, void* ctx) {
   json_object(j, tensor_member, c);
   t->name = strdup(key);
   c->s->tensor_count++;
+}
+
+/* ------------------------------------------------------------------------ */
+/* tokenizer.json                                                            */
+
+/* Entries of model.vocab in file order (reference json_parser.y:404-446):
+ * key bytes as written, the number as the score. */
+static void vocab_member(json_t* j, const char* key, void* ctx) {
+  tokenizer_t* t = ctx;
+  if (t->token_string_count >= TOKENIZER_MAX_TOKEN_STRING) json_fail(j, "too many token strings");
+  number_t n = json_number(j);
+  char* copy = strdup(key);
+  if (!copy) ST_DIE("malloc failed for token string");
+  t->token_string[t->token_string_count] = copy;
+  t->score[t->token_string_count] = (float)n.fval;
+  t->token_string_count++;
+}
+
+static void tokenizer_model_member(json_t* j, const char* key, void* ctx) {
+  if (strcmp(key, "vocab") != 0) {
+    json_skip(j);
+    return;
+  }
+  tokenizer_t* t = ctx;
+  size_t before = t->token_string_count;
+  json_object(j, vocab_member, t);
+  /* the reference grammar has no empty vocab object (json_parser.y:431) */
+  if (t->token_string_count == before) json_fail(j, "syntax error (empty vocab)");
+}
+
+static void tokenizer_member(json_t* j, const char* key, void* ctx) {
+  if (strcmp(key, "model") != 0) {
+    json_skip(j);
+    return;
+  }
+  if (json_peek(j) != '{') json_fail(j, "syntax error (model is not an object)");
+  json_object(j, tokenizer_model_member, ctx);
+}
+
+void st_read_tokenizer_json(const char* path, tokenizer_t* t) {
+  size_t len;
+  char* text = read_file_optional(path, &len);
+  if (!text) ST_DIE("failed to open tokenizer file");
+  json_t j = {text, text + len, TOKENIZER_FILE, 1};
+  json_object(&j, tokenizer_member, t);
+  free(text);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -1,17 +1,28 @@
 /*
- * strasgpt: greedy generation driver over libstrasgpt_hip, accepting the
- * reference driver's benchmark flags (reference source/options.c:102-224):
- *   -m <dir>  -n <steps>  -t <threads>  -s <seed>  --temp 0
- *   -p <prompt> | -f <file>  with --pre-tokenized (space/comma separated ids)
+ * strasgpt: generation driver over libstrasgpt_hip with the reference
+ * driver's flags and output (reference source/options.c:102-224,
+ * source/strasgpt.c:100-281):
+ *   -m <dir>  -n <steps>  -t <threads>  -s <seed>  --temp <t>  --top-k <k>
+ *   --top-p <p>  --presence-penalty <x>  -p <prompt> | -f <file>
+ *   --pre-tokenized (the prompt is space/comma separated ids, no BOS
+ *   added; otherwise the text is tokenized with tokenizer.json and BOS is
+ *   prepended)
  * plus:
  *   --host-loop   run the reference loop literally (source/strasgpt.c:
  *                 206-252): transformer_predict from every thread of an
- *                 OpenMP team, logits to the host, argmax on the host;
+ *                 OpenMP team, logits to the host, the token chosen by the
+ *                 device argmax (--temp 0) or the device sampler;
+ *   --ids         print the generated ids on one line instead of their
+ *                 strings;
  *   --show-model  print the model summary and exit.
- * Default: transformer_generate_greedy (device-resident decode loop).
- * Generated ids go to stdout, one line; timing lines go to stderr with the
- * reference's boundaries: prefill = first predict over the prompt, decode =
- * sum of the single-token steps (source/strasgpt.c:206-274).
+ * Default: transformer_generate_greedy / transformer_generate_sampled
+ * (device-resident decode loop). Generated token strings go to stdout as
+ * in the reference (the first token always, then up to EOS, printed as
+ * <|end_of_text|>); the tokenizer summary, the prompt tokens and the timing
+ * lines go to stderr with the reference's boundaries: prefill = first
+ * predict over the prompt, decode = sum of the single-token steps
+ * (source/strasgpt.c:206-274). --presence-penalty is range-checked and,
+ * as in the reference (whose sampler_build never reads it), not applied.
  */
 #define _GNU_SOURCE
 #include <omp.h>
@@ -22,6 +33,8 @@
 #include <time.h>
 
 #include "safetensors.h"
+#include "sampler_hip.h"
+#include "tokenizer.h"
 #include "transformer.h"
 #include "transformer_hip.h"
 
@@ -33,8 +46,9 @@ static double now_s(void) {
 
 static void usage(const char* argv0, int status) {
   fprintf(stderr,
-          "Usage: %s -m <model_dir> [-n steps] [-t threads] [--temp 0] "
-          "--pre-tokenized (-p \"ids\" | -f file) [--host-loop] [--show-model]\n",
+          "Usage: %s -m <model_dir> [-n steps] [-t threads] [-s seed] [--temp t] [--top-k k]\n"
+          "       [--top-p p] [--presence-penalty x] (-p <prompt> | -f <file>) [--pre-tokenized]\n"
+          "       [--host-loop] [--ids] [--show-model]\n",
           argv0);
   exit(status);
 }
@@ -60,6 +74,8 @@ static int* parse_ids(const char* text, size_t* count) {
   return ids;
 }
 
+/* Prompt file contents, one trailing newline removed (reference
+ * source/strasgpt.c:133-157). */
 static char* read_text(const char* path) {
   FILE* f = fopen(path, "rb");
   if (!f) {
@@ -70,20 +86,50 @@ static char* read_text(const char* path) {
   long n = ftell(f);
   fseek(f, 0, SEEK_SET);
   char* s = malloc((size_t)n + 1);
-  if (fread(s, 1, (size_t)n, f) != (size_t)n) exit(EXIT_FAILURE);
+  if (!s || fread(s, 1, (size_t)n, f) != (size_t)n) {
+    fprintf(stderr, "[StrasGPT] Error: can't read prompt file\n");
+    exit(EXIT_FAILURE);
+  }
   s[n] = 0;
+  if (n > 0 && s[n - 1] == '\n') s[n - 1] = 0;
   fclose(f);
   return s;
 }
 
+static float parse_float(const char* flag, const char* v, float lo, float hi) {
+  char* end;
+  float x = strtof(v, &end);
+  if (end == v || *end || !(x >= lo && x <= hi)) {
+    fprintf(stderr, "[StrasGPT] Error: %s expects a number in [%g, %g]\n", flag, lo, hi);
+    exit(EXIT_FAILURE);
+  }
+  return x;
+}
+
+/* One generated token to stdout as the reference prints it. Returns false
+ * when it ends the generation (EOS after the first token). */
+static bool emit(tokenizer_t* tk, int id, size_t index, int eos, bool ids_only) {
+  if (ids_only) {
+    printf("%s%d", index ? " " : "", id);
+    return index == 0 || id != eos;
+  }
+  if (index > 0 && id == eos) {
+    fputs(TOKENIZER_STRING_TOKEN_EOS, stdout);
+    return false;
+  }
+  tokenizer_print_token_string(stdout, tokenizer_decode(tk, id));
+  return true;
+}
+
 int main(int argc, char** argv) {
   const char* model = ".";
-  const char* prompt = NULL;
+  const char* prompt = "Once upon a time";
   char* file_text = NULL;
-  size_t steps = 256;
+  size_t steps = 256, top_k = 40;
   int threads = 1;
-  float temp = 1.0f;
-  bool pre_tokenized = false, host_loop = false, show_model = false;
+  unsigned long long seed = 0;
+  float temp = 1.0f, top_p = 0.9f;
+  bool pre_tokenized = false, host_loop = false, show_model = false, ids_only = false;
   for (int i = 1; i < argc; i++) {
     const char* a = argv[i];
     const char* v = i + 1 < argc ? argv[i + 1] : NULL;
@@ -91,50 +137,62 @@ int main(int argc, char** argv) {
     else if (!strcmp(a, "--pre-tokenized")) pre_tokenized = true;
     else if (!strcmp(a, "--host-loop")) host_loop = true;
     else if (!strcmp(a, "--show-model")) show_model = true;
+    else if (!strcmp(a, "--ids")) ids_only = true;
     else if (!v) usage(argv[0], EXIT_FAILURE);
     else if (!strcmp(a, "-m")) model = argv[++i];
     else if (!strcmp(a, "-n")) steps = strtoull(argv[++i], NULL, 10);
     else if (!strcmp(a, "-t")) threads = atoi(argv[++i]);
-    else if (!strcmp(a, "-s")) ++i;
-    else if (!strcmp(a, "--temp")) temp = strtof(argv[++i], NULL);
+    else if (!strcmp(a, "-s")) seed = strtoull(argv[++i], NULL, 10);
+    else if (!strcmp(a, "--temp")) temp = parse_float(a, argv[++i], 0.0f, 1e30f);
+    else if (!strcmp(a, "--top-k")) top_k = strtoull(argv[++i], NULL, 10);
+    else if (!strcmp(a, "--top-p")) top_p = parse_float(a, argv[++i], 0.0f, 1.0f);
+    else if (!strcmp(a, "--presence-penalty")) (void)parse_float(a, argv[++i], 0.0f, 2.0f);
     else if (!strcmp(a, "-p")) prompt = argv[++i];
     else if (!strcmp(a, "-f")) prompt = file_text = read_text(argv[++i]);
     else usage(argv[0], EXIT_FAILURE);
   }
 
+  if (steps == 0) steps = 1; /* the reference always predicts the first token */
   safetensors_t* st = safetensors_read_dir(model);
   if (show_model) {
     safetensors_print_model_infos(stderr, st);
     safetensors_free(st);
     return EXIT_SUCCESS;
   }
-  if (temp != 0.0f) {
-    fprintf(stderr, "[StrasGPT] Error: this driver implements greedy decoding only (--temp 0)\n");
-    return EXIT_FAILURE;
-  }
-  if (!pre_tokenized || !prompt) {
-    fprintf(stderr, "[StrasGPT] Error: pass token ids with --pre-tokenized and -p/-f\n");
-    return EXIT_FAILURE;
-  }
+  tokenizer_t* tk = tokenizer_read_dir(model);
+  tk->bos_token_id = st->bos_token_id;
+  tk->eos_token_id = st->eos_token_id;
+  tokenizer_print(stderr, tk);
+
   size_t n_tok = 0;
-  int* tok = parse_ids(prompt, &n_tok);
+  int* tok = NULL;
+  if (pre_tokenized) tok = parse_ids(prompt, &n_tok);
+  else tokenizer_tokenize(tk, (char*)prompt, true, false, &n_tok, &tok);
   if (n_tok < 1) {
     fprintf(stderr, "[StrasGPT] Error: expected at least 1 prompt token\n");
     return EXIT_FAILURE;
   }
-  int eos = st->eos_token_id;
+  tokenizer_print_tokens(tk, stderr, n_tok, tok, 4);
+  fprintf(stderr, "\n\033[1;34m");
+  for (size_t i = 0; i < n_tok; i++) tokenizer_print_token_string(stderr, tokenizer_decode(tk, tok[i]));
+  fprintf(stderr, "\033[0m");
+  const int eos = st->eos_token_id;
 
   transformer_t* t = transformer_from_safetensors(st);
   transformer_print(stderr, t);
+  sampler_hip_t* smp = NULL;
+  if (temp != 0.0f) smp = sampler_hip_build(t->config->vocabulary_len, temp, top_k, top_p, seed);
 
-  int* out = calloc(steps ? steps : 1, sizeof(int));
+  int* out = calloc(steps, sizeof(int));
   size_t produced = 0;
   double prefill_s = 0, decode_s = 0;
   if (!host_loop) {
     transformer_timing_t tm;
-    produced = transformer_generate_greedy(t, n_tok, tok, steps, eos, out, &tm);
+    produced = smp ? transformer_generate_sampled(t, n_tok, tok, steps, eos, smp, out, &tm)
+                   : transformer_generate_greedy(t, n_tok, tok, steps, eos, out, &tm);
     prefill_s = tm.prefill_s;
     decode_s = tm.decode_s;
+    for (size_t i = 0; i < produced; i++) emit(tk, out[i], i, eos, ids_only);
   } else {
     size_t V = 0;
     float* logits = transformer_logits_malloc(t, 1, &V);
@@ -148,12 +206,10 @@ int main(int argc, char** argv) {
       #pragma omp single
       {
         prefill_s = now_s() - start;
-        size_t best = 0;
-        for (size_t v = 1; v < V; v++)
-          if (logits[v] > logits[best]) best = v;
-        next = (int)best;
-        out[produced++] = next;
-        go = next != eos;
+        next = smp ? (int)sampler_hip_sample(smp, logits, tok[n_tok - 1])
+                   : (int)sampler_argmax(logits, V);
+        out[produced] = next;
+        emit(tk, next, produced++, eos, ids_only);
         start = now_s();
       }
       while (produced < steps && go) {
@@ -161,26 +217,24 @@ int main(int argc, char** argv) {
         #pragma omp single
         {
           decode_s += now_s() - start;
-          size_t best = 0;
-          for (size_t v = 1; v < V; v++)
-            if (logits[v] > logits[best]) best = v;
-          next = (int)best;
-          out[produced++] = next;
-          go = next != eos;
+          next = smp ? (int)sampler_hip_sample(smp, logits, next) : (int)sampler_argmax(logits, V);
+          out[produced] = next;
+          go = emit(tk, next, produced++, eos, ids_only);
           start = now_s();
         }
       }
     }
     free(logits);
   }
-  for (size_t i = 0; i < produced; i++) printf("%s%d", i ? " " : "", out[i]);
   printf("\n");
-  fprintf(stderr, "Prompt processing (prefill): %4zu tokens in %7.3f s (%f token/s)\n", n_tok,
+  fprintf(stderr, "\nPrompt processing (prefill): %4zu tokens in %7.3f s (%f token/s)\n", n_tok,
           prefill_s, n_tok / prefill_s);
   if (produced > 1)
     fprintf(stderr, "Token generation  (decode):  %4zu tokens in %7.3f s (%f token/s)\n",
             produced - 1, decode_s, (produced - 1) / decode_s);
+  if (smp) sampler_hip_free(smp);
   transformer_free(t);
+  tokenizer_free(tk);
   safetensors_free(st);
   free(out);
   free(tok);

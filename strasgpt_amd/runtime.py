@@ -117,6 +117,17 @@ def lib():
     L.transformer_generate_sampled.restype = sz
     L.transformer_generate_sampled.argtypes = [TP, sz, ctypes.POINTER(ctypes.c_int), sz, ctypes.c_int, VP,
                                                ctypes.POINTER(ctypes.c_int), ctypes.POINTER(Timing)]
+    TKP = ctypes.POINTER(TokenizerT)
+    L.tokenizer_read_dir.restype = TKP
+    L.tokenizer_read_dir.argtypes = [ctypes.c_char_p]
+    L.tokenizer_free.argtypes = [TKP]
+    L.tokenizer_decode.restype = ctypes.c_void_p
+    L.tokenizer_decode.argtypes = [TKP, ctypes.c_int]
+    L.tokenizer_tokenize.argtypes = [TKP, ctypes.c_char_p, ctypes.c_bool, ctypes.c_bool,
+                                     ctypes.POINTER(sz), ctypes.POINTER(ip)]
+    L.tokenizer_print.argtypes = [VP, TKP]
+    L.tokenizer_print_tokens.argtypes = [TKP, VP, sz, ip, sz]
+    L.tokenizer_print_token_string.argtypes = [VP, ctypes.c_char_p]
     _LIB = L
     return L
 
@@ -140,6 +151,80 @@ PROFILE_KERNELS = ["qkv_gemv", "attention_decode", "o_gemv", "gate_up_gemv", "do
                    "logits_gemv", "argmax", "moe_route", "moe_gate_up", "moe_down",
                    "qkv_gemm", "attention_prefill", "o_gemm", "gate_up_gemm", "down_gemm",
                    "elementwise", "moe_route_prefill", "moe_gate_up_prefill", "moe_down_prefill"]
+
+
+TOKENIZER_MAX_TOKEN_STRING = 262144
+
+
+class TokenizerIndex(ctypes.Structure):
+    _fields_ = [("token_string", ctypes.c_char_p), ("id", ctypes.c_int)]
+
+
+class TokenizerT(ctypes.Structure):
+    """tokenizer_t (include/tokenizer.h; the reference's field layout)."""
+    _fields_ = [("token_string_count", ctypes.c_size_t),
+                ("token_string", ctypes.c_void_p * TOKENIZER_MAX_TOKEN_STRING),
+                ("score", ctypes.c_float * TOKENIZER_MAX_TOKEN_STRING),
+                ("sorted_token_string", TokenizerIndex * TOKENIZER_MAX_TOKEN_STRING),
+                ("max_token_string_len", ctypes.c_size_t),
+                ("byte_string", ctypes.c_ubyte * 512),
+                ("bos_token_id", ctypes.c_int), ("eos_token_id", ctypes.c_int)]
+
+
+class Tokenizer:
+    """tokenizer_t of a model directory's tokenizer.json: encode text to
+    ids and ids to byte strings with the reference tokenizer's rules
+    (source/tokenizer.c). Host code only."""
+
+    def __init__(self, model_dir: str, bos: int = 0, eos: int = 0):
+        self._lib = lib()
+        self.handle = self._lib.tokenizer_read_dir(model_dir.encode())
+        self.t = self.handle.contents
+        self.t.bos_token_id = bos
+        self.t.eos_token_id = eos
+
+    def __len__(self) -> int:
+        return int(self.t.token_string_count)
+
+    def token_bytes(self, i: int) -> bytes:
+        """Vocabulary entry i after the byte-level map is undone."""
+        return ctypes.string_at(self.t.token_string[i])
+
+    def encode(self, text: bytes, bos: bool = True, eos: bool = False) -> List[int]:
+        n = ctypes.c_size_t(0)
+        out = ctypes.POINTER(ctypes.c_int)()
+        self._lib.tokenizer_tokenize(self.handle, text, bos, eos, ctypes.byref(n), ctypes.byref(out))
+        ids = [out[i] for i in range(n.value)]
+        _libc().free(ctypes.cast(out, ctypes.c_void_p))
+        return ids
+
+    def decode(self, token: int) -> bytes:
+        return ctypes.string_at(self._lib.tokenizer_decode(self.handle, int(token)))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self._lib.tokenizer_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_LIBC = None
+
+
+def _libc():
+    global _LIBC
+    if _LIBC is None:
+        _LIBC = ctypes.CDLL(None)
+        _LIBC.free.argtypes = [ctypes.c_void_p]
+        _LIBC.fopen.restype = ctypes.c_void_p
+        _LIBC.fopen.argtypes = [ctypes.c_char_p, ctypes.c_char_p]
+        _LIBC.fclose.argtypes = [ctypes.c_void_p]
+    return _LIBC
 
 
 class Transformer:

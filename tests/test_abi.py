@@ -9,7 +9,8 @@ import pytest
 from conftest import REPO
 from strasgpt_amd import _paths
 
-HEADERS = ["transformer.h", "transformer_hip.h", "safetensors.h", "sampler_hip.h", "strasgpt_kbench.h"]
+HEADERS = ["transformer.h", "transformer_hip.h", "safetensors.h", "sampler_hip.h", "strasgpt_kbench.h",
+           "tokenizer.h"]
 
 
 def declared_functions():

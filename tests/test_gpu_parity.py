@@ -349,12 +349,76 @@ def test_strasgpt_host_loop_openmp_team(model_dir):
     d = model_dir("tiny-qwen")
     exe = _paths.driver_exe()
     for extra in (["--host-loop", "-t", "8"], []):
-        cmd = [exe, "-m", d, "-n", str(len(want)), "--temp", "0", "--pre-tokenized", "-p", prompt] + extra
+        cmd = [exe, "-m", d, "-n", str(len(want)), "--temp", "0", "--pre-tokenized", "-p", prompt,
+               "--ids"] + extra
         r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
         log(f"strasgpt {' '.join(extra) or '(device loop)'}: rc {r.returncode} out {r.stdout.strip()}")
         assert r.returncode == 0, r.stderr[-2000:]
         assert [int(v) for v in r.stdout.split()] == want
         assert "Prompt processing (prefill)" in r.stderr
+
+
+def test_strasgpt_text_prompt_and_token_strings(model_dir):
+    """Without --pre-tokenized the driver tokenizes the text with the
+    model's tokenizer.json and prepends BOS (source/strasgpt.c:169-172),
+    then prints the generated tokens' strings (source/strasgpt.c:217-247):
+    the same ids as a --pre-tokenized run on the library tokenizer's
+    encoding, and their strings on stdout."""
+    import json
+    from strasgpt_amd import _paths
+    rt = runtime()
+    d = model_dir("tiny-qwen")
+    cfg = json.load(open(os.path.join(d, "config.json")))
+    bos, eos = cfg["bos_token_id"], cfg["eos_token_id"]
+    tk = rt.Tokenizer(d, bos, eos)
+    text = "<5> a"
+    prompt_ids = tk.encode(text.encode(), bos=True)
+    exe = _paths.driver_exe()
+    n = 10
+    assert len(prompt_ids) + n - 1 <= cfg["max_position_embeddings"]
+    ids_cmd = [exe, "-m", d, "-n", str(n), "--temp", "0", "--pre-tokenized", "-p",
+               " ".join(map(str, prompt_ids)), "--ids"]
+    r = subprocess.run(ids_cmd, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    ids = [int(v) for v in r.stdout.split()]
+    expect = tk.decode(ids[0])
+    for i in ids[1:]:
+        if i == eos:
+            expect += b"<|end_of_text|>"
+            break
+        expect += tk.decode(i)
+    txt_cmd = [exe, "-m", d, "-n", str(n), "--temp", "0", "-p", text]
+    r = subprocess.run(txt_cmd, capture_output=True, timeout=120)
+    out = r.stdout.decode("latin-1")
+    log(f"strasgpt text prompt: {len(prompt_ids)} prompt ids, rc {r.returncode} out {out[:120]!r}")
+    err = r.stderr.decode("latin-1")
+    assert r.returncode == 0, err[-2000:]
+    assert f"Tokens ({len(prompt_ids)}):" in err
+    assert out.rstrip("\n") == expect.decode("latin-1")
+    assert "Prompt processing (prefill): %4d tokens" % len(prompt_ids) in err
+    tk.close()
+
+
+def test_first_token_eos_does_not_stop(model_dir):
+    """The reference tests only decode steps' tokens against EOS
+    (source/strasgpt.c:217-248): an EOS predicted from the prompt is kept
+    and generation goes on; a later EOS ends it after being written."""
+    g = np.load(os.path.join(GOLDEN_DIR, "tiny-qwen.npz"))
+    prompt = [int(v) for v in g["prompt"]]
+    want = [int(v) for v in g["generated"]]
+    rt = runtime()
+    with rt.Transformer(model_dir("tiny-qwen")) as t:
+        eos = want[0]
+        later = [k for k in range(1, len(want)) if want[k] == eos]
+        expect = want[:later[0] + 1] if later else want
+        got, _ = t.generate(prompt, steps=len(want), eos=eos)
+        log(f"eos {eos}: got {len(got)} ids, expected {len(expect)}")
+        assert list(got) == expect
+        t.reset()
+        eos = want[3]
+        k = min(i for i in range(1, len(want)) if want[i] == eos)
+        got, _ = t.generate(prompt, steps=len(want), eos=eos)
+        assert list(got) == want[:k + 1]
 
 
 @pytest.mark.parametrize("hook", ["strasgpt_kbench_mxfp4_decode", "strasgpt_kbench_mxfp4_decode_bf16"])
