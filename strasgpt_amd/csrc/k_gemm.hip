@@ -44,17 +44,46 @@ __device__ __forceinline__ void store_split(uint16_t* hi, uint16_t* lo, size_t i
 
 // Block -> (m tile, n tile). Blocks are dispatched round-robin over the
 // XCDs; renumber so that each XCD receives a contiguous range of tiles.
-// Tiles are ordered in groups of kGroupM row tiles: within a group m runs
-// fastest, then n. The blocks resident on one XCD at a time then cover a
-// few row tiles x a few column tiles (about 8 x 4), so each A and W tile
-// fetched into that XCD's L2 serves several blocks; with every row tile in
-// flight at once (m fastest over all of M) each A tile would be fetched once
-// per block.
+// Order 0 (the 16x16x32 kernels): tiles in groups of kGroupM row tiles,
+// m fastest within a group, then n; the blocks resident on one XCD at a
+// time cover about 8 row tiles x 4 column tiles, so each A and W tile
+// fetched into that XCD's L2 serves several blocks (with every row tile in
+// flight at once, m fastest over all of M, each A tile would be fetched
+// once per block).
+// The 256 x 256 kernel (order 3 by default; STRASGPT_GEMM_ORDER forces 0-3
+// for measurements and tests): the tile grid is cut into 2 x 4 rectangles,
+// one per XCD, each walked m fastest within groups of 4 row tiles, so the
+// 32 blocks resident on an XCD cover 4 row tiles x 8 column tiles. Per
+// K step they then fetch 4 A tiles (32 KiB each as hi + lo planes) and 8 W
+// tiles (16 KiB) instead of 8 and 4: 256 instead of 320 KiB. Measured on
+// the Mistral-Small-24B shape at 2048 tokens: down (split-K, 8 x 20 tiles
+// per split) 1296 -> 1061 us, gate/up 2073 -> 2013 us, prefill +7.7%;
+// neutral on Llama-3.1-8B at 8192 tokens and Qwen3-4B at 512. Order 1
+// (whole row panels per XCD) and order 2 (rectangles walked m fastest over
+// the whole rectangle: 16 x 2 at 8192 tokens) measured no better than 0.
 constexpr int kGroupM = 8;
-__device__ __forceinline__ void tile_of(int mt, int nt, int& m_tile, int& n_tile) {
+__device__ __forceinline__ void tile_of(int mt, int nt, int& m_tile, int& n_tile, int order = 0) {
   const int b = blockIdx.x, total = mt * nt;
   int t = b;
   if (total % kXcds == 0) t = (b % kXcds) * (total / kXcds) + b / kXcds;
+  if (order == 1 && total % kXcds == 0) {
+    // row panels: each XCD takes whole rows of tiles, n fastest (one A
+    // panel shared by every block of the XCD)
+    m_tile = t / nt;
+    n_tile = t % nt;
+    return;
+  }
+  if (order >= 2 && total % kXcds == 0 && mt % 2 == 0 && nt % 4 == 0) {
+    // the tile grid cut into 2 x 4 rectangles, one per XCD, each walked
+    // m fastest (order 2), or m fastest within groups of 4 row tiles
+    // (order 3)
+    const int rm = mt / 2, rn = nt / 4, x = t / (rm * rn), in = t % (rm * rn);
+    const int gm = order == 3 ? 4 : rm, g = in / (gm * rn), rows = min(gm, rm - g * gm);
+    const int local = in - g * gm * rn;
+    m_tile = (x / 4) * rm + g * gm + local % rows;
+    n_tile = (x % 4) * rn + local / rows;
+    return;
+  }
   const int group = t / (kGroupM * nt), first = group * kGroupM;
   const int rows = min(kGroupM, mt - first), in = t - group * kGroupM * nt;
   m_tile = first + in % rows;
@@ -379,7 +408,7 @@ __global__ __launch_bounds__(NW * WAVE, OCC) void gemm3_kernel(GemmParams p) {
   const int cols = DUAL ? BN / 2 : BN;
   const int mtiles = (p.M + BM - 1) / BM, ntiles = (p.N + cols - 1) / cols;
   int m_tile, n_tile;
-  tile_of(mtiles, ntiles, m_tile, n_tile);
+  tile_of(mtiles, ntiles, m_tile, n_tile, p.order);
   const int m0 = m_tile * BM, n0 = n_tile * cols;
   const int M = p.M, N = p.N, K = p.K;
   const int ksplit = gridDim.z, kper = ((K + KS - 1) / KS + ksplit - 1) / ksplit * KS;
@@ -591,7 +620,10 @@ __global__ __launch_bounds__(NW * WAVE, OCC) void gemm3_kernel(GemmParams p) {
 }
 
 template <int BM, int BN, int NS, int EPI, int PREC, int NW, int KS, int OCC = 1>
-void launch3(const GemmParams& p, int splits, hipStream_t s) {
+void launch3(const GemmParams& p0, int splits, hipStream_t s) {
+  static const int order = getenv("STRASGPT_GEMM_ORDER") ? atoi(getenv("STRASGPT_GEMM_ORDER")) : 3;
+  GemmParams p = p0;
+  p.order = order;
   const int cols = EPI == GEMM_SWIGLU ? BN / 2 : BN;
   const int tiles = ((p.N + cols - 1) / cols) * ((p.M + BM - 1) / BM);
   constexpr size_t shm = (size_t)NS * (BM * (PREC == GEMM_SPLIT2 ? 2 : 1) + BN) * 2 * KS;

@@ -126,6 +126,7 @@ struct GemmParams {
   // keys into kstage [M][kv_dim] fp32 (qk_norm_rope rounds them after RoPE)
   int kv_bf16;
   float* kstage;
+  int order;           // tile order of the 256 x 256 kernel (set by the launcher)
 };
 void gemm(const GemmParams& p, int epilogue, int precision, int splits, hipStream_t s);
 // Split-K factor that fills the CUs for an M x N output (1: no split).

@@ -110,6 +110,10 @@ TINY: Dict[str, ModelShape] = {
     "mid-moe": ModelShape("mid-moe", 2880, 2880, 2, 8, 2, 64, 512, 150000.0, 1e-5, 6, 10,
                           untied=True, experts=8, experts_per_tok=4, model_type="stras_moe",
                           std=0.02),
+    # Prefill GEMM grids that the 256 x 256 kernel's XCD rectangles divide
+    # (512 rows: 2 row tiles; QKV 12, O 4, gate/up 16, down 4 column tiles).
+    "mid-dense": ModelShape("mid-dense", 1024, 2048, 1, 8, 8, 128, 512, 500000.0, 1e-5,
+                            512, 4, ctx=600, untied=True, std=0.02),
     # Interleaved RoPE pairs (2j, 2j + 1), written as
     # rope_scaling.mrope_interleaved = true, with QK RMSNorm.
     "tiny-rope-il": ModelShape("tiny-rope-il", 96, 192, 3, 6, 2, 32, 300, 10000.0, 1e-5,

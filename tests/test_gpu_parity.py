@@ -83,6 +83,40 @@ def test_gemm_tile_shapes(name, tile, model_dir, monkeypatch):
         assert tokens == [int(v) for v in g["generated"]]
 
 
+def test_gemm_tile_orders(model_dir, monkeypatch):
+    """The 256 x 256 prefill GEMM under each tile order (STRASGPT_GEMM_ORDER
+    0-3; 3 is the default) on grids its XCD rectangles divide: the order only
+    changes which block computes a tile, so every order gives bit-identical
+    logits, which agree with the oracle."""
+    rt = runtime()
+    d = model_dir("mid-dense")
+    shp = synth.shape("mid-dense")
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, PROMPT_SEED)
+    ol = oracle_model(d, 16).predict(prompt)
+    monkeypatch.setenv("STRASGPT_GEMM_TILE", "256x256")
+    got = {}
+    for order in ("0", "1", "2", "3"):
+        # the order is read once per process: each runs in a child
+        code = textwrap.dedent(f"""
+            import sys, numpy as np
+            sys.path.insert(0, {REPO!r})
+            from strasgpt_amd import runtime as rt
+            with rt.Transformer({d!r}) as t:
+                np.save(sys.argv[1], t.predict({list(prompt)!r}))
+        """)
+        out = os.path.join(d, f"order{order}.npy")
+        env = dict(os.environ, STRASGPT_GEMM_ORDER=order)
+        r = subprocess.run([sys.executable, "-c", code, out], env=env, capture_output=True, text=True,
+                           timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        got[order] = np.load(out)
+        err = float(np.abs(got[order] - ol).max())
+        log(f"mid-dense order {order}: max |logit error| {err:.3g}")
+        np.testing.assert_allclose(got[order], ol, rtol=RTOL, atol=ATOL)
+    for order in ("1", "2", "3"):
+        assert np.array_equal(got[order], got["0"])
+
+
 @pytest.mark.parametrize("kernel", ["x3", "x3-16", "x3-32", "fp32"])
 @pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk"])
 def test_prefill_attention_kernels(name, kernel, model_dir, monkeypatch):
