@@ -344,16 +344,30 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int EPI, bool NORM, bool EXACT, int kPD>
+// SPLIT (residual epilogue, no RMSNorm): block (x, y) takes the rows of x
+// over K range y of gridDim.y ranges of whole steps: its row sums are
+// partial sums, stored agent-coherently to p.part[y][n]; the last of the
+// gridDim.y blocks of a row range to arrive (counter p.counters[x]) adds
+// them in range order, y[n] += (part[0][n] + part[1][n]) + ..., and resets
+// the counter. Rows longer than an LDS stage (64 KiB of fp32) take this
+// path: each block stages only its range.
+template <int EPI, bool NORM, bool EXACT, int kPD, bool SPLIT = false>
 __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   constexpr int NT = kThreads, WV = kWaves;
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [S * kStep], zero past K
   __shared__ float red[WV];
+  __shared__ int last;
   constexpr bool DUAL = EPI == GEMV_SWIGLU;
+  static_assert(!SPLIT || (EPI == GEMV_RESIDUAL && !NORM), "split-K rows: residual epilogue only");
   constexpr int LOADS = kPD * (DUAL ? 2 : 1);  // ring loads issued before the staging wait
   const int lane = threadIdx.x % WAVE;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
-  const int K = p.K, N = p.N;
+  const int N = p.N, KR = p.K;  // KR: row length (stride of the weight rows)
+  const int SR = (KR + kStep - 1) / kStep, SP = SPLIT ? (SR + gridDim.y - 1) / gridDim.y : SR;
+  const int kbeg = SPLIT ? blockIdx.y * SP * kStep : 0;
+  const int K = SPLIT ? min(KR - kbeg, SP * kStep) : KR;  // this block's K range
+  const float* x = p.x + kbeg;
+  const uint16_t* wbase = p.w + kbeg;
   const int S = (K + kStep - 1) / kStep;
   const int groups = (N + WV - 1) / WV;
   const int G = gridDim.x, per = (groups + G - 1) / G;
@@ -377,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   for (int u0 = wave * WAVE; u0 < slots; u0 += NT) {
     const int u = u0 + lane;
     if (u < slots)  // inactive lanes write nothing
-      __builtin_amdgcn_global_load_lds((const void*)(p.x + u * 4), (lds_ptr_t)(xs + u0 * 4), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(x + u * 4), (lds_ptr_t)(xs + u0 * 4), 16, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);  // the row's DMA is issued before the ring loads
   // 3. the ring
@@ -388,9 +402,9 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
     const bool past = rrow >= nrows;  // wave-uniform
     const size_t row = (size_t)min((g0 + rrow) * WV + wave, N - 1);
     const int k = EXACT ? rstep * kStep + lk : min(rstep * kStep + lk, K - 8);
-    const uint16_t* wa = past ? (const uint16_t*)p.x + lk : p.w + row * K + k;
+    const uint16_t* wa = past ? (const uint16_t*)p.x + lk : wbase + row * KR + k;
     a = load_nt_u4(wa);
-    if (DUAL) b = load_nt_u4(past ? wa : p.w2 + row * K + k);
+    if (DUAL) b = load_nt_u4(past ? wa : p.w2 + row * KR + k);
     if (++rstep == S) {
       rstep = 0;
       rrow++;
@@ -455,7 +469,11 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
         if (DUAL) acc2 = dot8(b, xa, xb, acc2);
         if (++step == S) {
           const float r1 = wave_total(acc), r2 = DUAL ? wave_total(acc2) : 0.0f;
-          if (lane == 0) gemv_store<EPI>(p, (g0 + rowi) * WV + wave, r1, r2);
+          const int n = (g0 + rowi) * WV + wave;
+          if (lane == 0) {
+            if (SPLIT) cstore(p.part + (size_t)blockIdx.y * N + n, r1);
+            else gemv_store<EPI>(p, n, r1, r2);
+          }
           acc = acc2 = 0.0f;
           step = 0;
           rowi++;
@@ -464,7 +482,27 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
       load(w[j], w2[DUAL ? j : 0]);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // no load left in flight at exit
+  __builtin_amdgcn_s_waitcnt(0);  // no load left in flight, every partial stored
+  if (!SPLIT) return;
+  // Hand-off (the decode attention's): partials are written and read only
+  // by agent-scope relaxed atomic accesses, every store of the block has
+  // completed before the counter increment is issued, and the last block
+  // reads after its own increment has returned.
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned done = __hip_atomic_fetch_add(p.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    last = done == gridDim.y - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  const int n_end = min(N, min(groups, g0 + per) * WV);
+  for (int n = g0 * WV + (int)threadIdx.x; n < n_end; n += NT) {
+    float sum = cload(p.part + n);
+    for (int y = 1; y < (int)gridDim.y; y++) sum += cload(p.part + (size_t)y * N + n);
+    p.y[n] += sum;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(p.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Blocks: at most `cap`, the same number of row groups for each block, and
@@ -550,6 +588,32 @@ bool launch_v3(const GemvParams& p, hipStream_t s, int cap) {
   return true;
 }
 
+// The split-K third form for rows longer than an LDS stage (residual
+// epilogue without RMSNorm): ranges of at most kSplitSteps steps (32 KiB of
+// fp32 row per block, so several blocks per CU), blockIdx.y = the range.
+// Mistral-Small-24B down projection (K = 32768, 4 ranges): 57.5-58 us
+// against 60.2 for the chunked form (row read from L2 per step); 256, 512
+// or 768 row blocks per range measured the same.
+constexpr int kSplitSteps = 16;
+constexpr int kSplitMax = 8;  // ranges: K <= 65536
+template <int PD>
+bool launch_v3_split(const GemvParams& p, hipStream_t s, int cap) {
+  const int S = (p.K + kStep - 1) / kStep;
+  const int ranges = (S + kSplitSteps - 1) / kSplitSteps;
+  if (!p.part || !p.counters || p.norm_w || ranges < 2 || ranges > kSplitMax) return false;
+  const int SP = (S + ranges - 1) / ranges;
+  const size_t shm = (size_t)SP * kStep * sizeof(float);
+  const int groups = (p.N + kWaves - 1) / kWaves;
+  const int blocks = balanced_blocks(groups, cap);
+  if (blocks > kGemvCounters) ST_DIE("GEMV split-K: more row ranges than counters");
+  const bool exact = p.K % (SP * kStep) == 0;
+  if (exact) hipLaunchKernelGGL((gemv3_kernel<GEMV_RESIDUAL, false, true, PD, true>), dim3(blocks, ranges),
+                                dim3(kThreads), shm, s, p);
+  else hipLaunchKernelGGL((gemv3_kernel<GEMV_RESIDUAL, false, false, PD, true>), dim3(blocks, ranges),
+                          dim3(kThreads), shm, s, p);
+  return true;
+}
+
 template <int R, int U, int EPI>
 void launch(const GemvParams& p, hipStream_t s, int cap) {
   const bool lds = p.K <= kMaxLdsK;
@@ -581,7 +645,8 @@ void gemv(const GemvParams& p, int epi, hipStream_t s) {
   // Forms and launch shapes from sweeps of the decode shapes on MI355X
   // (weights streamed from HBM, back-to-back launches): the third form
   // (row staged by DMA) where it was faster, else the flat-stream form,
-  // else the chunked form (rows beyond 64 KiB).
+  // else, for rows beyond 64 KiB, the split-K third form (residual rows
+  // given the scratch) or the chunked form.
   switch (epi) {
     case GEMV_STORE:  // logits
       if (!launch_v3<GEMV_STORE, 4>(p, s, 8192) && !launch_v2<GEMV_STORE, 8>(p, s, 2048))
@@ -589,7 +654,7 @@ void gemv(const GemvParams& p, int epi, hipStream_t s) {
       break;
     case GEMV_RESIDUAL:  // O and down projections
       if (!(p.N >= 2560 && launch_v3<GEMV_RESIDUAL, 4>(p, s, 768)) &&
-          !launch_v2<GEMV_RESIDUAL, 8>(p, s, 256))
+          !launch_v2<GEMV_RESIDUAL, 8>(p, s, 256) && !launch_v3_split<8>(p, s, 256))
         launch<1, 4, GEMV_RESIDUAL>(p, s, 4096);
       break;
     case GEMV_QKV:

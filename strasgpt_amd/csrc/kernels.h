@@ -36,7 +36,14 @@ struct GemvParams {
   const int* pos;  // device: cache position of this step
   int q_dim, kv_dim, head_dim, ctx;
   int kv_bf16;     // the cache stores bf16 (round to nearest even)
+  // Split-K scratch for rows longer than one LDS stage (residual epilogue):
+  // partial sums [ranges][N] and one arrival counter per block, zero
+  // between launches (kGemvCounters of them). Without it such rows take the
+  // chunked form.
+  float* part;
+  unsigned* counters;
 };
+constexpr int kGemvCounters = 4096;
 void gemv(const GemvParams& p, int epilogue, hipStream_t s);
 
 // MXFP4 expert GEMV rows (decode MoE). Rows of expert e are

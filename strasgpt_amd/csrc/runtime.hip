@@ -157,6 +157,8 @@ struct transformer_device {
   float* attn_part = nullptr;
   int attn_splits = 0;
   unsigned* attn_cnt = nullptr;  // [kvh] decode attention arrivals
+  float* gemv_part = nullptr;    // [8][d] split-K GEMV partial sums (rows > 16384)
+  unsigned* gemv_cnt = nullptr;  // [kGemvCounters] their arrival counters
   float* am_v = nullptr;
   int* am_i = nullptr;
   int* h_tok = nullptr;
@@ -578,6 +580,8 @@ void layer_decode(Dev* D, int l) {
     dn.N = D->d;
     dn.K = D->H;
     dn.y = D->x;
+    dn.part = D->gemv_part;
+    dn.counters = D->gemv_cnt;
     {
       Prof pr(D, K_DOWN_GEMV, d * D->H * 2, 2.0 * d * D->H);
       sg::gemv(dn, sg::GEMV_RESIDUAL, s);
@@ -1179,6 +1183,9 @@ extern "C" transformer_t* sg_from_safetensors(struct safetensors* st) {
   D->attn_part = dalloc<float>((size_t)D->qh * D->attn_splits * (hd + 2));
   D->attn_cnt = dalloc<unsigned>(D->kvh);
   HIP_CHECK(hipMemset(D->attn_cnt, 0, D->kvh * sizeof(unsigned)));
+  D->gemv_part = dalloc<float>((size_t)8 * D->d);
+  D->gemv_cnt = dalloc<unsigned>(sg::kGemvCounters);
+  HIP_CHECK(hipMemset(D->gemv_cnt, 0, sg::kGemvCounters * sizeof(unsigned)));
   sg::attention_init();
   D->am_v = dalloc<float>(sg::argmax_blocks());
   D->am_i = dalloc<int>(sg::argmax_blocks());
@@ -1227,7 +1234,7 @@ extern "C" void sg_free(transformer_t* t) {
     }
     void* bufs[] = {D->x, D->xn, D->q, D->att, D->act, D->kraw, D->logits, D->kc, D->vc,
                     D->rope, D->tok, D->pos, D->next, D->seq, D->seq_len, D->attn_part, D->attn_cnt,
-                    D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
+                    D->gemv_part, D->gemv_cnt, D->am_v, D->am_i, D->cap_dev, D->cap_final_dev,
                     D->kp_hi, D->kp_lo, D->vt_hi, D->vt_lo,
                     D->moe_sel, D->moe_w, D->moe_act, D->moe_logits, D->moe_offs, D->moe_order, D->moe_out,
                     D->moe_ahi, D->moe_alo,

@@ -114,6 +114,13 @@ TINY: Dict[str, ModelShape] = {
     # (512 rows: 2 row tiles; QKV 12, O 4, gate/up 16, down 4 column tiles).
     "mid-dense": ModelShape("mid-dense", 1024, 2048, 1, 8, 8, 128, 512, 500000.0, 1e-5,
                             512, 4, ctx=600, untied=True, std=0.02),
+    # FFN rows longer than one LDS stage of the decode GEMV (64 KiB of
+    # fp32): the down projection takes the split-K form, in 3 ranges of
+    # 14 steps (20480 = 40 steps of 512, the last range short) or 4 of 16.
+    "tiny-wide": ModelShape("tiny-wide", 64, 20480, 2, 4, 2, 16, 256, 10000.0, 1e-5,
+                            8, 6, std=0.05),
+    "tiny-wide2": ModelShape("tiny-wide2", 64, 32768, 1, 4, 2, 16, 256, 10000.0, 1e-5,
+                             8, 6, std=0.05),
     # Interleaved RoPE pairs (2j, 2j + 1), written as
     # rope_scaling.mrope_interleaved = true, with QK RMSNorm.
     "tiny-rope-il": ModelShape("tiny-rope-il", 96, 192, 3, 6, 2, 32, 300, 10000.0, 1e-5,

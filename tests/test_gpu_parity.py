@@ -239,7 +239,7 @@ def test_prefill_after_decode_steps(name, model_dir):
 
 
 @pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk", "tiny-long",
-                                  "tiny-rope-il", "tiny-rope-il128"])
+                                  "tiny-rope-il", "tiny-rope-il128", "tiny-wide"])
 def test_decode_modes_agree(name, model_dir):
     """The graph-replayed decode step and the same kernels launched eagerly
     give identical greedy tokens, equal to the oracle's; a second graph run
@@ -267,7 +267,7 @@ def test_decode_modes_agree(name, model_dir):
     assert again == otok
 
 
-@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-rope-il128"])
+@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-rope-il128", "tiny-wide", "tiny-wide2"])
 def test_decode_step_logits(name, model_dir):
     """Single-token transformer_predict calls (decode GEMVs, split-K
     attention over the cache, final norm): logits at each of several
