@@ -302,10 +302,15 @@ def main():
         flops = sum(v["flops"] for v in pre.values())
         ms = sum(v["total_ms"] for v in pre.values())
         tf = flops / (ms * 1e-3) / 1e12
+        # bf16x2 issues two bf16 MFMAs per product (activations as hi + lo
+        # planes): the matrix cores execute twice the algorithmic FLOP
+        issue = 2 if args.precision == 0 else 1
         roofline_prefill = {"kernels": sorted(pre), "bound": "mfma", "achieved": round(tf, 1),
                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                             "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                            "precision": "bf16x2" if args.precision == 0 else "bf16"}
+                            "precision": "bf16x2" if args.precision == 0 else "bf16",
+                            "mfma_issued_tflops": round(issue * tf, 1),
+                            "mfma_issued_frac": round(issue * tf / BF16_PEAK_TFLOPS, 4)}
     decode_tok_s = decode_n / decode_s
     prefill_tok_s = args.steps * len(prompt) / prefill_s
     decode_bytes = sum(v["bytes"] for k, v in stats.items() if k in decode_kernels)
