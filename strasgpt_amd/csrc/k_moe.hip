@@ -613,6 +613,66 @@ __global__ void mxfp4_decode_kernel(const uint8_t* codes, const uint8_t* scales,
 
 constexpr int GBM = 32, GBN = 64, GBK = 32, GLD = 40;  // LDS row stride (bf16)
 
+// The same with the expert ids staged in LDS once (n <= kGroup2MaxN, E <=
+// 64): wave w takes a contiguous run of slots, 64 ids at a time in
+// registers, and lane e keeps expert e's count (one ballot per expert);
+// lane e of wave 0 turns the counts into each run's first position within
+// expert e (runs in order, so the slots of an expert stay increasing), and
+// each wave scatters its run. group_kernel below re-reads the ids for
+// every expert in dependent steps.
+constexpr int kGroup2MaxN = 32768;
+__global__ __launch_bounds__(1024) void group2_kernel(const int* sel, int n, int E, int* offs, int* order) {
+  extern __shared__ int ids[];       // [n]
+  __shared__ int cnt[16][WAVE];      // hits per (wave run, expert), then first positions
+  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  for (int i = threadIdx.x; i < n; i += 1024) ids[i] = sel[i];
+  __syncthreads();
+  const int groups = (n + WAVE - 1) / WAVE, per = (groups + 15) / 16;
+  const int b0 = wave * per * WAVE, b1 = min(n, (wave + 1) * per * WAVE);
+  int mine = 0;  // lane e: hits of expert e in this wave's run
+  for (int b = b0; b < b1; b += WAVE) {
+    const int v = b + lane < b1 ? ids[b + lane] : -1;
+    for (int e = 0; e < E; e++) {
+      const int c = __popcll(__ballot(v == e));
+      if (lane == e) mine += c;
+    }
+  }
+  if (lane < E) cnt[wave][lane] = mine;
+  __syncthreads();
+  if (wave == 0) {
+    int tot = 0;
+    if (lane < E)
+      for (int w = 0; w < 16; w++) tot += cnt[w][lane];
+    // exclusive prefix over experts (lanes)
+    int inc = tot;
+    for (int off = 1; off < WAVE; off <<= 1) {
+      const int y = __shfl_up(inc, off, WAVE);
+      if (lane >= off) inc += y;
+    }
+    int run = inc - tot;
+    if (lane < E) {
+      offs[lane] = run;
+      for (int w = 0; w < 16; w++) {
+        const int c = cnt[w][lane];
+        cnt[w][lane] = run;
+        run += c;
+      }
+    }
+    if (lane == E - 1) offs[E] = inc;
+  }
+  __syncthreads();
+  int next = lane < E ? cnt[wave][lane] : 0;  // lane e: next position of expert e
+  for (int b = b0; b < b1; b += WAVE) {
+    const int v = b + lane < b1 ? ids[b + lane] : -1;
+    for (int e = 0; e < E; e++) {
+      const unsigned long long m = __ballot(v == e);
+      const int pos = __builtin_amdgcn_readlane(next, e);
+      if (v == e) order[pos + __popcll(m & ((1ull << lane) - 1))] = b + lane;
+      if (lane == e) next += __popcll(m);
+    }
+  }
+}
+
 // order[offs[e] .. offs[e+1]) = the slots routed to expert e, increasing.
 __global__ __launch_bounds__(1024) void group_kernel(const int* sel, int n, int E, int* offs, int* order) {
   extern __shared__ int cnt[];  // [E + 1]
@@ -1208,7 +1268,17 @@ namespace sg {
 
 void moe_group(const int* sel, int n, int E, int* offs, int* order, hipStream_t s) {
   if (n <= 0 || E <= 0 || E > 1024) ST_DIE("MoE grouping needs slots and 1 <= E <= 1024");
-  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), (E + 1) * sizeof(int), s, sel, n, E, offs, order);
+  if (E <= WAVE && n <= kGroup2MaxN) {
+    static bool attr = false;
+    if (!attr) {
+      HIP_CHECK(hipFuncSetAttribute((const void*)group2_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)(kGroup2MaxN * sizeof(int))));
+      attr = true;
+    }
+    hipLaunchKernelGGL(group2_kernel, dim3(1), dim3(1024), (size_t)n * sizeof(int), s, sel, n, E, offs, order);
+  } else {
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), (E + 1) * sizeof(int), s, sel, n, E, offs, order);
+  }
   HIP_CHECK(hipGetLastError());
 }
 
