@@ -222,9 +222,11 @@ def main():
 
     t0 = time.time()
     t = runtime.Transformer(d)
+    load_s = time.time() - t0
+    load_bytes = sum(os.path.getsize(os.path.join(d, f)) for f in os.listdir(d) if f.endswith(".safetensors"))
     t.set_prefill_precision(args.precision)
     t.set_kv_cache_format(runtime.KV_BF16 if args.kv_cache == "bf16" else runtime.KV_FP32)
-    log(f"loaded into HBM in {time.time() - t0:.1f}s; {runtime.version()}")
+    log(f"loaded into HBM in {load_s:.1f}s ({load_bytes / load_s / 1e9:.1f} GB/s); {runtime.version()}")
 
     if args.probe_traffic:
         probe_traffic(t, prompt)
@@ -331,6 +333,12 @@ def main():
         "decode_effective_gbs": round(decode_bytes / ntok / (decode_s / decode_n) / 1e9, 1),
         "roofline": roofline,
         "roofline_prefill": roofline_prefill,
+        # transformer_from_safetensors: headers parsed, tensors read with
+        # pread into pinned staging buffers and uploaded while the next one
+        # is read (the files were just written, so they come from the page
+        # cache)
+        "model_load": {"seconds": round(load_s, 2), "file_bytes": load_bytes,
+                       "gbs": round(load_bytes / load_s / 1e9, 2)},
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
                         for kk, vv in v.items()} for k, v in kernels.items()},
         "tokens_head": tokens[:8],
