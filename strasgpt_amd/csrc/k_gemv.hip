@@ -592,8 +592,9 @@ bool launch_v3(const GemvParams& p, hipStream_t s, int cap) {
 // epilogue without RMSNorm): ranges of at most kSplitSteps steps (32 KiB of
 // fp32 row per block, so several blocks per CU), blockIdx.y = the range.
 // Mistral-Small-24B down projection (K = 32768, 4 ranges): 57.5-58 us
-// against 60.2 for the chunked form (row read from L2 per step); 256, 512
-// or 768 row blocks per range measured the same.
+// against 60.2 for the chunked form (row read from L2 per step); 128-768
+// row blocks per range, 4-16 steps in flight and ranges of 8 or 32 steps
+// measured the same.
 constexpr int kSplitSteps = 16;
 constexpr int kSplitMax = 8;  // ranges: K <= 65536
 template <int PD>
