@@ -30,6 +30,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/resource.h>
 #include <time.h>
 
 #include "safetensors.h"
@@ -227,6 +228,10 @@ int main(int argc, char** argv) {
     free(logits);
   }
   printf("\n");
+  // host peak resident set (Linux: ru_maxrss in KiB), as the reference reports it
+  struct rusage ru;
+  const double rss_gb = getrusage(RUSAGE_SELF, &ru) == 0 ? ru.ru_maxrss / (1024.0 * 1024.0) : -1.0;
+  fprintf(stderr, "\nMax memory used (RSS): %.2f GB", rss_gb);
   fprintf(stderr, "\nPrompt processing (prefill): %4zu tokens in %7.3f s (%f token/s)\n", n_tok,
           prefill_s, n_tok / prefill_s);
   if (produced > 1)
