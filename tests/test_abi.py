@@ -53,3 +53,15 @@ def test_config_struct_layout_matches_reference_prefix():
     from strasgpt_amd.runtime import TransformerConfig
     assert TransformerConfig.vocabulary_len.offset == 48
     assert TransformerConfig.aliased_out_weight.offset == 112
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message (the
+    path has no multi-GPU form)."""
+    import json
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "exactly one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
