@@ -154,7 +154,7 @@ def test_format_switch_and_refusal(model_dir):
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("name", ["llama3.2-1b", "qwen3-4b"])
 def test_bf16_cache_full_size(name, model_dir):
-    """configs[0] and [1] at full size with the bf16 cache. The GPU's greedy
+    """The Llama-3.2-1B and Qwen3-4B shapes at full size with the bf16 cache. The GPU's greedy
     tokens are replayed through the bf16-cache oracle (teacher forcing):
     every token is the oracle's argmax, or within 0.05 of it (a near tie
     that the ~5e-3 logit differences can flip; counted and printed). The

@@ -1,7 +1,7 @@
 """Parity of the HIP library (called through the C-ABI) with the golden
 fixtures of the reference C sources and with the CPU oracle.
 
-Bars (BASELINE north star): greedy token ids identical; logits and
+Bars: greedy token ids identical; logits and
 per-layer hidden states within 2e-2 relative and 1e-3 absolute
 (|gpu - ref| <= 1e-3 + 2e-2 |ref|), fp32 accumulation.
 """
