@@ -21,6 +21,7 @@
 // next kernel (RMSNorm with residual, k_elementwise.hip) sums in order.
 //
 // Algorithmic FLOP per launch: 2 * M * N * K (x2 for the SwiGLU pair).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -772,6 +773,76 @@ int gemm_splits(int M, int N, int K) {
   int s = (int)((K >= 16384 ? want : 256) + tiles - 1) / (int)tiles;
   while (s > 1 && (K + BK - 1) / BK < 4 * s) s--;  // keep at least 4 K tiles per split
   return s < 1 ? 1 : s;
+}
+
+namespace {
+
+// Epilogue of a split-K QKV or SwiGLU GEMM (few rows): thread (m, n) sums
+// the partials in split order and applies the fused GEMM epilogue (QKV:
+// the q row, the key row (or its staging row for a bf16 cache) and the
+// value row at position P + m; SwiGLU: silu(gate) * up stored as the next
+// GEMM's hi/lo planes).
+template <int EPI>
+__global__ __launch_bounds__(256) void split_epilogue_kernel(GemmParams p, const float* part, const float* part2,
+                                                             int splits) {
+  const int M = p.M, N = EPI == GEMM_SWIGLU ? p.N : p.q_dim + 2 * p.kv_dim;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)M * N) return;
+  const int m = (int)(idx / N), n = (int)(idx % N);
+  float v = 0.0f;
+  for (int sp = 0; sp < splits; sp++) v += part[((size_t)sp * M + m) * N + n];
+  if (EPI == GEMM_SWIGLU) {
+    float u = 0.0f;
+    for (int sp = 0; sp < splits; sp++) u += part2[((size_t)sp * M + m) * N + n];
+    store_split(p.c_hi, p.c_lo, (size_t)m * p.ldc + n, silu_mul(v, u), p.c_lo != nullptr);
+  } else if (n < p.q_dim) {
+    p.q[(size_t)m * p.q_dim + n] = v;
+  } else {
+    const int P = *p.pos;
+    const int kv = n - p.q_dim;
+    float* cache = kv < p.kv_dim ? p.kcache : p.vcache;
+    const int j2 = kv < p.kv_dim ? kv : kv - p.kv_dim;
+    const int head = j2 / p.head_dim, h = j2 % p.head_dim;
+    const size_t at = ((size_t)head * p.ctx + P + m) * p.head_dim + h;
+    if (!p.kv_bf16) cache[at] = v;
+    else if (kv < p.kv_dim) p.kstage[(size_t)m * p.kv_dim + kv] = v;  // rounded after RoPE
+    else ((uint16_t*)cache)[at] = f32_to_bf16_any(v);
+  }
+}
+
+}  // namespace
+
+int gemm_small_splits(int M, int N, int K, int epi, size_t ws_floats) {
+  if (M > kSmallM || (epi != GEMM_QKV && epi != GEMM_SWIGLU) || K % 64) return 1;
+  const int tiles = (N + 127) / 128 * (epi == GEMM_SWIGLU ? 2 : 1);  // 64 x 128 tiles of the partial GEMMs
+  int sp = std::min(8, std::max(1, (256 + tiles - 1) / tiles));
+  while (sp > 1 && K / 64 < 4 * sp) sp--;  // at least 4 K steps per split
+  while (sp > 1 && (size_t)sp * M * N * (epi == GEMM_SWIGLU ? 2 : 1) > ws_floats) sp--;
+  return sp;
+}
+
+void gemm_small(const GemmParams& p, int epi, int prec, int splits, float* ws, hipStream_t s) {
+  if (splits < 2 || (epi != GEMM_QKV && epi != GEMM_SWIGLU)) ST_DIE("gemm_small: split QKV or SwiGLU only");
+  const int N = epi == GEMM_SWIGLU ? p.N : p.q_dim + 2 * p.kv_dim;
+  if (epi == GEMM_QKV && p.N != N) ST_DIE("GEMM QKV column count mismatch");
+  GemmParams q = p;
+  q.w2 = nullptr;
+  q.c = ws;
+  q.ldc = N;
+  gemm(q, GEMM_PARTIAL, prec, splits, s);
+  float* ws2 = ws + (size_t)splits * p.M * N;
+  if (epi == GEMM_SWIGLU) {
+    q.w = p.w2;
+    q.c = ws2;
+    gemm(q, GEMM_PARTIAL, prec, splits, s);
+  }
+  const size_t threads = (size_t)p.M * N;
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (epi == GEMM_SWIGLU)
+    hipLaunchKernelGGL(split_epilogue_kernel<GEMM_SWIGLU>, grid, dim3(256), 0, s, p, ws, ws2, splits);
+  else
+    hipLaunchKernelGGL(split_epilogue_kernel<GEMM_QKV>, grid, dim3(256), 0, s, p, ws, nullptr, splits);
+  HIP_CHECK(hipGetLastError());
 }
 
 void gemm(const GemmParams& p, int epi, int prec, int splits, hipStream_t s) {

@@ -114,6 +114,10 @@ TINY: Dict[str, ModelShape] = {
     # (512 rows: 2 row tiles; QKV 12, O 4, gate/up 16, down 4 column tiles).
     "mid-dense": ModelShape("mid-dense", 1024, 2048, 1, 8, 8, 128, 512, 500000.0, 1e-5,
                             512, 4, ctx=600, untied=True, std=0.02),
+    # A short prompt on wide rows: the QKV prefill GEMM takes the split-K
+    # form with the separate epilogue (8 rows, 4 splits).
+    "small-m": ModelShape("small-m", 1024, 2048, 2, 8, 2, 128, 512, 500000.0, 1e-5,
+                          8, 6, ctx=64, untied=True, std=0.02),
     # FFN rows longer than one LDS stage of the decode GEMV (64 KiB of
     # fp32): the down projection takes the split-K form, in 3 ranges of
     # 14 steps (20480 = 40 steps of 512, the last range short) or 4 of 16.

@@ -117,6 +117,33 @@ def test_gemm_tile_orders(model_dir, monkeypatch):
         assert np.array_equal(got[order], got["0"])
 
 
+def test_small_prompt_split_gemms(model_dir):
+    """Prompts of at most 32 rows run the QKV GEMM split over K (partial
+    sums, then an epilogue kernel that adds them in split order and writes
+    q and the key / value cache rows): prefill logits and greedy tokens
+    against the oracle, and a 40-row prompt (the fused epilogue) agrees
+    too."""
+    rt = runtime()
+    d = model_dir("small-m")
+    shp = synth.shape("small-m")
+    om = oracle_model(d, 16)
+    with rt.Transformer(d) as t:
+        for T in (8, 40):
+            prompt = synth.prompt_tokens(shp.vocab, T, 17)
+            om.reset()
+            ol = om.predict(prompt)
+            om.reset()
+            otok = om.generate(prompt, 6)
+            t.reset()
+            gl = t.predict(prompt)
+            err = float(np.abs(gl - ol).max())
+            log(f"small-m T={T}: max |logit error| {err:.3g}")
+            np.testing.assert_allclose(gl, ol, rtol=RTOL, atol=ATOL)
+            t.reset()
+            gtok, _ = t.generate(prompt, 6)
+            assert gtok == otok
+
+
 @pytest.mark.parametrize("kernel", ["x3", "x3-16", "x3-32", "fp32"])
 @pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk"])
 def test_prefill_attention_kernels(name, kernel, model_dir, monkeypatch):
