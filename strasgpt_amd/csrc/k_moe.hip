@@ -867,7 +867,7 @@ __global__ __launch_bounds__(256) void group_gemm_kernel(MoeGemmParams p) {
 // (indexes past the last step are clamped to it and never read), so the
 // wait before a step is a constant: the groups of the QNA - 2 later steps
 // may stay in flight.
-constexpr int QBM = 32, QKS = 64, QBR = 128;  // slots, K per step, weight rows per block
+constexpr int QKS = 64, QBR = 128;  // K per step, weight rows per block
 constexpr int QFR = QBR / 64;                  // 16-row B fragments per wave
 constexpr int QBI = QBR / 128;                 // code DMA instructions per wave and step
 constexpr int kXcds = 8;                      // XCDs of an MI355X (round-robin block dispatch)
@@ -878,15 +878,17 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   return v;
 }
 constexpr int QNA = 3, QNB = 3;              // A ring, code ring stages
-constexpr int QAI = 2 * QBM * QKS * 2 / 1024 / 4;  // A DMA instructions per wave and step
+template <int BM>
+constexpr int q_ai() { return 2 * BM * QKS * 2 / 1024 / 4; }  // A DMA instructions per wave and step
 constexpr int kQMaxNb = 256;                  // K / 32 <= 256 (scales per row)
 
 // Scale bytes per run (one run per matrix): rows x nb, in whole 1 KiB DMA
 // instructions so that the runs' tails never overlap.
 __host__ __device__ constexpr int q_scale_run(int rows, int nb) { return (rows * nb + 1023) / 1024 * 1024; }
 
+template <int BM>
 struct QLds {
-  static constexpr int a_stage = 2 * QBM * QKS * 2;  // hi + lo rows of 128 bytes
+  static constexpr int a_stage = 2 * BM * QKS * 2;  // hi + lo rows of 128 bytes
   static constexpr int b_stage = QBR * 32;           // 2 code blocks per row
   static constexpr int a = 0;
   static constexpr int b = a + QNA * a_stage;
@@ -895,6 +897,7 @@ struct QLds {
   static constexpr int sc = (fsc + 2 * QBR * 2 * 4 + 1023) / 1024 * 1024;  // scales: QBR rows x nb bytes
 };
 static_assert(QNA == QNB, "one ring slot per step for the A rows and the codes");
+static_assert(QLds<64>::sc + 2 * ((128 * 256 / 2 + 1023) / 1024 * 1024) <= 160 * 1024, "grouped GEMM LDS");
 
 __device__ __forceinline__ int q_swz(int r) { return (r >> 1) & 7; }  // 128-byte rows
 
@@ -903,12 +906,17 @@ __device__ __forceinline__ int q_swz(int r) { return (r >> 1) & 7; }  // 128-byt
 // explicit waits and barriers order the data).
 typedef unsigned q_u32x4 __attribute__((ext_vector_type(4)));
 
-template <bool DUAL>
+// BM slots per block (32 or 64; 64 when experts average enough slots that
+// one tile covers most of them, so each expert's weights stream once).
+template <bool DUAL, int BM>
 __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
+  using QL = QLds<BM>;
+  constexpr int QAI = q_ai<BM>();
+  constexpr int MS = BM / 16;  // 16-slot sub-tiles
   // one LDS object (a second one makes the compiler wait for every LDS DMA
   // before any LDS read)
   extern __shared__ __attribute__((aligned(1024))) unsigned char ql[];
-  int* tile_info = (int*)(ql + QLds::info);
+  int* tile_info = (int*)(ql + QL::info);
   const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
   // Tile of this block. The (slot tile, column tile) grid is laid out per
   // XCD (blocks are dispatched to the 8 XCDs round-robin by linear id): XCD
@@ -917,12 +925,12 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   // its tiles stay in its L2 across column tiles and the slot tiles of one
   // expert, run side by side, share each column tile's codes.
   if (wave == 0) {
-    // total slot tiles (experts in order, ceil(count / QBM) each)
+    // total slot tiles (experts in order, ceil(count / BM) each)
     int tr = 0;
     for (int e0 = 0; e0 < p.E; e0 += WAVE) {
       const int e = e0 + lane;
       const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
-      tr += wave_sum_int((c + QBM - 1) / QBM);
+      tr += wave_sum_int((c + BM - 1) / BM);
     }
     const int lin = (int)(blockIdx.x + blockIdx.y * gridDim.x);
     const int xcd = lin % kXcds, j = lin / kXcds, ny = (int)gridDim.y;
@@ -935,7 +943,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
       for (int e0 = 0; e0 < p.E && e_found < 0; e0 += WAVE) {
         const int e = e0 + lane;
         const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
-        int tiles = (c + QBM - 1) / QBM, incl = tiles;
+        int tiles = (c + BM - 1) / BM, incl = tiles;
 #pragma unroll
         for (int off = 1; off < WAVE; off <<= 1) {
           const int v = __shfl_up(incl, off, WAVE);
@@ -946,7 +954,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
         if (m) {
           const int src = __ffsll((long long)m) - 1;
           e_found = __shfl(e0 + lane, src, WAVE);
-          m0 = (T - __shfl(excl, src, WAVE)) * QBM;
+          m0 = (T - __shfl(excl, src, WAVE)) * BM;
         }
         base += __shfl(incl, WAVE - 1, WAVE);
       }
@@ -967,16 +975,16 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
 
   // --- DMA sources (per lane) ---
   // A: instruction i (< QAI) of this wave covers stage rows 8 (QAI wave + i)
-  // .., rows 0..QBM-1 hi, QBM..2 QBM-1 lo; lane -> row + lane / 8, physical
+  // .., rows 0..BM-1 hi, BM..2 BM-1 lo; lane -> row + lane / 8, physical
   // chunk lane % 8.
   const uint16_t* asrc[QAI];
 #pragma unroll
   for (int i = 0; i < QAI; i++) {
     const int row = 8 * (QAI * wave + i) + lane / 8;
     const int c = (lane % 8) ^ q_swz(row);
-    const int r = row % QBM;
+    const int r = row % BM;
     const int grow = rbeg + min(m0 + r, cnt - 1);  // rows past the tile load its last row
-    asrc[i] = (row < QBM ? p.a_hi : p.a_lo) + (size_t)grow * K + 8 * c;
+    asrc[i] = (row < BM ? p.a_hi : p.a_lo) + (size_t)grow * K + 8 * c;
   }
   // codes: instruction i of wave w covers weight rows 32 (QBI w + i) ..
   // + 31, lane -> row + lane / 2, block lane % 2 of the step
@@ -1001,7 +1009,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
       const uint8_t* sb = rr == 0 ? p.scales : p.scales2;
       for (int n = wave; n < ni; n += 4) {
         const size_t o = min(off0 + (size_t)n * 1024 + 16 * lane, limit);
-        __builtin_amdgcn_global_load_lds((const void*)(sb + o), (lds_ptr)(ql + QLds::sc + rr * run + n * 1024),
+        __builtin_amdgcn_global_load_lds((const void*)(sb + o), (lds_ptr)(ql + QL::sc + rr * run + n * 1024),
                                          16, 0, 0);
       }
     }
@@ -1026,9 +1034,9 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     return *(const bf16x8*)(as + r * 128 + ((ch ^ q_swz(r)) << 4));
   };
 
-  f32x4 acc[2][QFR];  // [16-slot sub-tile][fragment]
+  f32x4 acc[MS][QFR];  // [16-slot sub-tile][fragment]
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < MS; i++)
 #pragma unroll
     for (int f = 0; f < QFR; f++) acc[i][f] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -1036,12 +1044,12 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   // step clamped to it: read, never used)
   auto issue_group = [&](int t) {
     const int tc = min(t, nk - 1);
-    unsigned char* as = ql + QLds::a + (t % QNA) * QLds::a_stage;
+    unsigned char* as = ql + QL::a + (t % QNA) * QL::a_stage;
 #pragma unroll
     for (int i = 0; i < QAI; i++)
       __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + tc * QKS),
                                        (lds_ptr)(as + (QAI * wave + i) * 1024), 16, 0, 0);
-    unsigned char* bs = ql + QLds::b + (t % QNB) * QLds::b_stage;
+    unsigned char* bs = ql + QL::b + (t % QNB) * QL::b_stage;
 #pragma unroll
     for (int i = 0; i < QBI; i++)
       __builtin_amdgcn_global_load_lds((const void*)(bsrc[i] + (size_t)tc * 32),
@@ -1054,13 +1062,13 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   __syncthreads();
   // the E8M0 scales of a step as fp32 (row q / 2, block q % 2 for q = tid,
   // tid + 256, ..), a step ahead of their use
-  float* fsc = (float*)(ql + QLds::fsc);
+  float* fsc = (float*)(ql + QL::fsc);
   constexpr int NCS = 2 * QBR / 256;  // scales per thread and step
   int csrc[NCS];
 #pragma unroll
   for (int i = 0; i < NCS; i++) {
     const int q = tid + 256 * i, crow = q / 2;
-    csrc[i] = QLds::sc + (DUAL ? (crow / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (crow % (QBR / 2)) * nb
+    csrc[i] = QL::sc + (DUAL ? (crow / (QBR / 2)) * q_scale_run(QBR / 2, nb) + (crow % (QBR / 2)) * nb
                                : crow * nb) + q % 2;
     fsc[q] = e8m0_scale(ql[csrc[i]]);
   }
@@ -1072,8 +1080,8 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     __syncthreads();
     // every operand of step kt from LDS first, then the next group's DMA
     // (into the slot of step kt - 1)
-    const unsigned char* as = ql + QLds::a + (kt % QNA) * QLds::a_stage;
-    const unsigned char* bs = ql + QLds::b + (kt % QNB) * QLds::b_stage;
+    const unsigned char* as = ql + QL::a + (kt % QNA) * QL::a_stage;
+    const unsigned char* bs = ql + QL::b + (kt % QNB) * QL::b_stage;
     unsigned w[QFR][2];  // [fragment][k-step]: 8 codes
     float sc[QFR][2];
 #pragma unroll
@@ -1088,14 +1096,14 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
 #pragma unroll
       for (int i = 0; i < NCS; i++) fsc[((kt + 1) & 1) * 2 * QBR + tid + 256 * i] = e8m0_scale(ql[csrc[i] + 2 * (kt + 1)]);
     }
-    bf16x8 ah[2][2], al[2][2];  // [k-step][16-slot sub-tile]
+    bf16x8 ah[2][MS], al[2][MS];  // [k-step][16-slot sub-tile]
 #pragma unroll
     for (int kk = 0; kk < 2; kk++)
 #pragma unroll
-      for (int mi = 0; mi < 2; mi++) {
+      for (int mi = 0; mi < MS; mi++) {
         const int ch = 4 * kk + g, r = 16 * mi + c;
         ah[kk][mi] = achunk(as, r, ch);
-        al[kk][mi] = achunk(as, QBM + r, ch);
+        al[kk][mi] = achunk(as, BM + r, ch);
       }
     issue_group(kt + QNA - 1);
 #pragma unroll
@@ -1112,7 +1120,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
         b[f] = __builtin_bit_cast(bf16x8, v);
       }
 #pragma unroll
-      for (int mi = 0; mi < 2; mi++)
+      for (int mi = 0; mi < MS; mi++)
 #pragma unroll
         for (int f = 0; f < QFR; f++) {
           acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kk][mi], b[f], acc[mi][f], 0, 0, 0);
@@ -1123,7 +1131,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   __builtin_amdgcn_s_waitcnt(0);  // the clamped tail loads land before the wave ends
   // lane holds C[4 (lane / 16) + i][lane % 16] of each 16 x 16 tile
 #pragma unroll
-  for (int mi = 0; mi < 2; mi++)
+  for (int mi = 0; mi < MS; mi++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int r = 16 * mi + 4 * g + i;
@@ -1294,24 +1302,44 @@ void moe_gather_split(const MoeGemmParams& p, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
+// Slots per tile of the grouped GEMM: 64 when the experts average at least
+// 24 slots (a 32-slot tiling would stream most experts' weights twice),
+// else 32. STRASGPT_MOE_TILE=32|64 forces one (tests run both).
+int moe_slot_tile(int slots, int E) {
+  const char* v = getenv("STRASGPT_MOE_TILE");
+  if (v && *v) {
+    const int t = atoi(v);
+    if (t != 32 && t != 64) ST_DIE("STRASGPT_MOE_TILE must be 32 or 64");
+    return t;
+  }
+  return slots >= 24 * E ? 64 : 32;
+}
+
 void moe_group_gemm(const MoeGemmParams& p, hipStream_t s) {
   if (p.K % 32 || p.N <= 0 || p.slots <= 0) ST_DIE("MoE grouped GEMM shape");
   if (moe_group_gemm2_ok(p)) {
     const bool dual = p.blocks2 != nullptr;
     const int nb = p.K / 32, runs = dual ? 2 : 1;
-    const size_t shm = QLds::sc + (size_t)runs * q_scale_run(QBR / runs, nb);
+    const int bm = moe_slot_tile(p.slots, p.E);
+    const size_t shm = (bm == 64 ? QLds<64>::sc : QLds<32>::sc) + (size_t)runs * q_scale_run(QBR / runs, nb);
     const int cols = dual ? QBR / 2 : QBR;
     // slot tiles: an upper bound (the counts are on the device), rounded to
     // whole rounds of the XCDs (the kernel's per-XCD layout)
-    const int tmax = ((p.slots + QBM - 1) / QBM + p.E + kXcds - 1) / kXcds * kXcds;
+    const int tmax = ((p.slots + bm - 1) / bm + p.E + kXcds - 1) / kXcds * kXcds;
     const dim3 grid(tmax, (p.N + cols - 1) / cols);
+#define GG2(D, B)                                                          \
+  do {                                                                     \
+    set_lds(group_gemm2_kernel<D, B>, shm);                                \
+    hipLaunchKernelGGL((group_gemm2_kernel<D, B>), grid, dim3(256), shm, s, p); \
+  } while (0)
     if (dual) {
-      set_lds(group_gemm2_kernel<true>, shm);
-      hipLaunchKernelGGL(group_gemm2_kernel<true>, grid, dim3(256), shm, s, p);
+      if (bm == 64) GG2(true, 64);
+      else GG2(true, 32);
     } else {
-      set_lds(group_gemm2_kernel<false>, shm);
-      hipLaunchKernelGGL(group_gemm2_kernel<false>, grid, dim3(256), shm, s, p);
+      if (bm == 64) GG2(false, 64);
+      else GG2(false, 32);
     }
+#undef GG2
     HIP_CHECK(hipGetLastError());
     return;
   }

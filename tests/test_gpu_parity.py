@@ -528,6 +528,28 @@ def test_logits_window_and_chunking(model_dir):
     np.testing.assert_allclose(gl2[0], ol[-1], rtol=RTOL, atol=ATOL)
 
 
+def test_moe_grouped_gemm_slot_tiles(model_dir, monkeypatch):
+    """The grouped prefill GEMM with 32- and with 64-slot tiles
+    (STRASGPT_MOE_TILE; 64 is taken when the experts average 24 slots or
+    more): the same logits to fp32 rounding, both against the oracle."""
+    rt = runtime()
+    d = model_dir("tiny-moe-long")
+    shp = synth.shape("tiny-moe-long")
+    prompt = synth.prompt_tokens(256, shp.prompt_len, PROMPT_SEED)
+    ol = oracle_model(d, 4).predict(prompt)
+    got = {}
+    with rt.Transformer(d) as t:
+        for tile in ("32", "64"):
+            monkeypatch.setenv("STRASGPT_MOE_TILE", tile)
+            t.reset()
+            got[tile] = t.predict(prompt)
+            err = float(np.abs(got[tile] - ol).max())
+            log(f"tiny-moe-long, {tile}-slot tiles: max |logit error| {err:.3g}")
+            np.testing.assert_allclose(got[tile], ol, rtol=RTOL, atol=ATOL)
+    # the slot tiling does not change any product's K order
+    np.testing.assert_array_equal(got["32"], got["64"])
+
+
 @pytest.mark.parametrize("name", ["tiny-moe", "tiny-moe-long",
                                   pytest.param("mid-moe", marks=pytest.mark.slow)])
 def test_moe_tiny_against_oracle(name, model_dir):
