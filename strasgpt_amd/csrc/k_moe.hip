@@ -852,10 +852,12 @@ __global__ __launch_bounds__(256) void group_gemm_kernel(MoeGemmParams p) {
 //   E8M0 scales are DMA'd once per block and converted to fp32 a step ahead;
 // * each wave converts the codes of its own weight rows straight into its
 //   MFMA B operands (hardware FP4 conversion to packed bf16 pairs, exact),
-//   so no decoded tile goes through LDS: 32 slots (experts average about 32
-//   slots per chunk: 64-slot tiles would be half empty) x QBR rows x 64 K
-//   per step, 8 QFR MFMAs per wave (each wave: all 32 slots x QFR 16-row
-//   fragments). Every wave reads the whole A stage, so wider blocks read A
+//   so no decoded tile goes through LDS: BM slots (32, or 64 when the
+//   experts average at least 24 slots, so that one tile covers most experts
+//   and their weights stream once) x QBR rows x 64 K per step, 4 BM / 16
+//   QFR MFMAs per wave (each wave: all BM slots x QFR 16-row fragments;
+//   a 2 x 2 split of the waves, half the A stage each but twice the code
+//   conversions, measured slower). Every wave reads the whole A stage, so wider blocks read A
 //   less often per product: QBR = 256 takes 1.2x the time of 128 for twice
 //   the work, but its grid of half as many blocks (at two per CU, 75 KiB of
 //   LDS) leaves a partial last round at the 256-token prefill and loses
