@@ -461,6 +461,29 @@ def test_strasgpt_text_prompt_and_token_strings(model_dir):
     tk.close()
 
 
+def test_strasgpt_sampling_flags(model_dir):
+    """--temp / --top-k / --top-p / -s select the device sampler in both
+    loops: the reference loop (--host-loop, logits on the host) and the
+    device loop draw the same tokens from the same seed; another seed
+    draws a different sequence."""
+    from strasgpt_amd import _paths
+    g = np.load(os.path.join(GOLDEN_DIR, "tiny-qwen.npz"))
+    prompt = " ".join(str(int(v)) for v in g["prompt"])
+    d = model_dir("tiny-qwen")
+    exe = _paths.driver_exe()
+    runs = {}
+    for key, extra in (("host", ["--host-loop", "-t", "4", "-s", "7"]), ("device", ["-s", "7"]),
+                       ("other", ["-s", "8"])):
+        cmd = [exe, "-m", d, "-n", "8", "--temp", "0.9", "--top-k", "20", "--top-p", "0.95",
+               "--pre-tokenized", "-p", prompt, "--ids"] + extra
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr[-2000:]
+        runs[key] = [int(v) for v in r.stdout.split()]
+        log(f"strasgpt sampled ({key}): {runs[key]}")
+    assert len(runs["host"]) == 8 and runs["host"] == runs["device"]
+    assert runs["other"] != runs["device"]
+
+
 def test_first_token_eos_does_not_stop(model_dir):
     """The reference tests only decode steps' tokens against EOS
     (source/strasgpt.c:217-248): an EOS predicted from the prompt is kept
