@@ -129,6 +129,13 @@ bool safetensors_aliased_out_weight(const safetensors_t* safetensors);
  * does with options->model_dir, reference source/json_parser.y:526-622). */
 safetensors_t* safetensors_read_dir(const char* model_dir);
 
+/* The JSON front-end's scanner cleanup, called by the reference driver at
+ * exit (reference source/strasgpt.c:30,287; flex-generated in the
+ * reference, source/json_scanner.l). The library's reader holds no scanner
+ * state, so it frees nothing; it exists so that the reference driver links
+ * against the library with its lex/yacc front-end removed. Returns 0. */
+int json_scanner_lex_destroy(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -512,6 +512,11 @@ safetensors_t* safetensors_read_dir(const char* dir) {
   return s;
 }
 
+/* The reference driver releases its JSON scanner at exit
+ * (source/strasgpt.c:30,287). This reader keeps no scanner state: nothing
+ * to free. */
+int json_scanner_lex_destroy(void) { return 0; }
+
 safetensors_t* safetensors_read(struct options* options) {
   if (!options) ST_DIE("NULL options");
   return safetensors_read_dir(((struct options_prefix*)options)->model_dir);

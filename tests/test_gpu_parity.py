@@ -484,6 +484,46 @@ def test_strasgpt_sampling_flags(model_dir):
     assert runs["other"] != runs["device"]
 
 
+REF_DRIVER = os.path.join(REPO, "oracle", "_ref", "ref_driver_hip")
+
+
+@pytest.mark.skipif(not os.path.exists(REF_DRIVER),
+                    reason="reference driver not built (oracle/Makefile ref_driver_hip needs "
+                           "the reference sources when building)")
+def test_reference_driver_on_the_library(model_dir):
+    """The reference's own driver (source/strasgpt.c, options.c, sampler.c,
+    util.c) linked against libstrasgpt_hip in place of its transformer,
+    safetensors, tokenizer and JSON front-end: its stdout matches the
+    library driver's byte for byte on the golden prompt (greedy, and
+    sampled with the reference's CPU sampler against the device sampler
+    from the same seed) and on a text prompt the library tokenizes."""
+    from strasgpt_amd import _paths
+    g = np.load(os.path.join(GOLDEN_DIR, "tiny-qwen.npz"))
+    prompt = " ".join(str(int(v)) for v in g["prompt"])
+    d = model_dir("tiny-qwen")
+    exe = _paths.driver_exe()
+    n = str(len(g["generated"]))
+    cases = {
+        "greedy": ["-n", n, "--temp", "0", "--pre-tokenized", "-p", prompt],
+        "sampled": ["-n", "8", "--temp", "0.9", "--top-k", "20", "--top-p", "0.95", "-s", "7",
+                    "--pre-tokenized", "-p", prompt],
+        "text": ["-n", "10", "--temp", "0", "-p", "<5> a"],
+    }
+    got = {}
+    for key, args in cases.items():
+        outs = []
+        for prog in (REF_DRIVER, exe):
+            r = subprocess.run([prog, "-m", d] + args, capture_output=True, timeout=120)
+            err = r.stderr.decode("latin-1")
+            assert r.returncode == 0, f"{prog} {key}: {err[-2000:]}"
+            assert "Prompt processing (prefill):" in err
+            outs.append(r.stdout)
+        log(f"reference driver ({key}): {outs[0][:80]!r}")
+        assert outs[0] == outs[1], (key, outs)
+        got[key] = outs[0]
+    assert got["greedy"].strip() and got["sampled"] != got["greedy"]
+
+
 def test_first_token_eos_does_not_stop(model_dir):
     """The reference tests only decode steps' tokens against EOS
     (source/strasgpt.c:217-248): an EOS predicted from the prompt is kept
