@@ -14,7 +14,11 @@
  *                 device argmax (--temp 0) or the device sampler;
  *   --ids         print the generated ids on one line instead of their
  *                 strings;
- *   --show-model  print the model summary and exit.
+ *   --show-model  print the model summary and exit;
+ *   --show-safetensors  print the safetensors summary and exit;
+ *   --instruct    wrap the prompt ids in the model family's chat template
+ *                 (no BOS added to a text prompt; source/strasgpt.c:
+ *                 170-179).
  * Default: transformer_generate_greedy / transformer_generate_sampled
  * (device-resident decode loop). Generated token strings go to stdout as
  * in the reference (the first token always, then up to EOS, printed as
@@ -45,11 +49,58 @@ static double now_s(void) {
   return ts.tv_sec + 1e-9 * ts.tv_nsec;
 }
 
+/* --instruct: ids put before and after the prompt per model family,
+ * chosen by a substring of config.json's model_type, first match wins; no
+ * match leaves the prompt as it is. The ids and the order of the checks are
+ * the reference's (source/util.c:514-575). */
+typedef struct {
+  const char* match[2];
+  int before[20];
+  int n_before;
+  int after[8];
+  int n_after;
+} chat_template_t;
+
+static const chat_template_t kChatTemplates[] = {
+    {{"qwen3", "qwen3_vl"},
+     {151644, 8948, 198, 2610, 525, 264, 10950, 17847, 624, 151645, 198, 151644, 872, 198},
+     14,
+     {198, 151645, 198, 151644, 77091},
+     5},
+    {{"Mistral", "mistral"}, {1, 1, 3}, 3, {4}, 1},
+    {{"Llama", "llama"},
+     {128000, 128000, 198, 128006, 9125, 128007, 198, 2675, 527, 264, 11190, 18328, 627, 128009, 198,
+      128006, 882, 128007, 198},
+     19,
+     {198, 128009, 198, 128006, 78191, 128007},
+     6},
+};
+
+static int* wrap_instruct(int* tok, size_t* n, const char* model_type) {
+  if (!model_type) return tok;
+  for (size_t t = 0; t < sizeof kChatTemplates / sizeof kChatTemplates[0]; t++) {
+    const chat_template_t* c = &kChatTemplates[t];
+    if (!strstr(model_type, c->match[0]) && !strstr(model_type, c->match[1])) continue;
+    int* out = malloc((c->n_before + *n + c->n_after) * sizeof(int));
+    if (!out) {
+      fprintf(stderr, "[StrasGPT] Error: out of memory for the instruction tokens\n");
+      exit(EXIT_FAILURE);
+    }
+    memcpy(out, c->before, c->n_before * sizeof(int));
+    memcpy(out + c->n_before, tok, *n * sizeof(int));
+    memcpy(out + c->n_before + *n, c->after, c->n_after * sizeof(int));
+    free(tok);
+    *n += c->n_before + c->n_after;
+    return out;
+  }
+  return tok;
+}
+
 static void usage(const char* argv0, int status) {
   fprintf(stderr,
           "Usage: %s -m <model_dir> [-n steps] [-t threads] [-s seed] [--temp t] [--top-k k]\n"
           "       [--top-p p] [--presence-penalty x] (-p <prompt> | -f <file>) [--pre-tokenized]\n"
-          "       [--host-loop] [--ids] [--show-model]\n",
+          "       [--instruct] [--host-loop] [--ids] [--show-model] [--show-safetensors]\n",
           argv0);
   exit(status);
 }
@@ -131,6 +182,7 @@ int main(int argc, char** argv) {
   unsigned long long seed = 0;
   float temp = 1.0f, top_p = 0.9f;
   bool pre_tokenized = false, host_loop = false, show_model = false, ids_only = false;
+  bool show_safetensors = false, instruct = false;
   for (int i = 1; i < argc; i++) {
     const char* a = argv[i];
     const char* v = i + 1 < argc ? argv[i + 1] : NULL;
@@ -138,6 +190,8 @@ int main(int argc, char** argv) {
     else if (!strcmp(a, "--pre-tokenized")) pre_tokenized = true;
     else if (!strcmp(a, "--host-loop")) host_loop = true;
     else if (!strcmp(a, "--show-model")) show_model = true;
+    else if (!strcmp(a, "--show-safetensors")) show_safetensors = true;
+    else if (!strcmp(a, "--instruct")) instruct = true;
     else if (!strcmp(a, "--ids")) ids_only = true;
     else if (!v) usage(argv[0], EXIT_FAILURE);
     else if (!strcmp(a, "-m")) model = argv[++i];
@@ -155,6 +209,11 @@ int main(int argc, char** argv) {
 
   if (steps == 0) steps = 1; /* the reference always predicts the first token */
   safetensors_t* st = safetensors_read_dir(model);
+  if (show_safetensors) {
+    safetensors_print(stderr, st);
+    safetensors_free(st);
+    return EXIT_SUCCESS;
+  }
   if (show_model) {
     safetensors_print_model_infos(stderr, st);
     safetensors_free(st);
@@ -168,11 +227,12 @@ int main(int argc, char** argv) {
   size_t n_tok = 0;
   int* tok = NULL;
   if (pre_tokenized) tok = parse_ids(prompt, &n_tok);
-  else tokenizer_tokenize(tk, (char*)prompt, true, false, &n_tok, &tok);
+  else tokenizer_tokenize(tk, (char*)prompt, !instruct, false, &n_tok, &tok);
   if (n_tok < 1) {
     fprintf(stderr, "[StrasGPT] Error: expected at least 1 prompt token\n");
     return EXIT_FAILURE;
   }
+  if (instruct) tok = wrap_instruct(tok, &n_tok, st->model_type);
   tokenizer_print_tokens(tk, stderr, n_tok, tok, 4);
   fprintf(stderr, "\n\033[1;34m");
   for (size_t i = 0; i < n_tok; i++) tokenizer_print_token_string(stderr, tokenizer_decode(tk, tok[i]));

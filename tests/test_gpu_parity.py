@@ -524,6 +524,58 @@ def test_reference_driver_on_the_library(model_dir):
     assert got["greedy"].strip() and got["sampled"] != got["greedy"]
 
 
+def _prompt_tokens_block(err):
+    """The driver's 'Tokens (n):' report of the prompt ids (stderr)."""
+    i = err.index("Tokens (")
+    return err[i:err.index("\033[1;34m", i)]
+
+
+@pytest.mark.skipif(not os.path.exists(REF_DRIVER),
+                    reason="reference driver not built (oracle/Makefile ref_driver_hip needs "
+                           "the reference sources when building)")
+def test_reference_driver_instruct(model_dir, tmp_path):
+    """--instruct wraps the prompt ids in the model family's chat template
+    (source/strasgpt.c:170-179, source/util.c:514-575): the reference
+    driver and the library driver report the same prompt ids for qwen3,
+    llama and mistral model types and, where the template's ids fit the
+    vocabulary (mistral), generate the same text. The qwen3 and llama
+    templates make the prompts longer than the tiny models' contexts: both
+    drivers stop with the library's host-side context error before any
+    device work."""
+    import json
+    import shutil
+    from strasgpt_amd import _paths
+    g = np.load(os.path.join(GOLDEN_DIR, "tiny-qwen.npz"))
+    ids = " ".join(str(int(v)) for v in g["prompt"])
+    exe = _paths.driver_exe()
+    mistral = str(tmp_path / "tiny-qwen-as-mistral")
+    shutil.copytree(model_dir("tiny-qwen"), mistral)
+    cfg_path = os.path.join(mistral, "config.json")
+    cfg = json.load(open(cfg_path))
+    cfg["model_type"] = "mistral"
+    json.dump(cfg, open(cfg_path, "w"))
+    cases = [(model_dir("tiny-qwen"), ["--pre-tokenized", "-p", ids], False),
+             (model_dir("tiny-llama"), ["--pre-tokenized", "-p", ids], False),
+             (mistral, ["--pre-tokenized", "-p", ids], True),
+             (mistral, ["-p", "<5> a"], True)]
+    for d, extra, runs in cases:
+        res = []
+        for prog in (REF_DRIVER, exe):
+            r = subprocess.run([prog, "-m", d, "-n", "4", "--temp", "0", "--instruct"] + extra,
+                               capture_output=True, timeout=120)
+            res.append((r.returncode, r.stdout, r.stderr.decode("latin-1")))
+        log(f"instruct {os.path.basename(d)} {extra[0]}: rc {res[0][0]}/{res[1][0]}, "
+            f"{_prompt_tokens_block(res[0][2]).splitlines()[0]}")
+        assert _prompt_tokens_block(res[0][2]) == _prompt_tokens_block(res[1][2])
+        if runs:
+            assert res[0][0] == 0 and res[1][0] == 0, res[1][2][-2000:]
+            assert res[0][1] == res[1][1]
+        else:
+            assert res[0][0] != 0 and res[1][0] != 0
+            assert res[0][2].rstrip().endswith("context length exhausted")
+            assert res[1][2].rstrip().endswith("context length exhausted")
+
+
 def test_first_token_eos_does_not_stop(model_dir):
     """The reference tests only decode steps' tokens against EOS
     (source/strasgpt.c:217-248): an EOS predicted from the prompt is kept
