@@ -1050,6 +1050,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParam
 // Blocks per kv head, at most: up to 256 blocks, one per CU (a block holds
 // each SIMD's register file), and at most one combine lane each.
 int attention_decode_chunks(int kv_heads) {
+  // STRASGPT_DECODE_ATTN_CHUNKS: blocks per kv head at most (1-64), for
+  // sweeps; by default one block per CU over the kv heads
+  if (const char* v = getenv("STRASGPT_DECODE_ATTN_CHUNKS")) {
+    const int n = atoi(v);
+    if (n < 1 || n > kDecMaxChunks) ST_DIE("STRASGPT_DECODE_ATTN_CHUNKS must be 1-64");
+    return n;
+  }
   return std::max(1, std::min(kDecMaxChunks, 256 / std::max(1, kv_heads)));
 }
 

@@ -170,6 +170,23 @@ def test_prefill_attention_kernels(name, kernel, model_dir, monkeypatch):
         assert tokens == [int(v) for v in g["generated"]]
 
 
+@pytest.mark.parametrize("chunks", ["1", "8", "64"])
+def test_decode_attention_chunk_counts(chunks, model_dir, monkeypatch):
+    """Decode attention with at most 1, 8 or 64 blocks per kv head
+    (STRASGPT_DECODE_ATTN_CHUNKS; the default is 256 / kv_heads): over the
+    520-token prompt of tiny-chunk that is one block holding all 17 key
+    tiles (its result written directly), 6 blocks of 3 tiles, and 9 blocks
+    of 2; the greedy tokens are the reference run's either way."""
+    rt = runtime()
+    g = np.load(os.path.join(GOLDEN_DIR, "tiny-chunk.npz"))
+    prompt = [int(v) for v in g["prompt"]]
+    monkeypatch.setenv("STRASGPT_DECODE_ATTN_CHUNKS", chunks)
+    with rt.Transformer(model_dir("tiny-chunk")) as t:
+        tokens, _ = t.generate(prompt, len(g["generated"]))
+    log(f"tiny-chunk attention chunks {chunks}: {tokens}")
+    assert tokens == [int(v) for v in g["generated"]]
+
+
 @pytest.mark.parametrize("chunk", ["512", "600"])
 def test_prefill_chunk_lengths(chunk, model_dir, monkeypatch):
     """The 520-token prompt of tiny-chunk in device chunks of 512 (two
