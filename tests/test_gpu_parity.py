@@ -541,6 +541,28 @@ def test_reference_driver_on_the_library(model_dir):
     assert got["greedy"].strip() and got["sampled"] != got["greedy"]
 
 
+@pytest.mark.skipif(not os.path.exists(REF_DRIVER),
+                    reason="reference driver not built (oracle/Makefile ref_driver_hip needs "
+                           "the reference sources when building)")
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-moe", "tiny-rope-il"])
+def test_reference_driver_model_families(name, model_dir):
+    """The reference driver on the library over a dense Llama-type model,
+    an MXFP4 mixture of experts and interleaved RoPE: greedy output equal
+    to the library driver's, byte for byte."""
+    from strasgpt_amd import _paths
+    shp = synth.shape(name)
+    prompt = " ".join(str(v) for v in synth.prompt_tokens(shp.vocab, shp.prompt_len, PROMPT_SEED))
+    d = model_dir(name)
+    outs = []
+    for prog in (REF_DRIVER, _paths.driver_exe()):
+        r = subprocess.run([prog, "-m", d, "-n", str(shp.decode_len), "--temp", "0", "--pre-tokenized",
+                            "-p", prompt], capture_output=True, timeout=120)
+        assert r.returncode == 0, r.stderr.decode("latin-1")[-2000:]
+        outs.append(r.stdout)
+    log(f"reference driver {name}: {outs[0][:60]!r}")
+    assert outs[0] == outs[1] and outs[0].strip()
+
+
 def _prompt_tokens_block(err):
     """The driver's 'Tokens (n):' report of the prompt ids (stderr)."""
     i = err.index("Tokens (")
