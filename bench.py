@@ -21,7 +21,11 @@ reported beside it). The cpu_baseline is the reference's own C sources
 for -march=native) driven by the reference's greedy loop on a bounded
 sample of the same model files on the host cores, with the reference's
 timing boundaries (source/strasgpt.c:206-274); where that binary is absent,
-the oracle (the C + OpenMP restatement of the reference forward pass).
+the oracle (the C + OpenMP restatement of the reference forward pass). The
+GPU runs the same sample, and cpu_baseline.parity compares the two: greedy
+tokens identical, prefill logits within 2e-2 relative / 1e-3 absolute.
+Under rocprofv3 (kernel trace or counters) the decode steps are launched
+eagerly instead of replayed from the captured graph.
 """
 import argparse
 import json
@@ -78,9 +82,35 @@ def host_cpu():
     return avail, cores, model
 
 
-def cpu_baseline(d, shp, prompt, threads, prefill_tokens, decode_tokens):
+RTOL, ATOL = 2e-2, 1e-3  # logits: |gpu - cpu| <= ATOL + RTOL |cpu|
+
+
+def parity(gpu, cpu_tokens, cpu_logits):
+    """The GPU's greedy tokens and prefill logits on the baseline's sample
+    against the CPU run's."""
+    import numpy as np
+    g_tokens, g_logits = gpu
+    err = np.abs(g_logits - cpu_logits)
+    return {"tokens_match": list(g_tokens) == list(cpu_tokens),
+            "tokens_cpu": list(cpu_tokens), "tokens_gpu": list(g_tokens),
+            "prefill_logits_max_abs_err": float(err.max()),
+            "prefill_logits_within_tol": bool((err <= ATOL + RTOL * np.abs(cpu_logits)).all()),
+            "tol": f"{RTOL} rel + {ATOL} abs"}
+
+
+def under_profiler():
+    """Whether rocprofv3 runs this process with kernel tracing or counter
+    collection (it sets these variables for its tool library)."""
+    return any(os.environ.get(v) == "1" for v in ("ROCPROF_KERNEL_TRACE",
+                                                  "ROCPROF_COUNTER_COLLECTION"))
+
+
+def cpu_baseline(d, shp, prompt, threads, prefill_tokens, decode_tokens, gpu):
     """The reference forward pass on the host cores: a short prefill, then
-    `decode_tokens` greedy steps, timed like the reference driver."""
+    `decode_tokens` greedy steps, timed like the reference driver. `gpu` is
+    (tokens, prefill logits) of the GPU on the same sample; the CPU run's
+    are compared with them."""
+    import numpy as np
     from oracle import ref_manifest
     avail, phys, model = host_cpu()
     threads = max(1, min(threads, avail))
@@ -100,12 +130,17 @@ def cpu_baseline(d, shp, prompt, threads, prefill_tokens, decode_tokens):
             fields = [ln for ln in r.stderr.splitlines() if ln.startswith("timing ")][-1].split()
             prefill_s, decode_s, n = float(fields[1]), float(fields[2]), int(fields[3])
             log(f"cpu baseline: reference run in {time.time() - t0:.1f}s ({threads} threads)")
+            # out.bin: int32 tokens[n + 1], float32 prefill logits[V], ...
+            raw = open(os.path.join(tmp, "out.bin"), "rb").read()
+            cpu_tokens = np.frombuffer(raw, np.int32, n + 1).tolist()
+            cpu_logits = np.frombuffer(raw, np.float32, shp.vocab, offset=4 * (n + 1))
         return {"value": n / decode_s, "unit": "tok/s", "kind": "reference", **info,
                 "prefill_tok_s": len(sample_prompt) / prefill_s,
                 "sample": (f"{shp.name}: {len(sample_prompt)}-token prefill then {n} greedy "
                            f"decode steps, the reference's C sources (oracle/_ref/ref_baseline: "
                            f"-O3 -march=x86-64-v3 -ffast-math -fno-finite-math-only -fopenmp), "
-                           f"OMP_WAIT_POLICY=ACTIVE, {threads} threads")}
+                           f"OMP_WAIT_POLICY=ACTIVE, {threads} threads"),
+                "parity": parity(gpu, cpu_tokens, cpu_logits)}
     from oracle import oracle as orc
     t0 = time.time()
     om = orc.OracleModel(d, threads=threads)
@@ -113,10 +148,12 @@ def cpu_baseline(d, shp, prompt, threads, prefill_tokens, decode_tokens):
     t0 = time.time()
     logits = om.predict(sample_prompt)
     t_prefill = time.time() - t0
-    nxt = int(logits[0].argmax())
+    cpu_logits = logits[0].copy()
+    amax = lambda row: int(om.lib.oracle_argmax(orc.fptr(row), row.size))  # sample_argmax
+    cpu_tokens = [amax(logits[0])]
     t0 = time.time()
     for _ in range(decode_tokens):
-        nxt = int(om.predict([nxt])[0].argmax())
+        cpu_tokens.append(amax(om.predict([cpu_tokens[-1]])[0]))
     t_decode = time.time() - t0
     om.close()
     return {
@@ -124,6 +161,7 @@ def cpu_baseline(d, shp, prompt, threads, prefill_tokens, decode_tokens):
         "prefill_tok_s": len(sample_prompt) / t_prefill,
         "sample": (f"{shp.name}: {len(sample_prompt)}-token prefill then {decode_tokens} "
                    f"greedy decode steps, oracle/oracle.c (OpenMP, {threads} threads)"),
+        "parity": parity(gpu, cpu_tokens, cpu_logits),
     }
 
 
@@ -227,6 +265,12 @@ def main():
     t.set_prefill_precision(args.precision)
     t.set_kv_cache_format(runtime.KV_BF16 if args.kv_cache == "bf16" else runtime.KV_FP32)
     log(f"loaded into HBM in {load_s:.1f}s ({load_bytes / load_s / 1e9:.1f} GB/s); {runtime.version()}")
+    if under_profiler():
+        # rocprofv3's kernel tracing and counter collection follow every
+        # eager launch; replays of the captured decode graph under its
+        # kernel trace ended in a host SIGSEGV inside the HIP runtime
+        t.set_decode_mode(runtime.DECODE_EAGER)
+        log("under rocprofv3: decode steps launched eagerly (the kernels the graph replays)")
 
     if args.probe_traffic:
         probe_traffic(t, prompt)
@@ -273,6 +317,15 @@ def main():
     # stream (the per-launch event pairs above also bracket each launch's
     # dispatch gap). Classes without this hook keep the per-launch figure.
     rate = t.kernel_rate(dom, reps=4)
+    # The CPU baseline's sample on the GPU (greedy tokens and prefill
+    # logits), for the comparison with the CPU run.
+    gpu_sample = None
+    if not args.no_cpu_baseline:
+        sample = prompt[:args.cpu_prefill_tokens]
+        t.reset()
+        sample_logits = t.predict(sample)[0]
+        t.reset()
+        gpu_sample = (t.generate(sample, args.cpu_decode_tokens + 1)[0], sample_logits)
     t.close()
 
     prefill_kernels = ["qkv_gemm", "o_gemm", "gate_up_gemm", "down_gemm", "moe_gate_up_prefill",
@@ -345,7 +398,12 @@ def main():
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(d, shp, prompt, args.cpu_threads,
-                                           args.cpu_prefill_tokens, args.cpu_decode_tokens)
+                                           args.cpu_prefill_tokens, args.cpu_decode_tokens,
+                                           gpu_sample)
+        par = out["cpu_baseline"]["parity"]
+        log(f"cpu baseline parity: tokens {'identical' if par['tokens_match'] else 'DIFFER'} "
+            f"(cpu {par['tokens_cpu']}, gpu {par['tokens_gpu']}); prefill logits max |err| "
+            f"{par['prefill_logits_max_abs_err']:.3g}")
     print(json.dumps(out), flush=True)
 
 

@@ -27,6 +27,9 @@ struct oracle_model {
   size_t cached;
   int kv_format; /* ORACLE_KV_*: rounding of the values written to kc, vc */
   float *cap, *cap_final;
+  /* router tie margins [L][cap_rows] of the capture call (MoE), or NULL */
+  float* cap_margin;
+  size_t cap_row, cap_rows;
 };
 
 /* ------------------------------------------------------------------------ */
@@ -522,6 +525,8 @@ void oracle_capture_hidden(oracle_model_t* m, float* out, float* out_final) {
   m->cap_final = out_final;
 }
 
+void oracle_capture_router_margin(oracle_model_t* m, float* out) { m->cap_margin = out; }
+
 static const uint16_t* W(const oracle_model_t* m, int cls, size_t layer) {
   return (const uint16_t*)m->w[cls] + layer * m->per_layer[cls];
 }
@@ -547,6 +552,17 @@ static void moe_chunk(const oracle_model_t* m, size_t l, size_t T, const float* 
     for (size_t e = 0; e < E; e++)
       logits[e] = oracle_dot_bf16(d, xn + t * d, W(m, ORACLE_ROUTER, l) + e * d);
     oracle_topk_softmax(E, logits, K, sel + t * K, wsel + t * K);
+    if (m->cap_margin) {
+      /* k-th largest logit minus the largest one left out: how far the
+       * selected set is from changing */
+      float kth = logits[sel[t * K + K - 1]], out_best = -INFINITY;
+      for (size_t e = 0; e < E; e++) {
+        int chosen = 0;
+        for (size_t j = 0; j < K; j++) chosen |= sel[t * K + j] == (int)e;
+        if (!chosen && logits[e] > out_best) out_best = logits[e];
+      }
+      m->cap_margin[l * m->cap_rows + m->cap_row + t] = kth - out_best;
+    }
   }
   const uint8_t* gb = (const uint8_t*)m->w[ORACLE_GATE_BLOCKS] + l * m->per_layer[ORACLE_GATE_BLOCKS];
   const uint8_t* gs = (const uint8_t*)m->w[ORACLE_GATE_SCALES] + l * m->per_layer[ORACLE_GATE_SCALES];
@@ -648,6 +664,8 @@ static void store_rows(void* c_, size_t r, size_t t, float v) {
 /* Reference transformer_predict_chunk (source/transformer.c:1186-1602). */
 static void predict_chunk(oracle_model_t* m, size_t T, const int* tok, size_t lc, float* logits,
                           size_t cap_row, size_t cap_rows) {
+  m->cap_row = cap_row;
+  m->cap_rows = cap_rows;
   const oracle_config_t* c = &m->c;
   size_t d = c->embedding_dim, hd = c->head_dim, H = c->hidden_dim, L = c->layer_count;
   size_t qh = c->q_head_count, kvh = c->kv_head_count, G = qh / kvh, ctx = c->context_len;
@@ -769,5 +787,6 @@ int oracle_predict(oracle_model_t* m, size_t T, const int* tok, size_t lc, float
   }
   m->cap = NULL;
   m->cap_final = NULL;
+  m->cap_margin = NULL;
   return 0;
 }

@@ -76,6 +76,12 @@ int oracle_predict(oracle_model_t* m, size_t token_count, const int* token,
 /* Capture for the next oracle_predict of T tokens (any count): residual
  * stream after every layer [L][T][d] and final-norm output [T][d]. */
 void oracle_capture_hidden(oracle_model_t* m, float* out, float* out_final);
+/* MoE models, for the next oracle_predict of T tokens: per layer and token
+ * [L][T], the k-th largest router logit minus the largest one not selected
+ * (0 for a tie at the cut; small values mean that another summation order
+ * can select another expert set). No reference counterpart (the reference
+ * has no MoE path). */
+void oracle_capture_router_margin(oracle_model_t* m, float* out);
 
 /* KV-cache storage formats (no reference counterpart: the reference cache
  * is fp32): every key and value row written to the cache (keys after their

@@ -100,6 +100,7 @@ def load_lib():
     lib.oracle_set_threads.argtypes = [ctypes.c_int]
     lib.oracle_predict.argtypes = [P, sz, ip, sz, fp]
     lib.oracle_capture_hidden.argtypes = [P, fp, fp]
+    lib.oracle_capture_router_margin.argtypes = [P, fp]
     lib.oracle_argmax.argtypes = [fp, sz]
     lib.oracle_argmax.restype = sz
     lib.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
@@ -286,6 +287,11 @@ class OracleModel:
             hid = np.zeros((self.layers, len(tokens), self.dim), np.float32)
             fin = np.zeros((len(tokens), self.dim), np.float32)
             self.lib.oracle_capture_hidden(self.handle, fptr(hid), fptr(fin))
+            # MoE: router tie margins of this call, [layers][tokens]
+            self.router_margin = None
+            if self.config.expert_count:
+                self.router_margin = np.zeros((self.layers, len(tokens)), np.float32)
+                self.lib.oracle_capture_router_margin(self.handle, fptr(self.router_margin))
         rc = self.lib.oracle_predict(self.handle, len(tokens), toks, logits_count,
                                      fptr(logits))
         if rc != 0:

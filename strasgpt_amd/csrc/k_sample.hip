@@ -169,8 +169,9 @@ __global__ __launch_bounds__(kPick) void sample_select_kernel(SampleParams p) {
   }
 }
 
-// The first index whose running sum of renormalised probabilities (index
-// order) exceeds the coin; then the token bookkeeping of the decode loop.
+// The first index of nonzero weight whose running sum of renormalised
+// probabilities (index order) exceeds the coin; then the token bookkeeping
+// of the decode loop.
 __global__ __launch_bounds__(kPick) void sample_pick_kernel(SampleParams p) {
   __shared__ float pre[kPick];
   __shared__ int best;
@@ -196,10 +197,15 @@ __global__ __launch_bounds__(kPick) void sample_pick_kernel(SampleParams p) {
     }
   }
   __syncthreads();
+  // A thread's start (the prefix of separately summed partials) can round
+  // above the previous thread's last running sum; only an index of nonzero
+  // weight is taken, so a coin in that gap never picks a token that top-k or
+  // top-p removed (the reference's loop never returns one either).
   float cdf = pre[tid];
   for (int i = lo; i < hi; i++) {
-    cdf += w(i);
-    if (coin < cdf) {
+    const float wi = w(i);
+    cdf += wi;
+    if (wi > 0.0f && coin < cdf) {
       atomicMin(&best, i);
       break;
     }

@@ -1570,5 +1570,6 @@ extern "C" int sg_profile_read(transformer_t* t, int cls, transformer_kernel_sta
 }
 
 extern "C" const char* sg_version(void) {
-  return "strasgpt-hip gfx950 (GEMV bf16/fp32, MFMA 16x16x32 bf16x2, split-K decode attention)";
+  return "strasgpt-hip gfx950 (decode GEMV bf16/MXFP4 -> fp32; prefill GEMM MFMA 32x32x16 and 16x16x32 "
+         "bf16x2; split-bf16 MFMA attention)";
 }

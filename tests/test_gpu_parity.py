@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN_DIR, PROMPT_SEED, REPO
+from hidden_states import check_hidden
 from strasgpt_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -748,6 +749,63 @@ def test_prefill_precision_modes(model_dir):
     assert e1 < 5e-2 and e1 > 50 * e2
 
 
+def _alias_language_model(src, dst):
+    """A copy of a model directory whose tensors carry the Qwen3-VL names
+    "model.language_model.<rest>" for "model.<rest>" (lm_head.weight keeps
+    its name: the reference's alias table, source/transformer.c:520-574,
+    maps it to itself). The data bytes and their offsets are unchanged."""
+    import json
+    import shutil
+    import struct
+    os.makedirs(dst)
+    for f in os.listdir(src):
+        if not f.endswith(".safetensors"):
+            shutil.copy(os.path.join(src, f), dst)
+            continue
+        hl, hdr = synth.read_header(os.path.join(src, f))
+        out = {}
+        for name, v in hdr.items():
+            if name.startswith("model."):
+                name = "model.language_model." + name[len("model."):]
+            out[name] = v
+        blob = json.dumps(out).encode()
+        with open(os.path.join(src, f), "rb") as fi, open(os.path.join(dst, f), "wb") as fo:
+            fo.write(struct.pack("<Q", len(blob)) + blob)
+            fi.seek(8 + hl)
+            shutil.copyfileobj(fi, fo)
+    return dst
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-llama"])
+def test_language_model_aliases(name, model_dir, tmp_path):
+    """A model whose tensors use the "model.language_model." names loads as
+    the same model: QK-norm detected from the aliased q_norm name, the
+    output tied (tiny-llama) or read from lm_head.weight (tiny-qwen), and
+    logits bit-identical to the base-named model's; tokens equal the
+    oracle's on the aliased files."""
+    rt = runtime()
+    d = model_dir(name)
+    a = _alias_language_model(d, str(tmp_path / "aliased"))
+    _, hdr = synth.read_header(os.path.join(a, "model.safetensors"))
+    assert any(k.startswith("model.language_model.layers.") for k in hdr)
+    assert not any(k.startswith("model.layers.") for k in hdr)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, PROMPT_SEED)
+    steps = shp.decode_len + 1
+    with rt.Transformer(d) as t:
+        base = t.predict(prompt)
+        qk, tied = t.config.qk_norm, t.config.aliased_out_weight
+    with rt.Transformer(a) as t:
+        assert (t.config.qk_norm, t.config.aliased_out_weight) == (qk, tied)
+        got = t.predict(prompt)
+        t.reset()
+        tokens, _ = t.generate(prompt, steps)
+    assert bool(qk) == shp.qk_norm and bool(tied) == (not shp.untied)
+    np.testing.assert_array_equal(got, base)
+    om = oracle_model(a, 4)
+    assert tokens == om.generate(prompt, steps)
+
+
 def test_context_exhausted_exits(model_dir):
     d = model_dir("tiny-llama")
     code = textwrap.dedent(f"""
@@ -764,6 +822,12 @@ def test_context_exhausted_exits(model_dir):
 
 
 def _full_size(name, model_dir, steps=None):
+    """Full-size model: greedy tokens of the device loop identical to the
+    oracle's; the prompt prefill's logits, the residual stream after every
+    layer (reference source/transformer.c:1498-1504; at the scale the next
+    layer reads it, each row divided by its RMS) and the final-norm output
+    within 2e-2 rel / 1e-3 abs of the oracle's (the prompt is one chunk of
+    at most 512 tokens, the capture's limit)."""
     rt = runtime()
     shp = synth.shape(name)
     t0 = time.time()
@@ -776,14 +840,16 @@ def _full_size(name, model_dir, steps=None):
         gtok, tm = t.generate(prompt, steps)
         log(f"{name}: GPU prefill {tm.prefill_s:.3f}s decode {tm.decode_s:.3f}s")
         t.reset()
-        gl = t.predict(prompt)
+        gl, gh, gf = t.predict(prompt, capture=True)
     om = oracle_model(d, 16)
     log(f"{name}: oracle loaded")
     t0 = time.time()
-    ol = om.predict(prompt)
+    ol, oh, of = om.predict(prompt, capture=True)
     log(f"{name}: oracle prefill {time.time() - t0:.1f}s")
     np.testing.assert_allclose(gl, ol, rtol=RTOL, atol=ATOL)
     log(f"{name}: max |logit error| {np.abs(gl - ol).max():.3g}")
+    check_hidden(gh, gf, oh, of, f"{name} prefill, every layer")
+    del gh, oh
     om.reset()
     otok = om.generate(prompt, steps)
     log(f"{name}: oracle generate done; tokens {otok[:8]}...")

@@ -67,6 +67,11 @@ def test_sampler_against_reference_steps(vocab, case):
         got = dev.sample(logits, prev)
         want, coin, margin, probs = ref.sample(logits, prev, probabilities=True)
         assert dev.rng_state == ref.rng_state, f"draw {i}: generator states differ"
+        # every draw is a token of nonzero final probability: with top-k or
+        # top-p, one of the kept set (the oracle zeroes the removed ones;
+        # at temperature 0 it returns the argmax without probabilities)
+        if temp > 0:
+            assert probs[got] > 0, f"draw {i}: token {got} has probability 0 (removed)"
         if got != want:
             cdf = np.cumsum(probs.astype(np.float64))
             lo, hi = (cdf[got - 1] if got > 0 else 0.0), cdf[got]

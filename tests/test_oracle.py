@@ -368,8 +368,30 @@ def test_oracle_moe_float64(model_dir):
     np.testing.assert_allclose(got, want, rtol=2e-4, atol=2e-4)
 
 
-def numpy_forward(model_dir, prompt):
-    """float64 restatement of the forward pass (dense or MoE), last logits."""
+def test_oracle_router_margins(model_dir):
+    """The router tie margins the oracle captures (k-th largest router logit
+    minus the largest one left out, per layer and token) against the float64
+    restatement's, on a prompt long enough to make some margins small; a
+    planted swap of k-th and (k+1)-th in the restatement would change every
+    margin's sign."""
+    d = model_dir("tiny-moe")
+    om = orc.OracleModel(d, threads=2)
+    prompt = synth.prompt_tokens(256, 12, 9)
+    om.predict(prompt, capture=True)
+    got = om.router_margin
+    want = []
+    numpy_forward(d, prompt, margins=want)
+    want = np.array(want)
+    assert got.shape == want.shape == (2, 12)
+    assert (want > 0).all()
+    np.testing.assert_allclose(got, want, rtol=1e-3, atol=2e-5)
+    om.close()
+
+
+def numpy_forward(model_dir, prompt, margins=None):
+    """float64 restatement of the forward pass (dense or MoE), last logits.
+    With a list `margins`, MoE models append per layer the [T] router tie
+    margins (k-th largest router logit minus the (k+1)-th)."""
     cfg = orc.read_config(model_dir)
     tab = {n: (p, o, s) for n, p, o, s in orc.tensor_table(model_dir)}
     meta = {n: (t, shp) for n, t, shp, *_ in synth.tensor_table(model_dir)}
@@ -440,6 +462,9 @@ def numpy_forward(model_dir, prompt):
         xn = rms(x, get(pre + "post_attention_layernorm.weight"))
         if E:
             r = xn @ get(pre + "mlp.router.weight").T
+            if margins is not None:
+                srt = -np.sort(-r, axis=1)
+                margins.append(srt[:, K - 1] - srt[:, K])
             G = mx(get(pre + "mlp.experts.gate_proj_blocks"), get(pre + "mlp.experts.gate_proj_scales"))
             U = mx(get(pre + "mlp.experts.up_proj_blocks"), get(pre + "mlp.experts.up_proj_scales"))
             D = mx(get(pre + "mlp.experts.down_proj_blocks"), get(pre + "mlp.experts.down_proj_scales"))

@@ -50,8 +50,8 @@ def test_noalloc_argmax_matches_allocating_entry_point():
     b[[4000, 4500]] = 15.0
     cases.append(("5000, tie", b))
     c = rng.standard_normal(262144).astype(np.float32)  # the size limit
-    c[::9] = np.nan
-    c[262143] = 30.0
+    c[1::9] = np.nan  # from index 1: a NaN at index 0 would win by itself
+    c[262143] = 30.0  # the last element of the full staging copy
     cases.append(("limit 262144, NaNs", c))
     d = np.array([np.nan, 1.0, 2.0], np.float32)
     cases.append(("3, NaN first", d))
