@@ -181,6 +181,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(AttnParams p) {
 #pragma unroll
     for (int j = 0; j < DJ; j++) {
       const size_t idx = (size_t)t * qd + head * HD + 16 * j + 4 * g;
+      if (!p.out_hi) {  // fp32 rows (the multi-row GEMV's input)
+        *(float4*)(p.out + idx) = make_float4(o[j][0] / l, o[j][1] / l, o[j][2] / l, o[j][3] / l);
+        continue;
+      }
       uint16_t hi[4], lo[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -527,6 +531,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
 #pragma unroll
     for (int j = 0; j < DJ; j++) {
       const size_t idx = (size_t)t[q] * qd + head * HD + 16 * j + 4 * g;
+      if (!p.out_hi) {  // fp32 rows (the multi-row GEMV's input)
+        *(float4*)(p.out + idx) = make_float4(o[q][j][0] / l[q], o[q][j][1] / l[q], o[q][j][2] / l[q],
+                                              o[q][j][3] / l[q]);
+        continue;
+      }
       uint16_t hi[4], lo[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -1129,7 +1138,7 @@ void attention_split_rows(const float* kcache, const float* vcache, uint16_t* kh
 
 void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s) {
   if (p.T <= 0 || p.q_heads % p.kv_heads) ST_DIE("bad attention shape");
-  if (!p.out_hi) ST_DIE("prefill attention writes bf16 planes");
+  if (!p.out_hi && !p.out) ST_DIE("prefill attention writes bf16 planes (out_hi) or fp32 rows (out)");
   if (variant == 0 && (!p.khi || !p.klo || !p.vthi || !p.vtlo || p.ctx_pad % 32 || p.ctx_pad < p.ctx))
     ST_DIE("split-bf16 prefill attention needs the cache's bf16 planes");
   if (variant < 0 || variant > 3) ST_DIE("prefill attention variant is 0 (split bf16), 1 (fp32), 2 or 3");

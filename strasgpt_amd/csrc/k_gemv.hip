@@ -505,6 +505,319 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   if (threadIdx.x == 0) __hip_atomic_store(p.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ------------------------------------------------------------ rows form --
+// The third form for M <= MM activation rows (prefill of a few tokens): the
+// block stages the M rows of its K range in LDS ([MM][S * kStep] fp32, zero
+// past K and past row M; the RMSNorm of each row when NORM), and each
+// wavefront streams one weight row at a time through the fixed-slot
+// register ring of gemv3, multiplying every 512-element step with all MM
+// rows: per activation row and lane the decode GEMV's fp32 FMAs in step
+// order, so each weight row is read from HBM once for all rows. The MM row
+// sums of a weight row are reduced together (multi_total).
+
+// Sum over the 64 lanes of each of MM (1, 2, 4 or 8) per-lane values: in
+// rounds over lane bits 5, 4, ... each lane keeps half of its values (the
+// upper half where the bit is set) and adds its partner's copy of them, so
+// after log2(MM) rounds a lane holds one value, that of row
+// lane >> (6 - log2(MM)), summed over the lanes that differ in those bits;
+// the remaining rounds sum over the other lane bits.
+template <int MM, int BIT = 32>
+__device__ __forceinline__ float multi_total(const float (&a)[MM], int lane) {
+  if constexpr (MM == 1) {
+    float v = a[0];
+#pragma unroll
+    for (int b = BIT; b >= 1; b >>= 1) v += __shfl_xor(v, b, WAVE);
+    return v;
+  } else {
+    constexpr int H = MM / 2;
+    const bool up = (lane & BIT) != 0;
+    float h[H];
+#pragma unroll
+    for (int i = 0; i < H; i++) {
+      const float send = up ? a[i] : a[i + H];
+      const float keep = up ? a[i + H] : a[i];
+      h[i] = keep + __shfl_xor(send, BIT, WAVE);
+    }
+    return multi_total<H, BIT / 2>(h, lane);
+  }
+}
+
+// The eight bf16 weights of a 16-byte load as fp32 (exact), and their dot
+// product with eight fp32 values in element order (dot8's arithmetic).
+__device__ __forceinline__ void widen8(uint4 w, float (&f)[8]) {
+  f[0] = bf16_lo(w.x);
+  f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y);
+  f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z);
+  f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w);
+  f[7] = bf16_hi(w.w);
+}
+__device__ __forceinline__ float dot8f(const float (&f)[8], const float4& a, const float4& b, float acc) {
+  acc = fmaf(f[0], a.x, acc);
+  acc = fmaf(f[1], a.y, acc);
+  acc = fmaf(f[2], a.z, acc);
+  acc = fmaf(f[3], a.w, acc);
+  acc = fmaf(f[4], b.x, acc);
+  acc = fmaf(f[5], b.y, acc);
+  acc = fmaf(f[6], b.z, acc);
+  acc = fmaf(f[7], b.w, acc);
+  return acc;
+}
+
+template <int MM>
+constexpr int log2_rows() {
+  return MM == 1 ? 0 : MM == 2 ? 1 : MM == 4 ? 2 : 3;
+}
+
+template <int EPI, int MM, bool SPLIT>
+__device__ __forceinline__ void gemvm_store(const GemvParams& p, int m, int n, float a, float a2) {
+  const int N = p.N;
+  if (SPLIT) {
+    cstore(p.part + ((size_t)blockIdx.y * MM + m) * N + n, a);
+  } else if (EPI == GEMV_STORE) {
+    p.y[(size_t)m * N + n] = a;
+  } else if (EPI == GEMV_RESIDUAL) {
+    p.y[(size_t)m * N + n] += a;
+  } else if (EPI == GEMV_SWIGLU) {
+    p.y[(size_t)m * N + n] = silu_mul(a, a2);
+  } else {  // GEMV_QKV: q, keys (cache or staging), values at position P + m
+    const int P = *p.pos;
+    if (n < p.q_dim) {
+      p.q[(size_t)m * p.q_dim + n] = a;
+    } else if (n < p.q_dim + p.kv_dim) {
+      const int j = n - p.q_dim;
+      if (p.kv_bf16) {
+        p.kstage[(size_t)m * p.kv_dim + j] = a;  // rounded after its RoPE
+      } else {
+        const int head = j / p.head_dim, h = j % p.head_dim;
+        p.kcache[((size_t)head * p.ctx + P + m) * p.head_dim + h] = a;
+      }
+    } else {
+      const int j = n - p.q_dim - p.kv_dim;
+      const int head = j / p.head_dim, h = j % p.head_dim;
+      const size_t at = ((size_t)head * p.ctx + P + m) * p.head_dim + h;
+      if (p.kv_bf16) ((uint16_t*)p.vcache)[at] = f32_to_bf16_any(a);
+      else p.vcache[at] = a;
+    }
+  }
+}
+
+// SPLIT (residual epilogue, no RMSNorm): block (x, y) takes the rows of x
+// over K range y; row sums go to p.part[y][m][n] (agent-coherent) and the
+// last block of a row range to arrive adds them in range order, as in
+// gemv3_kernel's split form.
+constexpr int kRowsThreads = 512;  // eight wavefronts share one staging of the rows
+
+// R weight rows per wavefront at a time: every activation value read from
+// LDS serves R rows (LDS traffic per weight byte / R); the launcher lowers
+// R where R rows per wavefront would leave CUs without a block.
+template <int MM, int EPI, bool NORM, bool EXACT, int kPD, bool SPLIT, int R>
+__global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
+  constexpr int NT = kRowsThreads, WV = NT / WAVE;
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [MM][S * kStep]
+  __shared__ float red[MM][WV];
+  __shared__ int last;
+  constexpr bool DUAL = EPI == GEMV_SWIGLU;
+  static_assert(!SPLIT || (EPI == GEMV_RESIDUAL && !NORM), "split-K rows: residual epilogue only");
+  constexpr int LOADS = kPD * R * (DUAL ? 2 : 1);  // ring loads issued before the staging wait
+  const int lane = threadIdx.x % WAVE;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int N = p.N, KR = p.K, M = p.M;
+  const int SR = (KR + kStep - 1) / kStep, SP = SPLIT ? (SR + gridDim.y - 1) / gridDim.y : SR;
+  const int kbeg = SPLIT ? blockIdx.y * SP * kStep : 0;
+  const int K = SPLIT ? min(KR - kbeg, SP * kStep) : KR;  // this block's K range
+  const int S = (K + kStep - 1) / kStep, LD = S * kStep;
+  const uint16_t* wbase = p.w + kbeg;
+  // a group is WV * R rows: wavefront w takes rows (group * WV + w) * R + r
+  const int groups = (N + WV * R - 1) / (WV * R);
+  const int G = gridDim.x, per = (groups + G - 1) / G;
+  const int v = (G % kXcds == 0) ? (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds : blockIdx.x;
+  const int g0 = v * per;
+  const int glast = N - 1 - wave * R >= 0 ? (N - 1 - wave * R) / (WV * R) : -1;
+  const int nrows = max(0, min(min(groups, g0 + per), glast + 1) - g0);  // row sets of R
+  const int T = nrows * S;
+
+  // 1. this thread's RMSNorm weights (elements tid*4 + i*NT*4)
+  uint2 nv[NORM ? kV3Nw : 1];
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < kV3Nw; i++) {
+      const int k = min((int)threadIdx.x * 4 + i * NT * 4, K - 4);
+      nv[i] = *(const uint2*)(p.norm_w + k);
+    }
+  }
+  // 2. the M rows into LDS: 16 bytes per lane, 1 KiB per wavefront instruction
+  const int slots = K / 4;
+  for (int m = 0; m < M; m++) {
+    const float* xr = p.x + (size_t)m * KR + kbeg;
+    float* dst = xs + m * LD;
+    for (int u0 = wave * WAVE; u0 < slots; u0 += NT) {
+      const int u = u0 + lane;
+      if (u < slots)  // inactive lanes write nothing
+        __builtin_amdgcn_global_load_lds((const void*)(xr + u * 4), (lds_ptr_t)(dst + u0 * 4), 16, 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the rows' DMA is issued before the ring loads
+  // 3. the ring: kPD steps of R rows (and their up rows)
+  uint4 w[kPD][R], w2[DUAL ? kPD : 1][R];
+  const int lk = lane * 8;
+  int rrow = 0, rstep = 0;
+  auto load = [&](uint4 (&a)[R], uint4 (&b)[R]) {
+    // past this wave's rows: loads inside row N - 1 (never multiplied)
+    const bool past = rrow >= nrows;  // wave-uniform
+    const int k = past ? min(lk, K - 8) : EXACT ? rstep * kStep + lk : min(rstep * kStep + lk, K - 8);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const size_t row = past ? (size_t)(N - 1) : (size_t)min(((g0 + rrow) * WV + wave) * R + r, N - 1);
+      a[r] = load_nt_u4(wbase + row * KR + k);
+      if (DUAL) b[r] = load_nt_u4(p.w2 + kbeg + row * KR + k);
+    }
+    if (++rstep == S) {
+      rstep = 0;
+      rrow++;
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kPD; j++) load(w[j], w2[DUAL ? j : 0]);
+  wait_vm<LOADS>();  // norm weights and rows landed; the ring stays in flight
+  __syncthreads();
+  for (int m = 0; m < MM; m++)  // zero past K, and rows past M
+    for (int k = (m < M ? K : 0) + threadIdx.x; k < LD; k += NT) xs[m * LD + k] = 0.0f;
+  if (NORM) {  // (x * s) * w per row
+    float ss[MM];
+#pragma unroll
+    for (int m = 0; m < MM; m++) ss[m] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kV3Nw; i++) {
+      const int k = (int)threadIdx.x * 4 + i * NT * 4;
+      if (k < K) {
+#pragma unroll
+        for (int m = 0; m < MM; m++) {  // rows past M are zero
+          const float4 xv = *(const float4*)(xs + m * LD + k);
+          ss[m] = fmaf(xv.x, xv.x, ss[m]);
+          ss[m] = fmaf(xv.y, xv.y, ss[m]);
+          ss[m] = fmaf(xv.z, xv.z, ss[m]);
+          ss[m] = fmaf(xv.w, xv.w, ss[m]);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MM; m++) {
+      const float t = wave_total(ss[m]);
+      if (lane == 0) red[m][wave] = t;
+    }
+    __syncthreads();
+    float sc[MM];
+#pragma unroll
+    for (int m = 0; m < MM; m++) {
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < WV; i++) t += red[m][i];
+      sc[m] = rms_scale(t, K, p.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < kV3Nw; i++) {
+      const int k = (int)threadIdx.x * 4 + i * NT * 4;
+      if (k < K) {
+        const float n0 = bf16_to_f32((uint16_t)(nv[i].x & 0xffffu)), n1 = bf16_to_f32((uint16_t)(nv[i].x >> 16));
+        const float n2 = bf16_to_f32((uint16_t)(nv[i].y & 0xffffu)), n3 = bf16_to_f32((uint16_t)(nv[i].y >> 16));
+#pragma unroll
+        for (int m = 0; m < MM; m++) {
+          float4 o = *(const float4*)(xs + m * LD + k);
+          o.x = (o.x * sc[m]) * n0;
+          o.y = (o.y * sc[m]) * n1;
+          o.z = (o.z * sc[m]) * n2;
+          o.w = (o.w * sc[m]) * n3;
+          *(float4*)(xs + m * LD + k) = o;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  float acc[R][MM], acc2[DUAL ? R : 1][MM];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int m = 0; m < MM; m++) acc[r][m] = acc2[DUAL ? r : 0][m] = 0.0f;
+  const int mrow = lane >> (6 - log2_rows<MM>());  // the activation row this lane stores
+  const bool storer = (lane & ((WAVE / MM) - 1)) == 0 && mrow < M;
+  int step = 0, rowi = 0;
+  for (int t0 = 0; t0 < T; t0 += kPD) {
+#pragma unroll
+    for (int j = 0; j < kPD; j++) {
+      if (t0 + j < T) {
+        const int k = step * kStep + lk;
+        uint4 a[R], b[DUAL ? R : 1];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          a[r] = w[j][r];
+          if (DUAL) b[r] = w2[DUAL ? j : 0][r];
+        }
+        if (!EXACT && k >= K) {  // past K: zero weights (the rows are zero there too)
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            a[r] = make_uint4(0u, 0u, 0u, 0u);
+            if (DUAL) b[r] = make_uint4(0u, 0u, 0u, 0u);
+          }
+        }
+        // the weights widened once per step (exact), then MM rows of FMAs
+        float wf[R][8], wg[DUAL ? R : 1][8];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          widen8(a[r], wf[r]);
+          if (DUAL) widen8(b[DUAL ? r : 0], wg[DUAL ? r : 0]);
+        }
+#pragma unroll
+        for (int m = 0; m < MM; m++) {
+          const float4 xa = *(const float4*)(xs + m * LD + k);
+          const float4 xb = *(const float4*)(xs + m * LD + k + 4);
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            acc[r][m] = dot8f(wf[r], xa, xb, acc[r][m]);
+            if (DUAL) acc2[DUAL ? r : 0][m] = dot8f(wg[DUAL ? r : 0], xa, xb, acc2[DUAL ? r : 0][m]);
+          }
+        }
+        if (++step == S) {
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            const float r1 = multi_total<MM>(acc[r], lane);
+            float r2 = 0.0f;
+            if constexpr (DUAL) r2 = multi_total<MM>(acc2[r], lane);
+            const int n = ((g0 + rowi) * WV + wave) * R + r;
+            if (storer && n < N) gemvm_store<EPI, MM, SPLIT>(p, mrow, n, r1, r2);
+#pragma unroll
+            for (int m = 0; m < MM; m++) acc[r][m] = acc2[DUAL ? r : 0][m] = 0.0f;
+          }
+          step = 0;
+          rowi++;
+        }
+      }
+      load(w[j], w2[DUAL ? j : 0]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load left in flight, every partial stored
+  if (!SPLIT) return;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned done = __hip_atomic_fetch_add(p.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    last = done == gridDim.y - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  const int n0 = g0 * WV * R, n_end = min(N, min(groups, g0 + per) * WV * R);
+  for (int i = (int)threadIdx.x; i < (n_end - n0) * M; i += NT) {
+    const int m = i / (n_end - n0), n = n0 + i % (n_end - n0);
+    float sum = cload(p.part + (size_t)m * N + n);
+    for (int y = 1; y < (int)gridDim.y; y++) sum += cload(p.part + ((size_t)y * MM + m) * N + n);
+    p.y[(size_t)m * N + n] += sum;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(p.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Blocks: at most `cap`, the same number of row groups for each block, and
 // a multiple of the XCD count when there are enough groups.
 int balanced_blocks(int groups, int cap) {
@@ -615,6 +928,90 @@ bool launch_v3_split(const GemvParams& p, hipStream_t s, int cap) {
   return true;
 }
 
+// The rows form: LDS for MM rows of the K range up to kRowsLds (one block
+// of eight wavefronts per CU); rows with RMSNorm must fit whole, residual
+// rows longer than that split over K (p.part / p.counters given).
+constexpr int kRowsLds = 128 * 1024;
+constexpr int kRowsSplitMax = 16;
+
+template <int MM, int EPI, bool NORM, bool EXACT, bool SPLIT, int R>
+void rows_go_r(const GemvParams& p, dim3 grid, size_t shm, hipStream_t s) {
+  constexpr int PD = R == 1 ? 4 : 2;  // steps of R rows in flight (R x 1 KiB each, twice for SwiGLU)
+  static bool attr = false;
+  if (!attr) {
+    HIP_CHECK(hipFuncSetAttribute((const void*)gemvm_kernel<MM, EPI, NORM, EXACT, PD, SPLIT, R>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kRowsLds));
+    attr = true;
+  }
+  hipLaunchKernelGGL((gemvm_kernel<MM, EPI, NORM, EXACT, PD, SPLIT, R>), grid, dim3(kRowsThreads), shm, s, p);
+}
+
+// Rows per wavefront: the largest R (4, or 2 for the SwiGLU pair) whose
+// groups of 8 R rows still give every CU a block (cap blocks in all).
+inline int rows_r(int epi, int N, int cap_x) {
+  const int rmax = epi == GEMV_SWIGLU ? 2 : 4;
+  for (int r = rmax; r > 1; r /= 2)
+    if ((N + 8 * r - 1) / (8 * r) >= cap_x) return r;
+  return 1;
+}
+
+template <int MM, int EPI, bool NORM, bool EXACT, bool SPLIT>
+void rows_go(const GemvParams& p, dim3 grid, size_t shm, int R, hipStream_t s) {
+  if (R == 4 && EPI != GEMV_SWIGLU) rows_go_r<MM, EPI, NORM, EXACT, SPLIT, 4>(p, grid, shm, s);
+  else if (R >= 2) rows_go_r<MM, EPI, NORM, EXACT, SPLIT, 2>(p, grid, shm, s);
+  else rows_go_r<MM, EPI, NORM, EXACT, SPLIT, 1>(p, grid, shm, s);
+}
+
+template <int MM, int EPI>
+bool launch_rows(const GemvParams& p, hipStream_t s, int cap) {
+  const bool norm = p.norm_w != nullptr;
+  const int S = (p.K + kStep - 1) / kStep;
+  const int fit = kRowsLds / (MM * kStep * (int)sizeof(float));  // steps per LDS stage
+  int ranges = (S + fit - 1) / fit;
+  if (norm && (ranges > 1 || p.K > kV3Nw * kRowsThreads * 4)) return false;
+  if (ranges > 1 && (EPI != GEMV_RESIDUAL || !p.part || !p.counters || ranges > kRowsSplitMax)) return false;
+  const int SP = (S + ranges - 1) / ranges;
+  ranges = (S + SP - 1) / SP;
+  const size_t shm = (size_t)MM * SP * kStep * sizeof(float);
+  const int cap_x = std::max(1, cap / ranges);  // cap blocks in all
+  const int R = rows_r(EPI, p.N, cap_x);
+  const int rows_per_group = kRowsThreads / WAVE * R;
+  const int groups = (p.N + rows_per_group - 1) / rows_per_group;
+  const int blocks = balanced_blocks(groups, cap_x);
+  if (ranges > 1 && blocks > kGemvCounters) return false;
+  const dim3 grid(blocks, ranges);
+  const bool exact = p.K % kStep == 0;  // every range's steps then lie inside K
+  if constexpr (EPI == GEMV_RESIDUAL) {
+    if (ranges > 1) {
+      if (exact) rows_go<MM, EPI, false, true, true>(p, grid, shm, R, s);
+      else rows_go<MM, EPI, false, false, true>(p, grid, shm, R, s);
+      return true;
+    }
+  }
+  if (norm) {
+    if (exact) rows_go<MM, EPI, true, true, false>(p, grid, shm, R, s);
+    else rows_go<MM, EPI, true, false, false>(p, grid, shm, R, s);
+  } else {
+    if (exact) rows_go<MM, EPI, false, true, false>(p, grid, shm, R, s);
+    else rows_go<MM, EPI, false, false, false>(p, grid, shm, R, s);
+  }
+  return true;
+}
+
+bool rows_fit(int M, int K, bool norm) {
+  const int MM = M <= 4 ? 4 : 8;
+  const int S = (K + kStep - 1) / kStep, fit = kRowsLds / (MM * kStep * (int)sizeof(float));
+  const int ranges = (S + fit - 1) / fit;
+  return M >= 1 && M <= kRowsMax && (norm ? ranges == 1 && K <= kV3Nw * kRowsThreads * 4 : ranges <= kRowsSplitMax);
+}
+
+template <int EPI>
+bool rows_dispatch(const GemvParams& p, hipStream_t s) {
+  constexpr int cap = 256;  // one block per CU: each CU stages the rows once (two per CU measured slower)
+  if (p.M <= 4) return launch_rows<4, EPI>(p, s, cap);
+  return launch_rows<8, EPI>(p, s, cap);
+}
+
 template <int R, int U, int EPI>
 void launch(const GemvParams& p, hipStream_t s, int cap) {
   const bool lds = p.K <= kMaxLdsK;
@@ -640,6 +1037,25 @@ void check(const GemvParams& p, int epi) {
 }
 
 }  // namespace
+
+bool gemv_rows_fit(int M, int K, bool norm) { return rows_fit(M, K, norm); }
+
+bool gemv_rows(const GemvParams& p, int epi, hipStream_t s) {
+  check(p, epi);
+  if (p.M < 1 || p.M > kRowsMax) ST_DIE("multi-row GEMV takes 1 to 8 activation rows");
+  if (epi == GEMV_QKV && !p.kv_bf16 && !p.kcache) ST_DIE("multi-row QKV GEMV needs the key cache");
+  if (epi == GEMV_QKV && p.kv_bf16 && !p.kstage) ST_DIE("multi-row QKV GEMV needs the key staging rows");
+  bool ok = false;
+  switch (epi) {
+    case GEMV_STORE: ok = rows_dispatch<GEMV_STORE>(p, s); break;
+    case GEMV_RESIDUAL: ok = rows_dispatch<GEMV_RESIDUAL>(p, s); break;
+    case GEMV_QKV: ok = rows_dispatch<GEMV_QKV>(p, s); break;
+    case GEMV_SWIGLU: ok = rows_dispatch<GEMV_SWIGLU>(p, s); break;
+    default: ST_DIE("unknown GEMV epilogue");
+  }
+  if (ok) HIP_CHECK(hipGetLastError());
+  return ok;
+}
 
 void gemv(const GemvParams& p, int epi, hipStream_t s) {
   check(p, epi);

@@ -42,9 +42,27 @@ struct GemvParams {
   // chunked form.
   float* part;
   unsigned* counters;
+  // Multi-row form (gemv_rows): M activation rows x[m][K] (row stride K),
+  // outputs y[m][N] (row stride N), q[m][q_dim]; QKV keys of row m go to
+  // kcache at position *pos + m (fp32 cache) or to kstage[m][kv_dim] (bf16
+  // cache: rounded after their RoPE), values to vcache at *pos + m.
+  int M;
+  float* kcache;
+  float* kstage;
 };
 constexpr int kGemvCounters = 4096;
 void gemv(const GemvParams& p, int epilogue, hipStream_t s);
+// Prompts of at most kRowsMax tokens: every weight row streamed once into
+// fp32 FMAs for all M rows (the decode GEMV's arithmetic per row), with the
+// RMSNorm of each input row fused in (p.norm_w); rows longer than one LDS
+// stage split over K (residual epilogue, p.part with kRowsMax * N floats
+// per range, p.counters). False when the shape is not supported (the
+// caller then runs the prefill GEMMs).
+constexpr int kRowsMax = 8;
+bool gemv_rows(const GemvParams& p, int epilogue, hipStream_t s);
+// Whether gemv_rows takes M rows of length K (norm: with the RMSNorm; rows
+// without it may split over K when the residual scratch is given).
+bool gemv_rows_fit(int M, int K, bool norm);
 
 // MXFP4 expert GEMV rows (decode MoE). Rows of expert e are
 // [N][K/32][16] code bytes and [N][K/32] E8M0 exponents.
@@ -186,7 +204,7 @@ struct AttnParams {
   const float* kcache;   // layer base [kv_heads][ctx][hd] (bf16 when kv_bf16)
   const float* vcache;
   int kv_bf16;
-  float* out;            // decode: [q_heads*hd] fp32
+  float* out;            // decode: [q_heads*hd] fp32; prefill without out_hi: [T][q_heads*hd] fp32
   uint16_t* out_hi;      // prefill: [T][q_heads*hd] bf16 planes (O-GEMM input)
   uint16_t* out_lo;      //   (out_lo may be null)
   const int* pos;        // device: position of the first query (cached count)

@@ -775,6 +775,132 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
   }
 }
 
+// Prompts of at most sg::kRowsMax tokens on dense models: the projections
+// as multi-row GEMVs (each weight row streamed once into fp32 FMAs for all
+// rows, the RMSNorms fused in; the residual stream x stays fp32 and is
+// updated in place), attention as in layer_prefill with fp32 output rows.
+// STRASGPT_PREFILL_ROWS=0 keeps such prompts on the GEMMs.
+bool prefill_rows(Dev* D, int T) {
+  const char* e = getenv("STRASGPT_PREFILL_ROWS");
+  const bool off = e && !strcmp(e, "0");
+  return !off && !D->moe && T >= 2 && T <= sg::kRowsMax && D->precision == sg::GEMM_SPLIT2 &&
+         sg::gemv_rows_fit(T, D->d, true) && sg::gemv_rows_fit(T, D->qd, false) &&
+         sg::gemv_rows_fit(T, D->H, false);
+}
+
+void layer_prefill_rows(Dev* D, int l, int T) {
+  hipStream_t s = D->stream;
+  const size_t cache_layer = (size_t)D->kvh * D->ctx * D->hd;
+  float* kc = kv_layer(D, D->kc, l);
+  float* vc = kv_layer(D, D->vc, l);
+  const double d = D->d, M = T;
+  auto need = [](bool ok) {
+    if (!ok) ST_DIE("multi-row GEMV refused a shape it was planned for");
+  };
+
+  sg::GemvParams g{};
+  g.w = W16(D, W_Q, l);
+  g.x = D->x;
+  g.norm_w = W16(D, W_MHA_NORM, l);
+  g.eps = D->eps;
+  g.N = D->qkv_rows;
+  g.K = D->d;
+  g.M = T;
+  g.q = D->q;
+  g.kcache = kc;
+  g.kstage = D->kv_bf16 ? D->kstage : nullptr;
+  g.vcache = vc;
+  g.pos = D->pos;
+  g.q_dim = D->qd;
+  g.kv_dim = D->kvd;
+  g.head_dim = D->hd;
+  g.ctx = D->ctx;
+  g.kv_bf16 = D->kv_bf16;
+  {
+    Prof pr(D, K_QKV_GEMM, (double)D->qkv_rows * d * 2, 2.0 * M * D->qkv_rows * d);
+    need(sg::gemv_rows(g, sg::GEMV_QKV, s));
+  }
+  {
+    Prof pr(D, K_ELEM, 2.0 * M * (D->qd + D->kvd) * 4, 0);
+    sg::qk_norm_rope(D->q, D->qh, kc, D->kvh, T, D->pos, D->ctx, D->hd,
+                     D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr,
+                     D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
+                     D->po, D->pst, D->kv_bf16 ? D->kstage : nullptr, s);
+  }
+  const size_t P0 = D->host_pos;
+  const size_t vt_layer = (size_t)D->kvh * D->hd * D->ctx_pad;
+  {
+    const int r0 = (int)(P0 / 32 * 32), r1 = (int)(P0 + T);
+    Prof pr(D, K_ELEM, 2.0 * (r1 - r0) * D->kvd * 4 * 2, 0);
+    sg::attention_split_rows(kc, vc, D->kp_hi + l * cache_layer, D->kp_lo + l * cache_layer,
+                             D->vt_hi + l * vt_layer, D->vt_lo + l * vt_layer, D->kvh, D->ctx,
+                             D->ctx_pad, D->hd, r0, r1, D->kv_bf16, s);
+  }
+  sg::AttnParams a{};
+  a.q = D->q;
+  a.kcache = kc;
+  a.vcache = vc;
+  a.kv_bf16 = D->kv_bf16;
+  a.khi = D->kp_hi + l * cache_layer;
+  a.klo = D->kp_lo + l * cache_layer;
+  a.vthi = D->vt_hi + l * vt_layer;
+  a.vtlo = D->vt_lo + l * vt_layer;
+  a.ctx_pad = D->ctx_pad;
+  a.out = D->att;  // fp32 rows [T][qd]
+  a.pos = D->pos;
+  a.T = T;
+  a.q_heads = D->qh;
+  a.kv_heads = D->kvh;
+  a.hd = D->hd;
+  a.ctx = D->ctx;
+  {
+    const double pairs = M * (double)D->host_pos + M * (M + 1) / 2;
+    Prof pr(D, K_ATT_PRE, 2.0 * D->kvh * ((double)D->host_pos + M) * D->hd * (D->kv_bf16 ? 2 : 4),
+            4.0 * D->qh * D->hd * pairs);
+    sg::attention_prefill(a, s);
+  }
+  sg::GemvParams o{};
+  o.w = W16(D, W_O, l);
+  o.x = D->att;
+  o.N = D->d;
+  o.K = D->qd;
+  o.M = T;
+  o.y = D->x;
+  o.part = D->ws;
+  o.counters = D->gemv_cnt;
+  {
+    Prof pr(D, K_O_GEMM, (double)D->qd * d * 2, 2.0 * M * D->qd * d);
+    need(sg::gemv_rows(o, sg::GEMV_RESIDUAL, s));
+  }
+  sg::GemvParams f{};
+  f.w = W16(D, W_GATE, l);
+  f.w2 = W16(D, W_UP, l);
+  f.x = D->x;
+  f.norm_w = W16(D, W_FFN_NORM, l);
+  f.eps = D->eps;
+  f.N = D->H;
+  f.K = D->d;
+  f.M = T;
+  f.y = D->act;  // [T][H]
+  {
+    Prof pr(D, K_GU_GEMM, 2.0 * D->H * d * 2, 4.0 * M * D->H * d);
+    need(sg::gemv_rows(f, sg::GEMV_SWIGLU, s));
+  }
+  sg::GemvParams dn{};
+  dn.w = W16(D, W_DOWN, l);
+  dn.x = D->act;
+  dn.N = D->d;
+  dn.K = D->H;
+  dn.M = T;
+  dn.y = D->x;
+  dn.part = D->ws;
+  dn.counters = D->gemv_cnt;
+  {
+    Prof pr(D, K_DOWN_GEMM, (double)D->H * d * 2, 2.0 * M * D->H * d);
+    need(sg::gemv_rows(dn, sg::GEMV_RESIDUAL, s));
+  }
+}
+
 // Logits of chunk rows [T - lc, T): final RMSNorm fused into the GEMV.
 void classifier(Dev* D, int T, int lc) {
   for (int r = 0; r < lc; r++) {
@@ -799,9 +925,11 @@ void forward_chunk(Dev* D, const int* tok, int T, int lc) {
     sg::embed(tok, T, W16(D, W_EMB), D->d, D->x, D->stream);
   }
   const bool capture = D->cap_out != nullptr;
-  if (T > 1) prefill_norm(D, T, 0, W16(D, W_MHA_NORM, 0));
+  const bool rows = T > 1 && prefill_rows(D, T);
+  if (T > 1 && !rows) prefill_norm(D, T, 0, W16(D, W_MHA_NORM, 0));
   for (int l = 0; l < D->L; l++) {
     if (T == 1) layer_decode(D, l);
+    else if (rows) layer_prefill_rows(D, l, T);
     else layer_prefill(D, l, T, l + 1 < D->L ? W16(D, W_MHA_NORM, l + 1) : nullptr);
     if (capture)
       HIP_CHECK(hipMemcpyAsync(D->cap_dev + (size_t)l * T * D->d, D->x,

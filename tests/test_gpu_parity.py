@@ -119,12 +119,14 @@ def test_gemm_tile_orders(model_dir, monkeypatch):
         assert np.array_equal(got[order], got["0"])
 
 
-def test_small_prompt_split_gemms(model_dir):
+def test_small_prompt_split_gemms(model_dir, monkeypatch):
     """Prompts of at most 32 rows run the QKV GEMM split over K (partial
     sums, then an epilogue kernel that adds them in split order and writes
     q and the key / value cache rows): prefill logits and greedy tokens
     against the oracle, and a 40-row prompt (the fused epilogue) agrees
-    too."""
+    too. (Dense prompts of at most 8 rows take the multi-row GEMVs unless
+    STRASGPT_PREFILL_ROWS=0, which this test sets.)"""
+    monkeypatch.setenv("STRASGPT_PREFILL_ROWS", "0")
     rt = runtime()
     d = model_dir("small-m")
     shp = synth.shape("small-m")
@@ -144,6 +146,47 @@ def test_small_prompt_split_gemms(model_dir):
             t.reset()
             gtok, _ = t.generate(prompt, 6)
             assert gtok == otok
+
+
+@pytest.mark.parametrize("name,kv", [("small-m", "fp32"), ("tiny-wide", "fp32"), ("tiny-wide2", "fp32"),
+                                     ("small-m", "bf16"), ("tiny-llama", "fp32")])
+def test_prefill_rows_form(name, kv, model_dir, monkeypatch):
+    """Dense prompts of 2 to 8 tokens take the multi-row GEMVs (each weight
+    row read once for every prompt row, fp32 FMAs, RMSNorm fused in; down
+    projections longer than one LDS stage split over K: tiny-wide's 20480
+    and tiny-wide2's 32768; rows not a multiple of 512 elements: tiny-wide's
+    64 and tiny-llama's): prefill logits and the hidden states of every
+    layer against the oracle, and against the GEMM path
+    (STRASGPT_PREFILL_ROWS=0) within 2e-3; greedy tokens from the prefill
+    identical to the oracle's; with a bf16 cache against the oracle's bf16
+    cache."""
+    from oracle import oracle as orc
+    rt = runtime()
+    d = model_dir(name)
+    shp = synth.shape(name)
+    om = orc.OracleModel(d, threads=16, kv_format=orc.KV_BF16 if kv == "bf16" else orc.KV_F32)
+    for T in (2, 3, 5, 8):
+        prompt = synth.prompt_tokens(shp.vocab, T, 40 + T)
+        om.reset()
+        ol, oh, of = om.predict(prompt, capture=True)
+        om.reset()
+        otok = om.generate(prompt, 4)
+        got = {}
+        for form in ("1", "0"):
+            monkeypatch.setenv("STRASGPT_PREFILL_ROWS", form)
+            with rt.Transformer(d) as t:
+                if kv == "bf16":
+                    t.set_kv_cache_format(rt.KV_BF16)
+                gl, gh, gf = t.predict(prompt, capture=True)
+                t.reset()
+                gtok, _ = t.generate(prompt, 4)
+            got[form] = gl
+            err = float(np.abs(gl - ol).max())
+            log(f"{name} kv {kv} T={T} rows form {form}: max |logit error| {err:.3g}")
+            np.testing.assert_allclose(gl, ol, rtol=RTOL, atol=ATOL)
+            check_hidden(gh, gf, oh, of, f"{name} T={T} form {form}")
+            assert gtok == otok
+        assert float(np.abs(got["1"] - got["0"]).max()) <= 2e-3
 
 
 @pytest.mark.parametrize("kernel", ["x3", "x3-16", "x3-32", "fp32"])
