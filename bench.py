@@ -21,7 +21,8 @@ reported beside it). The cpu_baseline is the reference's own C sources
 for -march=native) driven by the reference's greedy loop on a bounded
 sample of the same model files on the host cores, with the reference's
 timing boundaries (source/strasgpt.c:206-274); where that binary is absent,
-the oracle (the C + OpenMP restatement of the reference forward pass). The
+and for the MoE model (the reference has no MoE path), the oracle (the C +
+OpenMP restatement of the reference forward pass). The
 GPU runs the same sample, and cpu_baseline.parity compares the two: greedy
 tokens identical, prefill logits within 2e-2 relative / 1e-3 absolute.
 Under rocprofv3 (kernel trace or counters) the decode steps are launched
@@ -117,7 +118,9 @@ def cpu_baseline(d, shp, prompt, threads, prefill_tokens, decode_tokens, gpu):
     sample_prompt = prompt[:prefill_tokens]
     info = {"cores": threads, "host_physical_cores": phys, "threads_available": avail,
             "cpu_model": model}
-    if os.path.exists(ref_manifest.BASELINE):
+    # the reference has no MoE path: MoE models time the oracle (its C +
+    # OpenMP restatement with the MoE semantics of this library)
+    if os.path.exists(ref_manifest.BASELINE) and not shp.experts:
         with tempfile.TemporaryDirectory(prefix="strasgpt_cpu_") as tmp:
             man = ref_manifest.write(d, sample_prompt, decode_tokens + 1,
                                      os.path.join(tmp, "manifest.txt"))

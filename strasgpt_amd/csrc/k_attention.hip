@@ -353,8 +353,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
   const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, g = lane / 16, c = lane % 16;
   const int nqb = (p.T + PQB - 1) / PQB;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
-  const int head = blockIdx.y;
+  // grid (heads, query blocks): blocks are dispatched head-fastest, so
+  // every head's longest causal range goes first and the shortest last
+  const int qb = nqb - 1 - (int)blockIdx.y;
+  const int head = blockIdx.x;
   const int G = p.q_heads / p.kv_heads, kvh = head / G;
   const int P = *p.pos + p.q0, T = p.T;
   const int qd = p.q_heads * HD;
@@ -416,9 +418,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
     for (int kk = 0; kk < NKK; kk++) {
       float x[8];
       const int d = 32 * kk + 8 * g;
-      if (d < HD) {
+      if (d < HD) {  // the base-2 score scale folded into q
         const float4 a = *(const float4*)(qr + d), b = *(const float4*)(qr + d + 4);
-        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        x[0] = a.x * sl2; x[1] = a.y * sl2; x[2] = a.z * sl2; x[3] = a.w * sl2;
+        x[4] = b.x * sl2; x[5] = b.y * sl2; x[6] = b.z * sl2; x[7] = b.w * sl2;
       } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) x[e] = 0.0f;
@@ -480,36 +483,45 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_x3_kernel(AttnParams p) {
       }
     }
     // Causal mask and online softmax of each query (base 2; lane groups g
-    // hold keys 8 g .. 8 g + 7 of the tile).
+    // hold keys 8 g .. 8 g + 7 of the tile). The reference point m moves
+    // only when a query's tile maximum exceeds it by more than 8 (p then
+    // stays below 2^8), and then for the whole wave at once: most tiles
+    // skip the rescale of O and l. Key 0 is visible to every query, so m is
+    // finite from the first tile on and a fully masked row gives p = 0.
     bf16x8 ph[QS], pl[QS];
     const bool full = kv0 + KT - 1 <= vis_all;  // every key of the tile visible to every query of the block
 #pragma unroll
     for (int q = 0; q < QS; q++) {
       float pv[8];
-      float mx = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float v = full || kv0 + 8 * g + j <= vis[q] ? sc[q][j >> 2][j & 3] * sl2 : -INFINITY;
-        pv[j] = v;
-        mx = fmaxf(mx, v);
+        for (int j = 0; j < 8; j++) pv[j] = sc[q][j >> 2][j & 3];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) pv[j] = kv0 + 8 * g + j <= vis[q] ? sc[q][j >> 2][j & 3] : -INFINITY;
       }
+      float mx = fmaxf(fmaxf(fmaxf(pv[0], pv[1]), fmaxf(pv[2], pv[3])), fmaxf(fmaxf(pv[4], pv[5]), fmaxf(pv[6], pv[7])));
       mx = fmaxf(mx, xor16_max(mx));
       mx = fmaxf(mx, xor32_max(mx));
-      const float mn = fmaxf(m[q], mx);
-      const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[q] - mn);
+      const bool up = mx > m[q] + 8.0f;  // (m = -inf before the first tile)
+      if (__builtin_amdgcn_ballot_w64(up)) {
+        const float mn = up ? mx : m[q];
+        const float corr = __builtin_amdgcn_exp2f(m[q] - mn);  // 0 at the first tile (o, l are 0)
+        l[q] *= corr;
+#pragma unroll
+        for (int j = 0; j < DJ; j++) o[q][j] *= corr;
+        m[q] = mn;
+      }
       float rs = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float e = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pv[j] - mn);
+        const float e = __builtin_amdgcn_exp2f(pv[j] - m[q]);
         pv[j] = e;
         rs += e;
       }
       rs = xor16_sum(rs);
       rs = xor32_sum(rs);
-      l[q] = l[q] * corr + rs;
-      m[q] = mn;
-#pragma unroll
-      for (int j = 0; j < DJ; j++) o[q][j] *= corr;
+      l[q] += rs;
       split8(pv, ph[q], pl[q]);
     }
 #pragma unroll
@@ -1146,7 +1158,9 @@ void attention_prefill_variant(const AttnParams& p, int variant, hipStream_t s) 
   const bool fp32 = variant == 1;
   // split bf16: 32 queries per wave when 128-query blocks give 2 per CU
   const bool wide = variant == 3 || (variant == 0 && (long)((p.T + 2 * PQ - 1) / (2 * PQ)) * p.q_heads >= 512);
-  const dim3 grid((p.T + (wide ? 2 * PQ : PQ) - 1) / (wide ? 2 * PQ : PQ), p.q_heads);
+  const int nqb = (p.T + (wide ? 2 * PQ : PQ) - 1) / (wide ? 2 * PQ : PQ);
+  // x3: (heads, query blocks), longest ranges of every head first; fp32: (query blocks, heads)
+  const dim3 grid = fp32 ? dim3(nqb, p.q_heads) : dim3(p.q_heads, nqb);
   switch (p.hd) {
 #define PREFILL_CASE(HD)                                                                         \
   case HD:                                                                                       \

@@ -641,9 +641,10 @@ int residual_gemm(Dev* D, const uint16_t* a_hi, const uint16_t* a_lo, int lda,
 
 // Queries per prefill attention launch (measured on the 8192-token chunk):
 // 512 for the fp32 kernel (one block per CU: a launch over a long chunk
-// balances its causal ranges less well); 2048 for the split-bf16 kernel,
-// which holds two blocks per CU (512-query launches leave half of them
-// empty: 3.5 vs 2.5 ms per layer). STRASGPT_ATTN_ROWS overrides (>= 64).
+// balances its causal ranges less well); the whole chunk for the split-bf16
+// kernel, whose blocks go out longest causal range first across all heads
+// (2048, 4096, 8192 queries per launch: 1.82, 1.66, 1.59 ms per layer; 512:
+// 3.5 ms, half the CUs empty). STRASGPT_ATTN_ROWS overrides (>= 64).
 int attn_rows() {
   const char* e = getenv("STRASGPT_ATTN_ROWS");
   if (e && *e) {
@@ -652,7 +653,7 @@ int attn_rows() {
     return v;
   }
   const char* k = getenv("STRASGPT_PREFILL_ATTN");
-  return k && !strcmp(k, "fp32") ? 512 : 2048;
+  return k && !strcmp(k, "fp32") ? 512 : 1 << 30;
 }
 
 // One layer over T > 1 rows. On entry D->xn_hi/lo hold the layer's input
