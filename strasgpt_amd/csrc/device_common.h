@@ -182,6 +182,13 @@ __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
   return (float)(1.0 / (double)sqrtf(ss + eps));
 }
 
+// Compiler-only ordering point: no memory access is moved across it by the
+// compiler (no instruction is emitted). The cross-block hand-offs put one
+// before the wait that completes a block's partial stores and one after the
+// arrival check, so that their order is fixed in the code as well as by
+// the wait and the control dependence on the arrival count.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
 // Agent-coherent scalar access: relaxed atomics at device scope, which
 // bypass the per-XCD L2 for data exchanged between blocks of one launch.
 // A store is visible to another block's cload once the storing wave has

@@ -983,6 +983,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParam
   // sequence without its cache write-back and invalidate, which only
   // non-atomic accesses need. (An acq_rel increment adds both: +1.3 us per
   // launch at 640 positions, +2.6 us at 2176.)
+  compiler_fence();
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
@@ -992,6 +993,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParam
   }
   __syncthreads();
   if (!flag) return;
+  compiler_fence();
 
   // Last block of kv head g: wave w combines heads w*GW .., lane c holding
   // block c's weight (scores in base 2). Every block partial of the lane's

@@ -482,6 +482,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
       load(w[j], w2[DUAL ? j : 0]);
     }
   }
+  compiler_fence();
   __builtin_amdgcn_s_waitcnt(0);  // no load left in flight, every partial stored
   if (!SPLIT) return;
   // Hand-off (the decode attention's): partials are written and read only
@@ -496,6 +497,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   }
   __syncthreads();
   if (!last) return;
+  compiler_fence();
   const int n_end = min(N, min(groups, g0 + per) * WV);
   for (int n = g0 * WV + (int)threadIdx.x; n < n_end; n += NT) {
     float sum = cload(p.part + n);
@@ -798,9 +800,10 @@ __global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
       load(w[j], w2[DUAL ? j : 0]);
     }
   }
+  compiler_fence();
   __builtin_amdgcn_s_waitcnt(0);  // no load left in flight, every partial stored
   if (!SPLIT) return;
-  __syncthreads();
+  __syncthreads();  // (the hand-off of gemv3_kernel's split form)
   if (threadIdx.x == 0) {
     const unsigned done = __hip_atomic_fetch_add(p.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
@@ -808,6 +811,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
   }
   __syncthreads();
   if (!last) return;
+  compiler_fence();
   const int n0 = g0 * WV * R, n_end = min(N, min(groups, g0 + per) * WV * R);
   for (int i = (int)threadIdx.x; i < (n_end - n0) * M; i += NT) {
     const int m = i / (n_end - n0), n = n0 + i % (n_end - n0);
