@@ -908,6 +908,57 @@ __device__ __forceinline__ int q_swz(int r) { return (r >> 1) & 7; }  // 128-byt
 // explicit waits and barriers order the data).
 typedef unsigned q_u32x4 __attribute__((ext_vector_type(4)));
 
+// The tile of a grouped-GEMM block, found by one wavefront: tile_info =
+// {expert or -1 past the last tile, first slot of the tile, column tile}.
+// The (slot tile, column tile) grid is laid out per XCD (blocks are
+// dispatched to the 8 XCDs round-robin by linear id): XCD x takes a
+// contiguous run of the slot tiles (about an eighth of the experts) and
+// walks the column tiles in its outer loop, so the A rows of its tiles
+// stay in its L2 across column tiles and the slot tiles of one expert, run
+// side by side, share each column tile's codes.
+template <int BM>
+__device__ void group_tile_lookup(const MoeGemmParams& p, int lane, int* tile_info) {
+  // total slot tiles (experts in order, ceil(count / BM) each)
+  int tr = 0;
+  for (int e0 = 0; e0 < p.E; e0 += WAVE) {
+    const int e = e0 + lane;
+    const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
+    tr += wave_sum_int((c + BM - 1) / BM);
+  }
+  const int lin = (int)(blockIdx.x + blockIdx.y * gridDim.x);
+  const int xcd = lin % kXcds, j = lin / kXcds, ny = (int)gridDim.y;
+  const int lo = xcd * tr / kXcds, nt = (xcd + 1) * tr / kXcds - lo;
+  int e_found = -1, m0 = 0, y = 0;
+  if (nt > 0 && j < nt * ny) {
+    y = j / nt;
+    const int T = lo + j % nt;
+    int base = 0;
+    for (int e0 = 0; e0 < p.E && e_found < 0; e0 += WAVE) {
+      const int e = e0 + lane;
+      const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
+      int tiles = (c + BM - 1) / BM, incl = tiles;
+#pragma unroll
+      for (int off = 1; off < WAVE; off <<= 1) {
+        const int v = __shfl_up(incl, off, WAVE);
+        if (lane >= off) incl += v;
+      }
+      const int excl = base + incl - tiles;
+      const unsigned long long m = __ballot(T >= excl && T < excl + tiles);
+      if (m) {
+        const int src = __ffsll((long long)m) - 1;
+        e_found = __shfl(e0 + lane, src, WAVE);
+        m0 = (T - __shfl(excl, src, WAVE)) * BM;
+      }
+      base += __shfl(incl, WAVE - 1, WAVE);
+    }
+  }
+  if (lane == 0) {
+    tile_info[0] = e_found;
+    tile_info[1] = m0;
+    tile_info[2] = y;
+  }
+}
+
 // BM slots per block (32 or 64; 64 when experts average enough slots that
 // one tile covers most of them, so each expert's weights stream once).
 template <bool DUAL, int BM>
@@ -920,53 +971,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char ql[];
   int* tile_info = (int*)(ql + QL::info);
   const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
-  // Tile of this block. The (slot tile, column tile) grid is laid out per
-  // XCD (blocks are dispatched to the 8 XCDs round-robin by linear id): XCD
-  // x takes a contiguous run of the slot tiles (about an eighth of the
-  // experts) and walks the column tiles in its outer loop, so the A rows of
-  // its tiles stay in its L2 across column tiles and the slot tiles of one
-  // expert, run side by side, share each column tile's codes.
-  if (wave == 0) {
-    // total slot tiles (experts in order, ceil(count / BM) each)
-    int tr = 0;
-    for (int e0 = 0; e0 < p.E; e0 += WAVE) {
-      const int e = e0 + lane;
-      const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
-      tr += wave_sum_int((c + BM - 1) / BM);
-    }
-    const int lin = (int)(blockIdx.x + blockIdx.y * gridDim.x);
-    const int xcd = lin % kXcds, j = lin / kXcds, ny = (int)gridDim.y;
-    const int lo = xcd * tr / kXcds, nt = (xcd + 1) * tr / kXcds - lo;
-    int e_found = -1, m0 = 0, y = 0;
-    if (nt > 0 && j < nt * ny) {
-      y = j / nt;
-      const int T = lo + j % nt;
-      int base = 0;
-      for (int e0 = 0; e0 < p.E && e_found < 0; e0 += WAVE) {
-        const int e = e0 + lane;
-        const int c = e < p.E ? p.offs[e + 1] - p.offs[e] : 0;
-        int tiles = (c + BM - 1) / BM, incl = tiles;
-#pragma unroll
-        for (int off = 1; off < WAVE; off <<= 1) {
-          const int v = __shfl_up(incl, off, WAVE);
-          if (lane >= off) incl += v;
-        }
-        const int excl = base + incl - tiles;
-        const unsigned long long m = __ballot(T >= excl && T < excl + tiles);
-        if (m) {
-          const int src = __ffsll((long long)m) - 1;
-          e_found = __shfl(e0 + lane, src, WAVE);
-          m0 = (T - __shfl(excl, src, WAVE)) * BM;
-        }
-        base += __shfl(incl, WAVE - 1, WAVE);
-      }
-    }
-    if (lane == 0) {
-      tile_info[0] = e_found;
-      tile_info[1] = m0;
-      tile_info[2] = y;
-    }
-  }
+  if (wave == 0) group_tile_lookup<BM>(p, lane, tile_info);
   __syncthreads();
   const int e = tile_info[0], m0 = tile_info[1];
   if (e < 0) return;  // past the last tile (the grid is an upper bound)
@@ -974,6 +979,10 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
   const int cols = DUAL ? QBR / 2 : QBR;  // output columns per block
   const int n0 = tile_info[2] * cols;
   const int K = p.K, nb = K / 32, nk = K / QKS;
+  // 16-slot sub-tiles holding at least one slot of the expert: the others
+  // are padding, whose A reads and products are skipped (wave-uniform, so
+  // the MFMAs always run with every lane on)
+  const int act = __builtin_amdgcn_readfirstlane(min(MS, (cnt - m0 + 15) / 16));
 
   // --- DMA sources (per lane) ---
   // A: instruction i (< QAI) of this wave covers stage rows 8 (QAI wave + i)
@@ -1103,6 +1112,7 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     for (int kk = 0; kk < 2; kk++)
 #pragma unroll
       for (int mi = 0; mi < MS; mi++) {
+        if (mi >= act) break;
         const int ch = 4 * kk + g, r = 16 * mi + c;
         ah[kk][mi] = achunk(as, r, ch);
         al[kk][mi] = achunk(as, BM + r, ch);
@@ -1122,23 +1132,32 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
         b[f] = __builtin_bit_cast(bf16x8, v);
       }
 #pragma unroll
-      for (int mi = 0; mi < MS; mi++)
+      for (int mi = 0; mi < MS; mi++) {
+        if (mi >= act) break;
 #pragma unroll
         for (int f = 0; f < QFR; f++) {
           acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kk][mi], b[f], acc[mi][f], 0, 0, 0);
           acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[kk][mi], b[f], acc[mi][f], 0, 0, 0);
         }
+      }
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // the clamped tail loads land before the wave ends
-  // lane holds C[4 (lane / 16) + i][lane % 16] of each 16 x 16 tile
+  // lane holds C[4 (lane / 16) + i][lane % 16] of each 16 x 16 tile; the
+  // slots of its rows are read first (one wait for all of them, not one
+  // per row before its stores)
+  int slot[MS][4];
+#pragma unroll
+  for (int mi = 0; mi < MS; mi++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) slot[mi][i] = p.order[rbeg + min(m0 + 16 * mi + 4 * g + i, cnt - 1)];
 #pragma unroll
   for (int mi = 0; mi < MS; mi++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int r = 16 * mi + 4 * g + i;
       if (m0 + r >= cnt) continue;
-      const int s2 = p.order[rbeg + m0 + r];
+      const int s2 = slot[mi][i];
       if (DUAL) {
 #pragma unroll
         for (int j = 0; j < HF; j++) {
