@@ -670,8 +670,9 @@ int forced_tile() {
   if (!strcmp(v, "64x128")) return 2;
   if (!strcmp(v, "64x64")) return 1;
   if (!strcmp(v, "64x64x64s6")) return 8;
-  ST_DIE("STRASGPT_GEMM_TILE must be 256x256, 128x256, 128x128, 64x128x64, 64x128x64s4, 64x128, 64x64 "
-         "or 64x64x64s6");
+  if (!strcmp(v, "128x384")) return 9;
+  ST_DIE("STRASGPT_GEMM_TILE must be 256x256, 128x384, 128x256, 128x128, 64x128x64, 64x128x64s4, 64x128, "
+         "64x64 or 64x64x64s6");
 }
 
 template <int EPI, int PREC>
@@ -714,7 +715,16 @@ void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
     // for 64 x 128 tiles)
     if (EPI == GEMM_SWIGLU && p.M <= kSmallM && p.K % 64 == 0) shape = 8;
     else
-    if (huge >= 192 && 4 * huge >= 3 * 256 * rounds) shape = 7;
+    if (huge >= 192 && 4 * huge >= 3 * 256 * rounds) {
+      shape = 7;
+      // 128 x 384 tiles where their last round of blocks is at least a
+      // tenth fuller (bf16x2): the Mistral-Small-24B QKV projection at
+      // M = 2048 (N = 6144) is 256 of them against 192 of 256 x 256, 240
+      // against 264 us stand-alone with the weights from HBM
+      const long t384 = (long)((p.N + 3 * cols - 1) / (3 * cols)) * ((p.M + 127) / 128) * splits;
+      const long r384 = (t384 + 255) / 256;
+      if (PREC == GEMM_SPLIT2 && 10 * t384 * rounds >= 11 * huge * r384) shape = 9;
+    }
     else if (EPI == GEMM_SWIGLU && huge >= 128 && huge <= 256) shape = 7;
     else if (wide >= 1024) shape = 4;
     else if (p.K % 64 == 0 && small > 256) shape = 5;
@@ -723,6 +733,11 @@ void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
   }
   switch (shape) {
     case 7: launch3<256, 256, 3, EPI, PREC, 8, 32, 2>(p, splits, s); break;
+    case 9:  // 128 x 384, eight wavefronts of 32 x 192 (bf16x2: with single
+      // bf16 operands a sub-step has more fragment reads than MFMAs)
+      if constexpr (PREC == GEMM_SPLIT2) launch3<128, 384, 3, EPI, PREC, 8, 32, 1>(p, splits, s);
+      else launch3<256, 256, 3, EPI, PREC, 8, 32, 2>(p, splits, s);
+      break;
     case 4: launch<128, 256, 2, EPI, PREC, 2>(p, splits, s); break;
     case 5: launch<64, 128, 2, EPI, PREC, 2, 64, 1>(p, splits, s); break;
     case 6: launch<64, 128, 4, EPI, PREC, 1, 64>(p, splits, s); break;

@@ -59,8 +59,8 @@ def test_tiny_golden(name, model_dir):
         assert tokens == [int(v) for v in g["generated"]]
 
 
-@pytest.mark.parametrize("tile", ["256x256", "128x256", "128x128", "64x128x64", "64x128x64s4", "64x128", "64x64",
-                                  "64x64x64s6"])
+@pytest.mark.parametrize("tile", ["256x256", "128x384", "128x256", "128x128", "64x128x64", "64x128x64s4", "64x128",
+                                  "64x64", "64x64x64s6"])
 @pytest.mark.parametrize("name", ["tiny-qwen", "tiny-chunk"])
 def test_gemm_tile_shapes(name, tile, model_dir, monkeypatch):
     """Every prefill GEMM tile shape (forced with STRASGPT_GEMM_TILE; by
