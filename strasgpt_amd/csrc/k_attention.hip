@@ -28,7 +28,6 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // Decode: threads per block, query heads per kv head and blocks (partial
 // results) per kv head, at most.
-constexpr int kDecThreads = 256;
 constexpr int kDecMaxG = 8;
 constexpr int kDecMaxChunks = 64;
 
@@ -668,14 +667,18 @@ __device__ __forceinline__ void split8v(const float (&x)[8], bf16x8& hi, bf16x8&
   lo = __builtin_bit_cast(bf16x8, (uint4){l[0], l[1], l[2], l[3]});
 }
 
-template <int HD, int GW, bool B16>
-__global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParams p) {
-  constexpr int NW = kDecThreads / WAVE;
+// NW wavefronts per block: 4 (one per SIMD, kD2Tpw tiles each in flight)
+// or 8 (two per SIMD, half as many tiles each: the same tiles in flight per
+// block, and each SIMD interleaves two waves' chains of score MFMAs,
+// softmax and value MFMAs).
+template <int HD, int GW, bool B16, int NW>
+__global__ __launch_bounds__(NW * WAVE) void attn_decode_mfma_kernel(AttnParams p) {
+  constexpr int NT = NW * WAVE;
   constexpr int NKK = (HD + 31) / 32;  // 32-dim k-steps of S
   constexpr int DJ = HD / 16;          // 16-dim row blocks of O^T
   constexpr int PER = (HD + WAVE - 1) / WAVE;
   constexpr int MAXV = (kDecMaxG + 1 + NW - 1) / NW;  // head vectors per wave in the prologue
-  static_assert(NW == 4 && kD2Tile == 32, "four waves, 32-key tiles");
+  static_assert((NW == 4 || NW == 8) && kD2Tile == 32, "four or eight waves, 32-key tiles");
   __shared__ __attribute__((aligned(16))) float qs[kDecMaxG * HD];  // normalised, rotated queries
   __shared__ __attribute__((aligned(16))) float kn[HD];             // this step's key
   __shared__ float vn[HD];                                          // this step's value
@@ -764,7 +767,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParam
       if (!B16) r.vl[dj] = ld(rvl, off);
     }
   };
-  constexpr int TPW = kD2Tpw<B16>;
+  constexpr int TPW = NW == 4 ? kD2Tpw<B16> : kD2Tpw<B16> / 2;
   const int first = t0 + wave;                                 // tiles first, first + 4, ...
   const int cnt = first < t1 ? (t1 - first + NW - 1) / NW : 0;  // of this wave
   Regs r[TPW];
@@ -934,7 +937,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParam
     }
   }
   __syncthreads();
-  for (int i = tid; i < G * HD; i += kDecThreads) {
+  for (int i = tid; i < G * HD; i += NT) {
     const int h = i / HD, d = i % HD;
     float M = -INFINITY;
 #pragma unroll
@@ -1070,6 +1073,21 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(AttnParam
 
 }  // namespace
 
+// Wavefronts per decode attention block: 8 by default, 4 with
+// STRASGPT_DECODE_ATTN_WAVES=4. Eight (two per SIMD, one fp32 tile each)
+// against four (one per SIMD, two tiles each), stand-alone at the
+// Mistral-Small-24B / Llama-3.1-8B head shape (32 query heads, 8 kv heads,
+// head_dim 128): 9.04 -> 8.78 us at 600 positions, 11.50 -> 11.28 at 2112,
+// 19.87 -> 18.77 at 8300 (24-32 blocks per kv head within 0.2 us).
+int attention_decode_waves() {
+  if (const char* v = getenv("STRASGPT_DECODE_ATTN_WAVES")) {
+    const int n = atoi(v);
+    if (n != 4 && n != 8) ST_DIE("STRASGPT_DECODE_ATTN_WAVES must be 4 or 8");
+    return n;
+  }
+  return 8;
+}
+
 // Blocks per kv head, at most: up to 256 blocks, one per CU (a block holds
 // each SIMD's register file), and at most one combine lane each.
 int attention_decode_chunks(int kv_heads) {
@@ -1195,20 +1213,23 @@ void attention_decode(const AttnParams& p, hipStream_t s) {
       p.pair_bound - p.pair_stride + p.pair_offset >= p.hd)
     ST_DIE("decode attention: RoPE pairs must fit one per lane within the head");
   const dim3 grid(p.splits, p.kv_heads);
-  const bool two = G > kDecThreads / WAVE;  // the combine: two query heads per wave
+  const int nw = attention_decode_waves();
+  const bool two = nw == 4 && G > 4;  // the combine: two query heads per wave
   switch (p.hd) {
-#define DECODE2_LAUNCH(HD, GW)                                                                     \
-  if (p.kv_bf16)                                                                                   \
-    hipLaunchKernelGGL((attn_decode_mfma_kernel<HD, GW, true>), grid, dim3(kDecThreads), 0, s, p); \
-  else                                                                                             \
-    hipLaunchKernelGGL((attn_decode_mfma_kernel<HD, GW, false>), grid, dim3(kDecThreads), 0, s, p);
-#define DECODE2_CASE(HD)     \
-  case HD:                   \
-    if (two) {               \
-      DECODE2_LAUNCH(HD, 2)  \
-    } else {                 \
-      DECODE2_LAUNCH(HD, 1)  \
-    }                        \
+#define DECODE2_LAUNCH(HD, GW, NW)                                                                        \
+  if (p.kv_bf16)                                                                                          \
+    hipLaunchKernelGGL((attn_decode_mfma_kernel<HD, GW, true, NW>), grid, dim3(NW * WAVE), 0, s, p);     \
+  else                                                                                                    \
+    hipLaunchKernelGGL((attn_decode_mfma_kernel<HD, GW, false, NW>), grid, dim3(NW * WAVE), 0, s, p);
+#define DECODE2_CASE(HD)        \
+  case HD:                      \
+    if (nw == 8) {              \
+      DECODE2_LAUNCH(HD, 1, 8)  \
+    } else if (two) {           \
+      DECODE2_LAUNCH(HD, 2, 4)  \
+    } else {                    \
+      DECODE2_LAUNCH(HD, 1, 4)  \
+    }                           \
     break;
     DECODE2_CASE(16)
     DECODE2_CASE(32)
