@@ -43,6 +43,12 @@ int strasgpt_kbench_copy(size_t bytes, int iters, double* avg_us);
 int strasgpt_kbench_mfma(int random_operands, int waves_per_simd, int iters, int launches,
                          double* tflops);
 
+/* The device sampler's sort on n host pairs (key, index): a stable
+ * descending sort by key (equal keys in index order), the order the top-k
+ * and top-p cuts walk. keys_out[r] = the r-th key, index_out[r] its index.
+ * 1 <= n <= 1 << 26. */
+int strasgpt_kbench_sort_desc(const uint32_t* keys, int n, uint32_t* keys_out, int32_t* index_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,27 @@ __global__ __launch_bounds__(256) void copy_probe_kernel(const float4* __restric
 
 }  // namespace
 
+extern "C" int strasgpt_kbench_sort_desc(const uint32_t* keys, int n, uint32_t* keys_out, int32_t* index_out) {
+  if (!keys || !keys_out || !index_out || n < 1 || n > sg::kSortMax) return -1;
+  unsigned *k, *ko;
+  int* vo;
+  void* tmp;
+  const size_t tb = sg::sample_sort_temp_bytes(n);
+  HIP_CHECK(hipMalloc(&k, (size_t)n * 4));
+  HIP_CHECK(hipMalloc(&ko, (size_t)n * 4));
+  HIP_CHECK(hipMalloc(&vo, (size_t)n * 4));
+  HIP_CHECK(hipMalloc(&tmp, tb));
+  HIP_CHECK(hipMemcpy(k, keys, (size_t)n * 4, hipMemcpyHostToDevice));
+  sg::sort_pairs_desc(k, nullptr, n, ko, vo, tmp, nullptr);
+  HIP_CHECK(hipMemcpy(keys_out, ko, (size_t)n * 4, hipMemcpyDeviceToHost));
+  HIP_CHECK(hipMemcpy(index_out, vo, (size_t)n * 4, hipMemcpyDeviceToHost));
+  HIP_CHECK(hipFree(k));
+  HIP_CHECK(hipFree(ko));
+  HIP_CHECK(hipFree(vo));
+  HIP_CHECK(hipFree(tmp));
+  return 0;
+}
+
 extern "C" int strasgpt_kbench_copy(size_t bytes, int iters, double* avg_us) {
   if (bytes < 16 || bytes % 16 || iters <= 0 || !avg_us) return -1;
   hipStream_t s;

@@ -15,14 +15,12 @@
 // are formed from fixed-order partial sums (deterministic, but rounded
 // differently), so a draw can differ from the reference's only when the
 // coin or top_p lies within that rounding of a boundary. Equal
-// probabilities rank by index (the radix sort is stable), as a stable sort
-// of the reference's index-ordered array ranks them. The coin stream, the
+// probabilities rank by index (the radix sort below is stable), as a
+// stable sort of the reference's index-ordered array ranks them. The coin stream, the
 // penalty and every per-element operation (division by the temperature,
 // expf, division by the sum, multiplication by the float inverse of the
 // double sum) are the reference's.
 #include <limits.h>
-
-#include <rocprim/device/device_radix_sort.hpp>
 
 #include "device_common.h"
 #include "hip_check.h"
@@ -219,14 +217,149 @@ __global__ __launch_bounds__(kPick) void sample_pick_kernel(SampleParams p) {
   }
 }
 
+// ------------------------------------------------------------ radix sort --
+// Stable descending sort of (key, value) pairs: a least-significant-digit
+// radix sort of the inverted keys (ascending on ~key is descending on key),
+// four passes of 8-bit digits. A pass is three launches over kRsBlocks
+// contiguous chunks of the input:
+// * histogram: the digit counts of each chunk, stored bin-major
+//   (hist[digit][chunk]);
+// * scan: one block turns them into exclusive offsets in that order, so a
+//   digit's elements of chunk c land after those of chunks < c;
+// * scatter: each chunk, in tiles of kRsThreads elements in input order,
+//   ranks every element among the equal digits of its tile (within a
+//   wavefront by ballots over the digit's bits, across wavefronts by
+//   per-wavefront counts) and writes it at its digit's running offset.
+// Every step keeps input order among equal digits, hence the stability.
+constexpr int kRsThreads = 256;
+constexpr int kRsWaves = kRsThreads / WAVE;
+constexpr int kRsBlocks = 64;
+constexpr int kRsBins = 256;
+constexpr int kRsScan = 1024;  // threads of the scan: kRsBins * kRsBlocks / kRsScan entries each
+static_assert(kRsBins * kRsBlocks % kRsScan == 0, "scan partition");
+
+__device__ __forceinline__ int rs_chunk(int n) { return (n + kRsBlocks - 1) / kRsBlocks; }
+__device__ __forceinline__ unsigned rs_digit(unsigned key, int shift) { return (~key >> shift) & (kRsBins - 1); }
+
+__global__ __launch_bounds__(kRsThreads) void rs_hist_kernel(const unsigned* keys, int n, int shift,
+                                                           unsigned* hist) {
+  __shared__ unsigned h[kRsBins];
+  for (int i = threadIdx.x; i < kRsBins; i += kRsThreads) h[i] = 0u;
+  __syncthreads();
+  const int ch = rs_chunk(n), lo = min(n, (int)blockIdx.x * ch), hi = min(n, lo + ch);
+  for (int i = lo + threadIdx.x; i < hi; i += kRsThreads) atomicAdd(&h[rs_digit(keys[i], shift)], 1u);
+  __syncthreads();
+  for (int d = threadIdx.x; d < kRsBins; d += kRsThreads) hist[d * kRsBlocks + blockIdx.x] = h[d];
+}
+
+// Exclusive scan of the kRsBins * kRsBlocks counts in place: each thread a
+// run of consecutive entries, then a scan of the runs' sums in thread order.
+__global__ __launch_bounds__(kRsScan) void rs_scan_kernel(unsigned* hist) {
+  constexpr int PER = kRsBins * kRsBlocks / kRsScan;
+  __shared__ unsigned run[2][kRsScan];
+  const int t = threadIdx.x;
+  unsigned v[PER], sum = 0u;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    v[i] = hist[t * PER + i];
+    sum += v[i];
+  }
+  int cur = 0;
+  run[0][t] = sum;
+  __syncthreads();
+  for (int off = 1; off < kRsScan; off <<= 1) {  // inclusive scan of the run sums
+    const unsigned add = t >= off ? run[cur][t - off] : 0u;
+    run[cur ^ 1][t] = run[cur][t] + add;
+    cur ^= 1;
+    __syncthreads();
+  }
+  unsigned base = run[cur][t] - sum;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    hist[t * PER + i] = base;
+    base += v[i];
+  }
+}
+
+__global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(const unsigned* kin, const int* vin, int n,
+                                                              int shift, const unsigned* offs, unsigned* kout,
+                                                              int* vout) {
+  __shared__ unsigned base[kRsBins];           // the digits' running output offsets
+  __shared__ unsigned cnt[kRsWaves][kRsBins];  // a tile's digit counts per wavefront, then their prefixes
+  __shared__ unsigned tot[kRsBins];            // a tile's digit counts
+  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+  for (int e = tid; e < kRsBins; e += kRsThreads) base[e] = offs[e * kRsBlocks + blockIdx.x];
+  const int ch = rs_chunk(n), lo = min(n, (int)blockIdx.x * ch), hi = min(n, lo + ch);
+  const unsigned long long below = (1ull << lane) - 1ull;  // the lanes before this one
+  for (int t0 = lo; t0 < hi; t0 += kRsThreads) {
+    for (int e = tid; e < kRsWaves * kRsBins; e += kRsThreads) cnt[e / kRsBins][e % kRsBins] = 0u;
+    __syncthreads();
+    const int i = t0 + tid;
+    const bool valid = i < hi;  // the invalid lanes are the tile's last ones
+    const unsigned key = valid ? kin[i] : 0u;
+    const int val = valid ? (vin ? vin[i] : i) : 0;
+    const unsigned d = rs_digit(key, shift);
+    // the lanes of this wavefront holding the same digit
+    unsigned long long same = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const unsigned long long ones = __ballot((d >> b) & 1u);
+      same &= ((d >> b) & 1u) ? ones : ~ones;
+    }
+    const unsigned rank = (unsigned)__popcll(same & below), group = (unsigned)__popcll(same);
+    if (valid && rank == group - 1u) cnt[wave][d] = group;  // the group's last lane
+    __syncthreads();
+    for (int e = tid; e < kRsBins; e += kRsThreads) {  // prefixes over the wavefronts in order
+      unsigned r = 0u;
+#pragma unroll
+      for (int w = 0; w < kRsWaves; w++) {
+        const unsigned c = cnt[w][e];
+        cnt[w][e] = r;
+        r += c;
+      }
+      tot[e] = r;
+    }
+    __syncthreads();
+    if (valid) {
+      const unsigned pos = base[d] + cnt[wave][d] + rank;
+      kout[pos] = key;
+      vout[pos] = val;
+    }
+    __syncthreads();  // every read of base and cnt for this tile is done
+    for (int e = tid; e < kRsBins; e += kRsThreads) base[e] += tot[e];
+  }
+}
+
 }  // namespace
 
 size_t sample_sort_temp_bytes(int V) {
-  size_t bytes = 0;
-  HIP_CHECK(rocprim::radix_sort_pairs_desc((void*)nullptr, bytes, (unsigned*)nullptr, (unsigned*)nullptr,
-                                           (int*)nullptr, (int*)nullptr, (unsigned)V, 0, 32,
-                                           (hipStream_t)0));
-  return bytes;
+  // a key and a value buffer for the passes between the input and the
+  // output, and the digit counts
+  return (size_t)V * (sizeof(unsigned) + sizeof(int)) + (size_t)kRsBins * kRsBlocks * sizeof(unsigned) + 256;
+}
+
+void sort_pairs_desc(const unsigned* keys, const int* vals, int n, unsigned* keys_out, int* vals_out, void* temp,
+                     hipStream_t s) {
+  if (n < 0 || n > kSortMax) ST_DIE("sort_pairs_desc: n out of range");
+  if (n == 0) return;
+  unsigned* tk = (unsigned*)temp;
+  int* tv = (int*)(tk + n);
+  unsigned* hist = (unsigned*)(((uintptr_t)(tv + n) + 255) & ~(uintptr_t)255);
+  // passes 0..3: input -> temp -> output -> temp -> output
+  const unsigned* kin = keys;
+  const int* vin = vals;
+  for (int pass = 0; pass < 4; pass++) {
+    unsigned* ko = pass % 2 ? keys_out : tk;
+    int* vo = pass % 2 ? vals_out : tv;
+    const int shift = 8 * pass;
+    hipLaunchKernelGGL(rs_hist_kernel, dim3(kRsBlocks), dim3(kRsThreads), 0, s, kin, n, shift, hist);
+    hipLaunchKernelGGL(rs_scan_kernel, dim3(1), dim3(kRsScan), 0, s, hist);
+    hipLaunchKernelGGL(rs_scatter_kernel, dim3(kRsBlocks), dim3(kRsThreads), 0, s, kin, vin, n, shift, hist, ko,
+                       vo);
+    kin = ko;
+    vin = vo;
+  }
+  HIP_CHECK(hipGetLastError());
 }
 
 void sample(const SampleParams& p, hipStream_t s) {
@@ -254,9 +387,8 @@ void sample(const SampleParams& p, hipStream_t s) {
   hipLaunchKernelGGL(sample_exp_kernel, dim3(kSB), dim3(kST), 0, s, q);
   hipLaunchKernelGGL(sample_norm_kernel, dim3(kSB), dim3(kST), 0, s, q);
   if (filter) {
-    size_t bytes = p.sort_temp_bytes;
-    HIP_CHECK(rocprim::radix_sort_pairs_desc(p.sort_temp, bytes, p.keys, p.keys_sorted, p.vals, p.vals_sorted,
-                                             (unsigned)p.V, 0, 32, s));
+    if (p.sort_temp_bytes < sample_sort_temp_bytes(p.V)) ST_DIE("sample: sort scratch too small");
+    sort_pairs_desc(p.keys, p.vals, p.V, p.keys_sorted, p.vals_sorted, p.sort_temp, s);
   }
   hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(kPick), 0, s, q);
   hipLaunchKernelGGL(sample_pick_kernel, dim3(1), dim3(kPick), 0, s, q);

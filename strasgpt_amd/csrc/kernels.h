@@ -300,6 +300,13 @@ struct SampleParams {
 };
 void sample(const SampleParams& p, hipStream_t s);
 size_t sample_sort_temp_bytes(int V);
+// Stable descending sort of n (key, value) pairs by key (equal keys keep
+// their input order): keys_out / vals_out; vals null means the values are
+// the indices 0..n-1. temp holds sample_sort_temp_bytes(n) bytes. Keys and
+// the input are untouched; n <= kSortMax.
+constexpr int kSortMax = 1 << 26;
+void sort_pairs_desc(const unsigned* keys, const int* vals, int n, unsigned* keys_out, int* vals_out, void* temp,
+                     hipStream_t s);
 
 // ---------------------------------------------------------------- MoE --
 // Router logits (bf16 GEMV), top-k with lowest-index ties, softmax over

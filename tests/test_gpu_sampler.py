@@ -133,3 +133,39 @@ def test_generate_sampled_against_oracle(name, model_dir):
     log(f"{name}: {steps} sampled tokens {gtok}; {near} near-boundary draws")
     assert ref.rng_state == state
     assert near <= 1
+
+
+@pytest.mark.parametrize("n", [1, 63, 256, 1000, 151936, 262145])
+@pytest.mark.parametrize("kind", ["probabilities", "full-range"])
+def test_sort_desc_stable(n, kind):
+    """The sampler's radix sort (hand-written, four 8-bit passes) through
+    strasgpt_kbench_sort_desc: keys in descending order, equal keys in index
+    order, bit for bit against numpy's stable argsort. Probability-like keys
+    (fp32 bit patterns of values in [0, 1]: most of the high digits equal,
+    many zeros and planted ties) and full-range 32-bit keys (every digit
+    varies); sizes with ragged last tiles and chunks."""
+    import ctypes
+    rt = runtime()
+    L = rt.lib()
+    rng = np.random.default_rng(n + (7 if kind == "full-range" else 0))
+    if kind == "probabilities":
+        p = rng.exponential(1.0, n).astype(np.float32) ** 4
+        p[rng.random(n) < 0.3] = 0.0  # many exact zeros
+        p /= max(float(p.sum()), 1e-30)
+        if n > 8:
+            p[rng.integers(0, n, n // 8)] = p[rng.integers(0, n)]  # ties with one value
+        keys = p.astype(np.float32).view(np.uint32)
+    else:
+        keys = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+        if n > 8:
+            keys[rng.integers(0, n, n // 8)] = keys[rng.integers(0, n)]
+    keys = np.ascontiguousarray(keys)
+    got_k = np.zeros(n, np.uint32)
+    got_i = np.zeros(n, np.int32)
+    fn = L.strasgpt_kbench_sort_desc
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    assert fn(keys.ctypes.data, n, got_k.ctypes.data, got_i.ctypes.data) == 0
+    order = np.argsort(-keys.astype(np.int64), kind="stable")
+    np.testing.assert_array_equal(got_i, order.astype(np.int32))
+    np.testing.assert_array_equal(got_k, keys[order])
+    log(f"sort n={n} {kind}: order identical")
