@@ -231,6 +231,60 @@ def test_decode_attention_chunk_counts(chunks, model_dir, monkeypatch):
     assert tokens == [int(v) for v in g["generated"]]
 
 
+@pytest.mark.parametrize("kv", ["fp32", "bf16"])
+@pytest.mark.parametrize("name", ["tiny-chunk", "tiny-long"])
+def test_decode_attention_four_waves(name, kv, model_dir, monkeypatch):
+    """Decode attention with four wavefronts per block
+    (STRASGPT_DECODE_ATTN_WAVES=4: one per SIMD, two fp32 key tiles each;
+    the default is eight): tiny-chunk (4 query heads per kv head, one per
+    wave in the combine) and tiny-long (8 on one kv head, two per wave),
+    with an fp32 and a bf16 cache. Greedy tokens (graph and eager decode)
+    equal the oracle's run with the same cache format. The logits of
+    single-token steps after the prompt meet the 2e-2 / 1e-3 bar against
+    it with an fp32 cache; with a bf16 cache they stay within a quarter of
+    the format's own effect (the bf16-cache oracle against the fp32-cache
+    one), the bar of the bf16-cache tests."""
+    from oracle import oracle as orc
+    rt = runtime()
+    d = model_dir(name)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(shp.vocab, shp.prompt_len, 31)
+    steps = shp.decode_len + 1
+    om = orc.OracleModel(d, threads=16, kv_format=orc.KV_BF16 if kv == "bf16" else orc.KV_F32)
+    of = orc.OracleModel(d, threads=16) if kv == "bf16" else None
+    otok = om.generate(prompt, steps)
+    monkeypatch.setenv("STRASGPT_DECODE_ATTN_WAVES", "4")
+    with rt.Transformer(d) as t:
+        if kv == "bf16":
+            t.set_kv_cache_format(rt.KV_BF16)
+        got = {}
+        for mode in (rt.DECODE_GRAPH, rt.DECODE_EAGER):
+            t.set_decode_mode(mode)
+            t.reset()
+            got[mode], _ = t.generate(prompt, steps)
+        t.reset()
+        om.reset()
+        t.predict(prompt)
+        om.predict(prompt)
+        if of is not None:
+            of.predict(prompt)
+        worst, fmt = 0.0, 0.0
+        for tok in otok[:3]:
+            g, o = t.predict([tok])[0], om.predict([tok])[0]
+            if of is None:
+                np.testing.assert_allclose(g, o, rtol=RTOL, atol=ATOL)
+            else:
+                fmt = max(fmt, float(np.abs(o - of.predict([tok])[0]).max()))
+            worst = max(worst, float(np.abs(g - o).max()))
+    log(f"{name} {kv} cache, four waves: oracle {otok}, graph {got[rt.DECODE_GRAPH]}, "
+        f"eager {got[rt.DECODE_EAGER]}; decode steps max |logit difference| {worst:.3g}"
+        + (f" (format effect {fmt:.3g})" if of is not None else ""))
+    if of is not None:
+        assert fmt > 0 and worst <= 0.25 * fmt
+    assert got[rt.DECODE_GRAPH] == otok
+    assert got[rt.DECODE_EAGER] == otok
+
+
 @pytest.mark.parametrize("chunk", ["512", "600"])
 def test_prefill_chunk_lengths(chunk, model_dir, monkeypatch):
     """The 520-token prompt of tiny-chunk in device chunks of 512 (two
