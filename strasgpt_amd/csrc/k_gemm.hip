@@ -773,6 +773,26 @@ void check(const GemmParams& p, int epi, int prec, int splits) {
     ST_DIE("GEMM split-K is only available with the partial-sum epilogue");
 }
 
+// Split count that puts the 64 x 128 tiles with 64-deep stages (two blocks
+// per CU) in one round of at least 3/4 of the 512 block slots; 0 if none
+// does. Each split adds a set of M x N partial sums to write and read back,
+// and a second, partial round of blocks costs a whole K range more, so the
+// largest count that still fits one round wins. Measured stand-alone with
+// the weights from HBM, partial sums added by the next kernel: Qwen3-4B O
+// and down projections at M = 512 (160 tiles), 3 splits 35.5 and 66.3 us
+// against 42.2 and 74.8 with 4 (1.25 rounds); the MXFP4 MoE O projection at
+// M = 256 (92 tiles), 5 splits 30.8 us against 36.7 with 6; its QKV
+// projection (160 tiles), 3 splits and the split epilogue 29.2 us against
+// 35.2 unsplit.
+int round_splits(int M, int N, int K) {
+  if (K % 64) return 0;
+  const long t64 = (long)((N + 127) / 128) * ((M + 63) / 64);
+  if (t64 >= 512) return 0;
+  int s = (int)std::min<long>(8, 512 / t64);
+  while (s > 1 && K / 64 < 4 * s) s--;  // at least 4 K steps per split
+  return 4 * t64 * s >= 3 * 512 ? s : 0;
+}
+
 }  // namespace
 
 int gemm_splits(int M, int N, int K) {
@@ -790,6 +810,7 @@ int gemm_splits(int M, int N, int K) {
       if (blocks >= 192 && 4 * blocks >= 3 * 256 * rounds) return s;
     }
   }
+  if (const int s = round_splits(M, N, K)) return s;
   // Enough blocks for the 256 CUs on the N = embedding_dim projections;
   // long reductions (K >= 16384: a 1024-step K loop and more) split until
   // there are about four 128 x 128 tiles per CU.
@@ -839,6 +860,11 @@ __global__ __launch_bounds__(256) void split_epilogue_kernel(GemmParams p, const
 }  // namespace
 
 int gemm_small_splits(int M, int N, int K, int epi, size_t ws_floats) {
+  if (M > kSmallM && epi == GEMM_QKV) {  // mid-size prompts: one full round of split tiles
+    int sp = std::max(1, round_splits(M, N, K));
+    while (sp > 1 && (size_t)sp * M * N > ws_floats) sp--;
+    return sp;
+  }
   if (M > kSmallM || (epi != GEMM_QKV && epi != GEMM_SWIGLU) || K % 64) return 1;
   const int tiles = (N + 127) / 128 * (epi == GEMM_SWIGLU ? 2 : 1);  // 64 x 128 tiles of the partial GEMMs
   int sp = std::min(8, std::max(1, (256 + tiles - 1) / tiles));
