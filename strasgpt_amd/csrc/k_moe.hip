@@ -181,17 +181,58 @@ __device__ __forceinline__ void wait_dma_behind() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Top-k of one token's router logits (E <= 64, one per lane) with the
+// semantics of route_kernel's selection: each round takes the largest
+// untaken logit, ties to the lowest expert id, NaN never selected unless it
+// is the first untaken expert (a sequential scan starting from it would
+// keep it); -inf only when nothing larger is left (the first untaken).
+// Lane j < k ends with the j-th pick and its weight e^(l_j - l_0) / sum,
+// the sum over the picks in pick order. Whole wave, uniform control flow.
+__device__ __forceinline__ void topk_lanes(const float* lg, int E, int k, int& mine, float& wmine) {
+  const int lane = threadIdx.x % WAVE;
+  const float v = lane < E ? lg[lane] : -INFINITY;
+  bool taken = false;
+  int top = 0;
+  mine = 0;
+  for (int j = 0; j < k; j++) {
+    const int first = __ffsll((unsigned long long)__ballot(lane < E && !taken)) - 1;  // k <= E: one is left
+    const bool cand = lane < E && !taken && v > -INFINITY;
+    int pick = first;
+    if (__ballot(cand)) {
+      const float M = wave_peak(cand ? v : -INFINITY);
+      pick = __ffsll((unsigned long long)__ballot(cand && v == M)) - 1;
+    }
+    const float fv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), first));
+    if (fv != fv) pick = first;
+    if (j == 0) top = pick;
+    if (lane == j) mine = pick;
+    if (lane == pick) taken = true;
+  }
+  const float lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
+  const float lm = __shfl(v, mine, WAVE);
+  const float ev = lane < k ? expf(lm - lt) : 0.0f;
+  float sum = 0.0f;
+  for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
+  wmine = ev / sum;
+}
+
 // Router + top-k + softmax, one block of kRouteThreads per token: the
 // activation row goes to LDS by DMA, then each wave issues every 128-bit
 // weight load of its first kRouteE experts before any is used (further
 // experts, for E > kRouteWaves * kRouteE, follow in a loop); wave 0 then
-// selects.
+// selects. Measured at the MXFP4 MoE shape (256 tokens, 32 experts,
+// d = 2880): 14.4 us with non-temporal weight loads, each row chunk read
+// from LDS once per expert and every block starting at expert 0; 8.4 us
+// with cached loads, one LDS read per chunk and the expert groups rotated
+// by block. Two or more tokens per block (the weights applied to each row)
+// spill registers and took 18-24 us.
 constexpr int kRouteThreads = 512;
 constexpr int kRouteWaves = kRouteThreads / WAVE;
 constexpr int kRouteE = 4;     // experts per wave per pass
 constexpr int kRouteLd = 6;    // 8-value chunks per lane per expert per pass
 constexpr int kRouteDma = 4;   // unrolled DMA instructions per wave: d <= 8192
 
+// Plain (cached) loads: every block reads the same router rows.
 __device__ __forceinline__ void route_load(const uint16_t* router, int E, int d, int e0, int c0, int lane,
                                            uint4 (&w)[kRouteE][kRouteLd]) {
   const int chunks = d / 8;
@@ -199,28 +240,31 @@ __device__ __forceinline__ void route_load(const uint16_t* router, int E, int d,
   for (int i = 0; i < kRouteE; i++) {
     const uint16_t* wr = router + (size_t)min(e0 + i, E - 1) * d;
 #pragma unroll
-    for (int u = 0; u < kRouteLd; u++) w[i][u] = load_nt_u4(wr + min(c0 + u * WAVE + lane, chunks - 1) * 8);
+    for (int u = 0; u < kRouteLd; u++) w[i][u] = *(const uint4*)(wr + min(c0 + u * WAVE + lane, chunks - 1) * 8);
   }
 }
 
+// Each 8-value chunk of the row is read from LDS once for the wave's
+// kRouteE experts; logit i still sums its chunks in order u = 0, 1, ...
 __device__ __forceinline__ void route_dot(const uint4 (&w)[kRouteE][kRouteLd], const float* xs, int chunks,
                                           int c0, int lane, float (&acc)[kRouteE]) {
 #pragma unroll
-  for (int i = 0; i < kRouteE; i++)
+  for (int u = 0; u < kRouteLd; u++) {
+    const int c = c0 + u * WAVE + lane;
+    if (c < chunks) {
+      const float4 xa = *(const float4*)(xs + c * 8), xb = *(const float4*)(xs + c * 8 + 4);
 #pragma unroll
-    for (int u = 0; u < kRouteLd; u++) {
-      const int c = c0 + u * WAVE + lane;
-      if (c < chunks)
-        acc[i] = dot8(w[i][u], *(const float4*)(xs + c * 8), *(const float4*)(xs + c * 8 + 4), acc[i]);
+      for (int i = 0; i < kRouteE; i++) acc[i] = dot8(w[i][u], xa, xb, acc[i]);
     }
+  }
 }
 
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, const uint16_t* router,
-                                                              int E, int d, int k, int* sel,
-                                                              float* sel_w) {
+template <bool LANE_E>
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, const uint16_t* router, int E,
+                                                              int d, int k, int* sel, float* sel_w) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
-  float* xs = sm;        // [d]
-  float* lg = sm + d;    // [E]
+  float* xs = sm;      // [d]
+  float* lg = sm + d;  // [E]
   const int t = blockIdx.x, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   {
     const float* xrow = xn + (size_t)t * d;
@@ -233,15 +277,18 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, c
   }
   const int chunks = d / 8;
   uint4 w[kRouteE][kRouteLd];
-  route_load(router, E, d, wave * kRouteE, 0, lane, w);  // (clamped rows for a wave without experts)
+  // expert groups rotated by block, so that the blocks of an XCD do not all
+  // request the same router rows at once
+  const int g0 = (wave + (int)blockIdx.x) % kRouteWaves * kRouteE;
+  route_load(router, E, d, g0, 0, lane, w);  // (clamped rows for a wave without experts)
   wait_dma_behind<kRouteE * kRouteLd>();
   __syncthreads();
-  for (int e0 = wave * kRouteE; e0 < E; e0 += kRouteWaves * kRouteE) {
+  for (int e0 = g0; e0 < E; e0 += kRouteWaves * kRouteE) {
     float acc[kRouteE];
 #pragma unroll
     for (int i = 0; i < kRouteE; i++) acc[i] = 0.0f;
     for (int c0 = 0; c0 < chunks; c0 += kRouteLd * WAVE) {
-      if (e0 != wave * kRouteE || c0 != 0) route_load(router, E, d, e0, c0, lane, w);
+      if (e0 != g0 || c0 != 0) route_load(router, E, d, e0, c0, lane, w);
       route_dot(w, xs, chunks, c0, lane, acc);
     }
 #pragma unroll
@@ -251,7 +298,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* xn, c
     }
   }
   __syncthreads();
-  if (wave == 0) {
+  if (LANE_E) {  // E <= 64: one expert per lane
+    if (wave == 0) {
+      int mine;
+      float wm;
+      topk_lanes(lg, E, k, mine, wm);
+      if (lane < k) {
+        sel[t * k + lane] = mine;
+        sel_w[t * k + lane] = wm;
+      }
+    }
+  } else if (wave == 0) {
     // k rounds of a wave-wide selection with the semantics of a sequential
     // scan over the experts not yet taken: start from the first, replace
     // on strictly greater (ties keep the lower id; a NaN first candidate
@@ -366,41 +423,6 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const float* x, const
   }
   acc = wave_total(acc);
   if (lane == 0 && e < E) logits[e] = acc;
-}
-
-// Top-k of one token's router logits (E <= 64, one per lane) with the
-// semantics of route_kernel's selection: each round takes the largest
-// untaken logit, ties to the lowest expert id, NaN never selected unless it
-// is the first untaken expert (a sequential scan starting from it would
-// keep it); -inf only when nothing larger is left (the first untaken).
-// Lane j < k ends with the j-th pick and its weight e^(l_j - l_0) / sum,
-// the sum over the picks in pick order. Whole wave, uniform control flow.
-__device__ __forceinline__ void topk_lanes(const float* lg, int E, int k, int& mine, float& wmine) {
-  const int lane = threadIdx.x % WAVE;
-  const float v = lane < E ? lg[lane] : -INFINITY;
-  bool taken = false;
-  int top = 0;
-  mine = 0;
-  for (int j = 0; j < k; j++) {
-    const int first = __ffsll((unsigned long long)__ballot(lane < E && !taken)) - 1;  // k <= E: one is left
-    const bool cand = lane < E && !taken && v > -INFINITY;
-    int pick = first;
-    if (__ballot(cand)) {
-      const float M = wave_peak(cand ? v : -INFINITY);
-      pick = __ffsll((unsigned long long)__ballot(cand && v == M)) - 1;
-    }
-    const float fv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), first));
-    if (fv != fv) pick = first;
-    if (j == 0) top = pick;
-    if (lane == j) mine = pick;
-    if (lane == pick) taken = true;
-  }
-  const float lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
-  const float lm = __shfl(v, mine, WAVE);
-  const float ev = lane < k ? expf(lm - lt) : 0.0f;
-  float sum = 0.0f;
-  for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
-  wmine = ev / sum;
 }
 
 // act[s][h] = silu(gate_e[h] . x_s) * (up_e[h] . x_s), slot s = (token, j):
@@ -1222,8 +1244,17 @@ void moe_route(const float* xn, int T, const uint16_t* router, int E, int d, int
   if (d % 8 || (uintptr_t)router % 16 || (uintptr_t)xn % 16) ST_DIE("MoE router rows must be 16-byte aligned");
   if (d > kRouteDma * kRouteThreads * 4) ST_DIE("MoE router supports embedding_dim <= 8192");
   const size_t shm = (size_t)(d + E) * sizeof(float);
-  set_lds(route_kernel, shm);
-  hipLaunchKernelGGL(route_kernel, dim3(T), dim3(kRouteThreads), shm, s, xn, router, E, d, k, sel, sel_w);
+  // STRASGPT_MOE_ROUTE_SCAN=1: the selection for more than 64 experts at
+  // any E (for tests: both selections take the same experts)
+  const char* sv = getenv("STRASGPT_MOE_ROUTE_SCAN");
+  const bool scan = sv && atoi(sv);
+  if (E <= WAVE && !scan) {
+    set_lds(route_kernel<true>, shm);
+    hipLaunchKernelGGL(route_kernel<true>, dim3(T), dim3(kRouteThreads), shm, s, xn, router, E, d, k, sel, sel_w);
+  } else {
+    set_lds(route_kernel<false>, shm);
+    hipLaunchKernelGGL(route_kernel<false>, dim3(T), dim3(kRouteThreads), shm, s, xn, router, E, d, k, sel, sel_w);
+  }
   HIP_CHECK(hipGetLastError());
 }
 

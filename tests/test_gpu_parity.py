@@ -825,6 +825,32 @@ def test_moe_tiny_against_oracle(name, model_dir):
     assert gtok == otok
 
 
+@pytest.mark.parametrize("name", ["tiny-moe-long", "mid-moe"])
+def test_moe_prefill_router_selections_agree(name, model_dir, monkeypatch):
+    """The prefill router's two top-k selections (one expert per lane for at
+    most 64 experts, the default here; the scan over groups of 64 experts
+    that larger expert counts take, forced by STRASGPT_MOE_ROUTE_SCAN=1)
+    route every token alike: prefill logits bit-identical, greedy tokens
+    equal to the oracle's either way."""
+    rt = runtime()
+    d = model_dir(name)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(256, shp.prompt_len, PROMPT_SEED)
+    om = oracle_model(d, 4 if shp.dim < 1024 else 16)
+    otok = om.generate(prompt, 9)
+    got = {}
+    for scan in ("0", "1"):
+        monkeypatch.setenv("STRASGPT_MOE_ROUTE_SCAN", scan)
+        with rt.Transformer(d) as t:
+            logits = t.predict(prompt)
+            t.reset()
+            tokens, _ = t.generate(prompt, 9)
+        got[scan] = (logits, tokens)
+    log(f"{name}: oracle {otok}, lane selection {got['0'][1]}, scan {got['1'][1]}")
+    assert np.array_equal(got["0"][0], got["1"][0])
+    assert got["0"][1] == otok and got["1"][1] == otok
+
+
 def test_prefill_precision_modes(model_dir):
     """bf16x2 (default) agrees with the oracle to fp32 noise; the single
     bf16 mode (documented as lossy) stays within a few percent RMS and is
