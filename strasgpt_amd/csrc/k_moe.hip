@@ -1017,7 +1017,8 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
     const int c = (lane % 8) ^ q_swz(row);
     const int r = row % BM;
     const int grow = rbeg + min(m0 + r, cnt - 1);  // rows past the tile load its last row
-    asrc[i] = (row < BM ? p.a_hi : p.a_lo) + (size_t)grow * K + 8 * c;
+    const int srow = p.a_per_token ? p.order[grow] / p.topk : grow;
+    asrc[i] = (row < BM ? p.a_hi : p.a_lo) + (size_t)srow * K + 8 * c;
   }
   // codes: instruction i of wave w covers weight rows 32 (QBI w + i) ..
   // + 31, lane -> row + lane / 2, block lane % 2 of the step
@@ -1180,7 +1181,19 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
       const int r = 16 * mi + 4 * g + i;
       if (m0 + r >= cnt) continue;
       const int s2 = slot[mi][i];
-      if (DUAL) {
+      if (DUAL && p.y_hi) {  // the down GEMM's A planes, expert order
+        const size_t row = (size_t)(rbeg + m0 + r) * p.N;
+#pragma unroll
+        for (int j = 0; j < HF; j++) {
+          const int n = n0 + 16 * HF * wave + 16 * j + c;
+          if (n < p.N) {
+            const float v = silu_mul(acc[mi][j][i], acc[mi][HF + j][i]);
+            const uint16_t h = f32_to_bf16_rne(v);
+            p.y_hi[row + n] = h;
+            p.y_lo[row + n] = f32_to_bf16_rne(v - bf16_to_f32(h));
+          }
+        }
+      } else if (DUAL) {
 #pragma unroll
         for (int j = 0; j < HF; j++) {
           const int n = n0 + 16 * HF * wave + 16 * j + c;
@@ -1369,6 +1382,8 @@ int moe_slot_tile(int slots, int E) {
 
 void moe_group_gemm(const MoeGemmParams& p, hipStream_t s) {
   if (p.K % 32 || p.N <= 0 || p.slots <= 0) ST_DIE("MoE grouped GEMM shape");
+  if ((p.y_hi || p.y_lo) && (!p.y_hi || !p.y_lo || !p.blocks2 || !moe_group_gemm2_ok(p)))
+    ST_DIE("MoE grouped GEMM output planes need the pipelined SwiGLU pair");
   if (moe_group_gemm2_ok(p)) {
     const bool dual = p.blocks2 != nullptr;
     const int nb = p.K / 32, runs = dual ? 2 : 1;

@@ -100,14 +100,21 @@ struct MoeGemmParams {
   const int *offs, *order;           // moe_group output
   int slots, topk, E, N, K;
   float* y;                          // [slot][N]: silu(g) * u, or the product
-  // optional: the A rows gathered in expert order (row i = the row of slot
-  // order[i]) as bf16 hi/lo planes [slots][K] (moe_gather_split); with them
-  // the pipelined kernel runs (needs K % 64 == 0, N % 16 == 0)
+  // optional: A as bf16 hi/lo planes; with them the pipelined kernel runs
+  // (needs K % 64 == 0, N % 16 == 0). a_per_token: one row per token
+  // ([T][K], row order[i] / topk read for expert-order row i); else the
+  // rows in expert order ([slots][K], row i = the row of slot order[i]:
+  // moe_gather_split, or y_hi/y_lo of the gate/up GEMM)
   uint16_t *a_hi, *a_lo;
+  // optional, SwiGLU pair on the pipelined kernel: silu(g) * u written as
+  // bf16 hi/lo planes in expert order ([slots][N], the next GEMM's A)
+  // instead of y
+  uint16_t *y_hi, *y_lo;
 };
 void moe_group_gemm(const MoeGemmParams& p, hipStream_t s);
 // a_hi/a_lo[i] = split of the A row of slot order[i] (a[order[i] / topk] when
-// a_per_token, else a[order[i]]), i < slots.
+// a_per_token, else a[order[i]]), i < slots (for an A in expert order when
+// the previous GEMM could not write its planes).
 void moe_gather_split(const MoeGemmParams& p, hipStream_t s);
 // Whether moe_group_gemm takes the pipelined kernel for p (a_hi/a_lo set,
 // K % 64 == 0, K <= 8192, N % 16 == 0, 16-byte aligned operands).

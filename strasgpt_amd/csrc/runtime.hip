@@ -378,7 +378,7 @@ void ffn_moe(Dev* D, int l, int T) {
     sg::moe_route_logits(D->x, W16(D, W_FFN_NORM, l), D->eps, W16(D, W_ROUTER, l), D->E, D->d, D->moe_logits,
                          D->xn, s);
   } else {
-    {
+    if (T == 1) {  // (prefill: the RMSNorm rows came with the residual add)
       Prof pr(D, K_ELEM, 2.0 * T * d * 4, 0);
       sg::rmsnorm_rows(D->x, W16(D, W_FFN_NORM, l), D->xn, T, D->d, D->eps, s);
     }
@@ -408,14 +408,10 @@ void ffn_moe(Dev* D, int l, int T) {
     g.N = D->H;
     g.K = D->d;
     g.y = D->moe_act;
-    g.a_hi = D->moe_ahi;
-    g.a_lo = D->moe_alo;
+    // A: the RMSNorm rows' planes, one per token, read through the grouping
+    g.a_hi = D->xn_hi;
+    g.a_lo = D->xn_lo;
     if (!sg::moe_group_gemm2_ok(g)) g.a_hi = g.a_lo = nullptr;
-    {
-      Prof pr(D, K_MOE_GU_PRE, used * mxfp4_bytes(2 * H * d), 4.0 * n * H * d);
-      if (g.a_hi) sg::moe_gather_split(g, s);
-      sg::moe_group_gemm(g, s);
-    }
     sg::MoeGemmParams dn{};
     dn.blocks = W8(D, W_DB, l);
     dn.scales = W8(D, W_DS, l);
@@ -432,9 +428,20 @@ void ffn_moe(Dev* D, int l, int T) {
     dn.a_hi = D->moe_ahi;
     dn.a_lo = D->moe_alo;
     if (!sg::moe_group_gemm2_ok(dn)) dn.a_hi = dn.a_lo = nullptr;
+    // the gate/up GEMM writes the down GEMM's A planes in expert order
+    // when both run the pipelined kernel (no gather between them)
+    const bool planes = g.a_hi && dn.a_hi;
+    if (planes) {
+      g.y_hi = D->moe_ahi;
+      g.y_lo = D->moe_alo;
+    }
+    {
+      Prof pr(D, K_MOE_GU_PRE, used * mxfp4_bytes(2 * H * d), 4.0 * n * H * d);
+      sg::moe_group_gemm(g, s);
+    }
     {
       Prof pr(D, K_MOE_DOWN_PRE, used * mxfp4_bytes(H * d), 2.0 * n * H * d);
-      if (dn.a_hi) sg::moe_gather_split(dn, s);
+      if (dn.a_hi && !planes) sg::moe_gather_split(dn, s);
       sg::moe_group_gemm(dn, s);
       sg::moe_combine(D->moe_out, D->moe_w, T, D->topk, D->d, D->x, s);
     }
@@ -605,7 +612,8 @@ void prefill_norm(Dev* D, int T, int splits, const uint16_t* w) {
   n.d = D->d;
   n.y = D->moe ? D->xn : nullptr;
   n.y_hi = D->xn_hi;
-  n.y_lo = D->precision == sg::GEMM_SPLIT2 ? D->xn_lo : nullptr;
+  // (the MoE grouped GEMMs take both planes in either precision)
+  n.y_lo = D->precision == sg::GEMM_SPLIT2 || D->moe ? D->xn_lo : nullptr;
   Prof pr(D, K_ELEM, (double)T * D->d * (8 + 4.0 * n.splits), 0);
   sg::residual_norm(n, D->stream);
 }
