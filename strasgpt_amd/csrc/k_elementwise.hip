@@ -32,7 +32,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const uint
 // Residual add of a split-K projection and RMSNorm of the updated row. The
 // split partial sums are added in split order first, so x gains one
 // rounded term like the reference's x += dot (source/transformer.c:
-// 1439-1445, 1498-1504); then the reference RMSNorm (source/transformer.c:
+// 1439-1445, 1498-1504); an MoE layer's routed sum (the weighted expert
+// outputs, fmaf-chained in top-k order) is added the same way; then the
+// reference RMSNorm (source/transformer.c:
 // 978-999) is written as fp32 and/or as the bf16 hi/lo planes that the next
 // GEMM consumes (hi = bf16(y), lo = bf16(y - hi)).
 // One block per row, the row held in registers (NV float4 per thread,
@@ -80,6 +82,37 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(NormParams p) {
         v[i].y += o[i].y;
         v[i].z += o[i].z;
         v[i].w += o[i].w;
+        xr[e] = v[i];
+      }
+    }
+  }
+  if (p.routed) {
+    float4 acc[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < p.topk; j++) {
+      const float wj = p.routed_w[(size_t)row * p.topk + j];
+      const float4* oj = (const float4*)(p.routed + ((size_t)row * p.topk + j) * p.d);
+#pragma unroll
+      for (int i = 0; i < NV; i++) {
+        const int e = tid + 256 * i;
+        if (e < d4) {
+          const float4 q = oj[e];
+          acc[i].x = fmaf(wj, q.x, acc[i].x);
+          acc[i].y = fmaf(wj, q.y, acc[i].y);
+          acc[i].z = fmaf(wj, q.z, acc[i].z);
+          acc[i].w = fmaf(wj, q.w, acc[i].w);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int e = tid + 256 * i;
+      if (e < d4) {
+        v[i].x += acc[i].x;
+        v[i].y += acc[i].y;
+        v[i].z += acc[i].z;
+        v[i].w += acc[i].w;
         xr[e] = v[i];
       }
     }
@@ -278,6 +311,8 @@ void rmsnorm_rows(const float* x, const uint16_t* w, float* y, int rows, int d, 
 void residual_norm(const NormParams& p, hipStream_t s) {
   if (p.rows <= 0 || p.d <= 0) ST_DIE("residual_norm needs rows, d > 0");
   if (p.splits > 0 && !p.part) ST_DIE("residual_norm needs the partial sums");
+  if (p.routed && (!p.routed_w || p.topk < 1 || (uintptr_t)p.routed % 16))
+    ST_DIE("residual_norm: routed sum needs weights, top-k and aligned rows");
   if (p.d % 4 || p.d > 8192) ST_DIE("residual_norm needs d % 4 == 0 and d <= 8192");
   if ((uintptr_t)p.x % 16 || (p.part && (uintptr_t)p.part % 16) || (p.y && (uintptr_t)p.y % 16) ||
       (p.y_hi && (uintptr_t)p.y_hi % 8) || (p.y_lo && (uintptr_t)p.y_lo % 8) || (p.w && (uintptr_t)p.w % 8))

@@ -1231,16 +1231,6 @@ __global__ __launch_bounds__(256) void gather_split_kernel(MoeGemmParams p) {
   }
 }
 
-// x[t][n] += sum over j in top-k order of fmaf(w_j, out[t k + j][n], .).
-__global__ void combine_kernel(const float* out, const float* w, int T, int k, int N, float* x) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)T * N) return;
-  const size_t t = i / N, n = i % N;
-  float acc = 0.0f;
-  for (int j = 0; j < k; j++) acc = fmaf(w[t * k + j], out[(t * k + j) * N + n], acc);
-  x[i] += acc;
-}
-
 template <typename F>
 void set_lds(F kernel, size_t bytes) {
   if (bytes > 160 * 1024) ST_DIE("MoE kernel rows do not fit in LDS");
@@ -1419,10 +1409,5 @@ void moe_group_gemm(const MoeGemmParams& p, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
-void moe_combine(const float* out, const float* w, int T, int k, int N, float* x, hipStream_t s) {
-  const size_t n = (size_t)T * N;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, w, T, k, N, x);
-  HIP_CHECK(hipGetLastError());
-}
 
 }  // namespace sg

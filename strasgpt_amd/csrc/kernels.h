@@ -119,8 +119,6 @@ void moe_gather_split(const MoeGemmParams& p, hipStream_t s);
 // Whether moe_group_gemm takes the pipelined kernel for p (a_hi/a_lo set,
 // K % 64 == 0, K <= 8192, N % 16 == 0, 16-byte aligned operands).
 bool moe_group_gemm2_ok(const MoeGemmParams& p);
-// x[t][n] += sum_j in top-k order fmaf(w[t k + j], out[t k + j][n], .)
-void moe_combine(const float* out, const float* w, int T, int k, int N, float* x, hipStream_t s);
 // The device MXFP4 decode of the expert kernels on `nblocks` blocks of 32
 // values (16 code bytes + 1 E8M0 scale each): out[32 b + i] (test hook);
 // bf16_tiles: the grouped prefill GEMM's bf16 conversion, widened back.
@@ -189,6 +187,11 @@ struct NormParams {
   float* x;
   const float* part;  // [splits][rows][d] or null
   int splits;
+  // MoE routed sum or null: x[r] += sum over j in top-k order of
+  // fmaf(routed_w[r topk + j], routed[r topk + j][.], .) (after the partials)
+  const float* routed;
+  const float* routed_w;
+  int topk;
   const uint16_t* w;  // norm weight or null (residual only)
   float eps;
   int rows, d;

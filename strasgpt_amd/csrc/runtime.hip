@@ -367,7 +367,9 @@ constexpr int kMoeGroupedMinTokens = 8;
 
 // MoE FFN of T rows: RMSNorm, router top-k, MXFP4 SwiGLU experts, routed
 // down-projection accumulated into the residual stream.
-void ffn_moe(Dev* D, int l, int T) {
+// Returns true when the routed sum of the expert outputs is left for the
+// next prefill_norm to add (D->moe_out, weights D->moe_w).
+bool ffn_moe(Dev* D, int l, int T) {
   hipStream_t s = D->stream;
   const double d = D->d, H = D->H, k = D->topk;
   const bool fused = T == 1 && sg::moe_route_logits_supported(D->E, D->topk, D->d);
@@ -443,9 +445,8 @@ void ffn_moe(Dev* D, int l, int T) {
       Prof pr(D, K_MOE_DOWN_PRE, used * mxfp4_bytes(H * d), 2.0 * n * H * d);
       if (dn.a_hi && !planes) sg::moe_gather_split(dn, s);
       sg::moe_group_gemm(dn, s);
-      sg::moe_combine(D->moe_out, D->moe_w, T, D->topk, D->d, D->x, s);
     }
-    return;
+    return true;
   }
   sg::MoeGemvParams g{};
   g.blocks = W8(D, W_GB, l);
@@ -482,6 +483,7 @@ void ffn_moe(Dev* D, int l, int T) {
     Prof pr(D, T == 1 ? K_MOE_DOWN : K_MOE_DOWN_PRE, T * k * mxfp4_bytes(H * d), 2.0 * T * k * H * d);
     sg::moe_gemv_down(dn, s);
   }
+  return false;
 }
 
 // Layer l's K and V cache bases (fp32 or bf16 elements).
@@ -601,11 +603,16 @@ void layer_decode(Dev* D, int l) {
 // Residual add of a projection (split-K partial sums in D->ws, or already
 // added) and the RMSNorm with weight w of the updated rows into the bf16
 // planes of the next GEMM (and the fp32 rows for the MoE experts).
-void prefill_norm(Dev* D, int T, int splits, const uint16_t* w) {
+void prefill_norm(Dev* D, int T, int splits, const uint16_t* w, bool routed = false) {
   sg::NormParams n{};
   n.x = D->x;
   n.part = splits > 1 ? D->ws : nullptr;
   n.splits = splits > 1 ? splits : 0;
+  if (routed) {  // the MoE layer's routed sum, in top-k order
+    n.routed = D->moe_out;
+    n.routed_w = D->moe_w;
+    n.topk = D->topk;
+  }
   n.w = w;
   n.eps = D->eps;
   n.rows = T;
@@ -779,8 +786,8 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
                                  W16(D, W_DOWN, l), T, D->d, D->H, K_DOWN_GEMM);
     prefill_norm(D, T, sd, next_norm);
   } else {
-    ffn_moe(D, l, T);
-    prefill_norm(D, T, 0, next_norm);
+    const bool routed = ffn_moe(D, l, T);
+    prefill_norm(D, T, 0, next_norm, routed);
   }
 }
 
