@@ -714,18 +714,18 @@ void dispatch_tile(const GemmParams& p, int splits, hipStream_t s) {
     // in flight (SwiGLU at 8 rows, Llama-3.2-1B shape: 23.0 us against 25.0
     // for 64 x 128 tiles)
     if (EPI == GEMM_SWIGLU && p.M <= kSmallM && p.K % 64 == 0) shape = 8;
-    else
-    if (huge >= 192 && 4 * huge >= 3 * 256 * rounds) {
+    else if ((huge >= 192 && 4 * huge >= 3 * 256 * rounds) || (EPI == GEMM_SWIGLU && huge >= 128 && huge <= 256)) {
       shape = 7;
       // 128 x 384 tiles where their last round of blocks is at least a
       // tenth fuller (bf16x2): the Mistral-Small-24B QKV projection at
       // M = 2048 (N = 6144) is 256 of them against 192 of 256 x 256, 240
-      // against 264 us stand-alone with the weights from HBM
+      // against 264 us stand-alone with the weights from HBM; the Qwen3-4B
+      // gate/up SwiGLU GEMM at M = 512, 204 against 152 tiles, 115 against
+      // 127 us
       const long t384 = (long)((p.N + 3 * cols - 1) / (3 * cols)) * ((p.M + 127) / 128) * splits;
       const long r384 = (t384 + 255) / 256;
       if (PREC == GEMM_SPLIT2 && 10 * t384 * rounds >= 11 * huge * r384) shape = 9;
     }
-    else if (EPI == GEMM_SWIGLU && huge >= 128 && huge <= 256) shape = 7;
     else if (wide >= 1024) shape = 4;
     else if (p.K % 64 == 0 && small > 256) shape = 5;
     else if (p.K % 64 == 0 && small >= 64) shape = 6;
