@@ -298,23 +298,40 @@ template <int HD, bool B16>
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* kc, const float* vc, uint16_t* khi,
                                                          uint16_t* klo, uint16_t* vthi, uint16_t* vtlo,
                                                          int ctx, int ctx_pad, int r0, int r1) {
+  // every load of the thread is issued before the first is used (a loop of
+  // load, convert, store per element waits a memory latency per element)
+  constexpr int KP = 32 * HD / 2 / 256;  // K pairs per thread
+  constexpr int VE = 32 * HD / 256;      // V elements per thread
   __shared__ float vs[32][HD + 1];
   const int tid = threadIdx.x, h = blockIdx.y;
   const int rb = r0 + blockIdx.x * 32;  // first row of the block
   const size_t kbase = (size_t)h * ctx * HD;
-  for (int i = tid; i < 32 * HD / 2; i += 256) {
-    const int r = rb + (2 * i) / HD, dd = (2 * i) % HD;
+  float2 kx[KP];
+  float vx[VE];
+#pragma unroll
+  for (int j = 0; j < KP; j++) {
+    const int i = tid + 256 * j, r = min(rb + (2 * i) / HD, r1 - 1), dd = (2 * i) % HD;
+    kx[j] = cache_pair<HD, B16>(kc, kbase + (size_t)r * HD + dd);
+  }
+#pragma unroll
+  for (int j = 0; j < VE; j++) {
+    const int i = tid + 256 * j, r = min(rb + i / HD, r1 - 1), dd = i % HD;
+    vx[j] = cache_at<B16>(vc, kbase + (size_t)r * HD + dd);
+  }
+#pragma unroll
+  for (int j = 0; j < KP; j++) {
+    const int i = tid + 256 * j, r = rb + (2 * i) / HD, dd = (2 * i) % HD;
     if (r < r1) {
-      const float2 x = cache_pair<HD, B16>(kc, kbase + (size_t)r * HD + dd);
       uint32_t hi, lo;
-      split2(x.x, x.y, hi, lo);
+      split2(kx[j].x, kx[j].y, hi, lo);
       *(uint32_t*)(khi + kbase + (size_t)r * HD + dd) = hi;
       *(uint32_t*)(klo + kbase + (size_t)r * HD + dd) = lo;
     }
   }
-  for (int i = tid; i < 32 * HD; i += 256) {
-    const int r = rb + i / HD, dd = i % HD;
-    vs[i / HD][dd] = r < r1 ? cache_at<B16>(vc, kbase + (size_t)r * HD + dd) : 0.0f;
+#pragma unroll
+  for (int j = 0; j < VE; j++) {
+    const int i = tid + 256 * j;
+    vs[i / HD][i % HD] = rb + i / HD < r1 ? vx[j] : 0.0f;
   }
   __syncthreads();
   const size_t vbase = (size_t)h * HD * ctx_pad;

@@ -218,6 +218,94 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   for (int e = lane; e < hd; e += WAVE) row16[e] = f32_to_bf16_any(v[e]);
 }
 
+// The same for head sizes 16-128 with at most one rotated pair per lane,
+// four heads per block (one per wavefront; the loop form's one-wavefront
+// blocks are dispatched slower than they finish), with every load of the
+// wavefront (the row, the norm weights, the lane's rotation) issued before
+// the first is used: the loop form waits a memory latency per step (row,
+// then weights, then rotation). Same arithmetic in the same order.
+constexpr int kQkrHeads = 4;
+template <int HD>
+__global__ __launch_bounds__(kQkrHeads * WAVE) void qk_norm_rope_hd_kernel(
+    float* q, int q_heads, int heads, float* kcache, int ctx, const int* pos, const uint16_t* qn,
+    const uint16_t* kn, float eps, const float* rope, int pair_bound, int pair_offset, int pair_stride,
+    const float* kstage) {
+#pragma clang fp contract(off)
+  constexpr int PER = (HD + WAVE - 1) / WAVE;
+  __shared__ float vsh[kQkrHeads][HD];
+  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const int t = blockIdx.x, head = blockIdx.y * kQkrHeads + wave;
+  if (head >= heads) return;  // (no block-wide barrier below)
+  float* v = vsh[wave];
+  const int P = *pos + t;
+  const bool staged = kstage && head >= q_heads;
+  float* row;
+  const float* src;
+  const uint16_t* nw;
+  if (head < q_heads) {
+    row = q + ((size_t)t * q_heads + head) * HD;
+    src = row;
+    nw = qn;
+  } else {
+    const int kh = head - q_heads;
+    row = kcache + ((size_t)kh * ctx + P) * HD;  // a bf16 row when staged
+    src = staged ? kstage + ((size_t)t * (heads - q_heads) + kh) * HD : row;
+    nw = kn;
+  }
+  float xv[PER], wv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int e = lane + i * WAVE;
+    xv[i] = e < HD ? src[e] : 0.0f;
+    wv[i] = nw && e < HD ? bf16_to_f32(nw[e]) : 1.0f;
+  }
+  const int h = lane * pair_stride;
+  const bool pair = h < pair_bound;
+  const float* cs = rope + (size_t)P * HD;
+  const float fr = pair ? cs[h] : 1.0f, fi = pair ? cs[h + pair_offset] : 0.0f;
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; i++)
+    if (lane + i * WAVE < HD) ss = fmaf(xv[i], xv[i], ss);
+  ss = wave_sum(ss);
+  const float s = nw ? rms_scale(ss, HD, eps) : 1.0f;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int e = lane + i * WAVE;
+    if (e < HD) v[e] = nw ? (xv[i] * s) * wv[i] : xv[i];
+  }
+  // the wavefront's LDS writes before its reads of other lanes' elements
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  float r0 = 0.0f, r1 = 0.0f;
+  if (pair) {
+    const float v0 = v[h], v1 = v[h + pair_offset];
+    r0 = v0 * fr - v1 * fi;
+    r1 = v0 * fi + v1 * fr;
+  }
+  if (!staged) {
+    if (pair) {
+      row[h] = r0;
+      row[h + pair_offset] = r1;
+    }
+    return;
+  }
+  // staged key: rotate in LDS, then store every element rounded
+  __builtin_amdgcn_wave_barrier();
+  if (pair) {
+    v[h] = r0;
+    v[h + pair_offset] = r1;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  uint16_t* row16 = (uint16_t*)kcache + ((size_t)(head - q_heads) * ctx + P) * HD;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int e = lane + i * WAVE;
+    if (e < HD) row16[e] = f32_to_bf16_any(v[e]);
+  }
+}
+
 // ------------------------------------------------------------- argmax --
 constexpr int kArgmaxBlocks = 512;
 
@@ -335,9 +423,27 @@ void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T, con
   if (hd > 512 || hd % 2) ST_DIE("head_dim must be even and at most 512");
   if (pair_stride < 1 || pair_bound - pair_stride + pair_offset >= hd)
     ST_DIE("inconsistent RoPE pair geometry");
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(T, q_heads + kv_heads), dim3(64), 0, s, q,
-                     q_heads, kcache, ctx, hd, pos, qn, kn, eps, rope, pair_bound,
-                     pair_offset, pair_stride, kstage);
+  const dim3 grid(T, q_heads + kv_heads);
+  if ((pair_bound + pair_stride - 1) / pair_stride <= WAVE) {
+    const dim3 g4(T, (q_heads + kv_heads + kQkrHeads - 1) / kQkrHeads);
+    switch (hd) {
+#define QKR_CASE(HD)                                                                                        \
+  case HD:                                                                                                 \
+    hipLaunchKernelGGL(qk_norm_rope_hd_kernel<HD>, g4, dim3(kQkrHeads * WAVE), 0, s, q, q_heads,             \
+                       q_heads + kv_heads, kcache, ctx, pos, qn, kn, eps, rope, pair_bound, pair_offset,    \
+                       pair_stride, kstage);                                                              \
+    HIP_CHECK(hipGetLastError());                                                                         \
+    return;
+      QKR_CASE(16)
+      QKR_CASE(32)
+      QKR_CASE(64)
+      QKR_CASE(128)
+#undef QKR_CASE
+      default: break;
+    }
+  }
+  hipLaunchKernelGGL(qk_norm_rope_kernel, grid, dim3(64), 0, s, q, q_heads, kcache, ctx, hd, pos, qn, kn, eps,
+                     rope, pair_bound, pair_offset, pair_stride, kstage);
   HIP_CHECK(hipGetLastError());
 }
 
