@@ -60,17 +60,26 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(NormParams p) {
       const int e = tid + 256 * i;
       o[i] = e < d4 ? p0[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (int sp = 1; sp < p.splits; sp++) {
-      const float4* ps = (const float4*)(p.part + ((size_t)sp * p.rows + row) * p.d);
+    // four splits' loads in flight before their sums, added in split order
+    for (int sp = 1; sp < p.splits; sp += 4) {
+      float4 q[4][NV];
 #pragma unroll
-      for (int i = 0; i < NV; i++) {
-        const int e = tid + 256 * i;
-        if (e < d4) {
-          const float4 q = ps[e];
-          o[i].x += q.x;
-          o[i].y += q.y;
-          o[i].z += q.z;
-          o[i].w += q.w;
+      for (int u = 0; u < 4; u++) {
+        const float4* ps = (const float4*)(p.part + ((size_t)min(sp + u, p.splits - 1) * p.rows + row) * p.d);
+#pragma unroll
+        for (int i = 0; i < NV; i++) q[u][i] = ps[min(tid + 256 * i, d4 - 1)];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (sp + u >= p.splits) break;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+          if (tid + 256 * i < d4) {
+            o[i].x += q[u][i].x;
+            o[i].y += q[u][i].y;
+            o[i].z += q[u][i].z;
+            o[i].w += q[u][i].w;
+          }
         }
       }
     }
@@ -90,18 +99,29 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(NormParams p) {
     float4 acc[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < p.topk; j++) {
-      const float wj = p.routed_w[(size_t)row * p.topk + j];
-      const float4* oj = (const float4*)(p.routed + ((size_t)row * p.topk + j) * p.d);
+    // four experts' rows in flight before their products, in top-k order
+    for (int j = 0; j < p.topk; j += 4) {
+      float4 q[4][NV];
+      float wj[4];
 #pragma unroll
-      for (int i = 0; i < NV; i++) {
-        const int e = tid + 256 * i;
-        if (e < d4) {
-          const float4 q = oj[e];
-          acc[i].x = fmaf(wj, q.x, acc[i].x);
-          acc[i].y = fmaf(wj, q.y, acc[i].y);
-          acc[i].z = fmaf(wj, q.z, acc[i].z);
-          acc[i].w = fmaf(wj, q.w, acc[i].w);
+      for (int u = 0; u < 4; u++) {
+        const size_t slot = (size_t)row * p.topk + min(j + u, p.topk - 1);
+        wj[u] = p.routed_w[slot];
+        const float4* oj = (const float4*)(p.routed + slot * p.d);
+#pragma unroll
+        for (int i = 0; i < NV; i++) q[u][i] = oj[min(tid + 256 * i, d4 - 1)];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (j + u >= p.topk) break;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+          if (tid + 256 * i < d4) {
+            acc[i].x = fmaf(wj[u], q[u][i].x, acc[i].x);
+            acc[i].y = fmaf(wj[u], q[u][i].y, acc[i].y);
+            acc[i].z = fmaf(wj[u], q[u][i].z, acc[i].z);
+            acc[i].w = fmaf(wj[u], q[u][i].w, acc[i].w);
+          }
         }
       }
     }
