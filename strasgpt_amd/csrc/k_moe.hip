@@ -1076,20 +1076,32 @@ __global__ __launch_bounds__(256, 2) void group_gemm2_kernel(MoeGemmParams p) {
 
   // step t: A rows and codes into ring slot t % QNA (indexes past the last
   // step clamped to it: read, never used)
-  auto issue_group = [&](int t) {
+  auto issue_a = [&](int t) {
     const int tc = min(t, nk - 1);
     unsigned char* as = ql + QL::a + (t % QNA) * QL::a_stage;
 #pragma unroll
     for (int i = 0; i < QAI; i++)
       __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + tc * QKS),
                                        (lds_ptr)(as + (QAI * wave + i) * 1024), 16, 0, 0);
+  };
+  auto issue_b = [&](int t) {
+    const int tc = min(t, nk - 1);
     unsigned char* bs = ql + QL::b + (t % QNB) * QL::b_stage;
 #pragma unroll
     for (int i = 0; i < QBI; i++)
       __builtin_amdgcn_global_load_lds((const void*)(bsrc[i] + (size_t)tc * 32),
                                        (lds_ptr)(bs + (QBI * wave + i) * 1024), 16, 0, 0);
   };
-  for (int t = 0; t < QNA - 1; t++) issue_group(t);
+  auto issue_group = [&](int t) {
+    issue_a(t);
+    issue_b(t);
+  };
+  // the codes of the first steps go out before the A rows, whose addresses
+  // wait for the slot indices when A is read one row per token
+#pragma unroll
+  for (int t = 0; t < QNA - 1; t++) issue_b(t);
+#pragma unroll
+  for (int t = 0; t < QNA - 1; t++) issue_a(t);
   // the scales (a per-shape number of DMA instructions) and the first
   // groups: waited for here, so that the loop's waits are exact counts
   wait_dma_behind<0>();
