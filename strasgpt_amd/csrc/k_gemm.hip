@@ -836,11 +836,22 @@ __global__ __launch_bounds__(256) void split_epilogue_kernel(GemmParams p, const
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (size_t)M * N) return;
   const int m = (int)(idx / N), n = (int)(idx % N);
-  float v = 0.0f;
-  for (int sp = 0; sp < splits; sp++) v += part[((size_t)sp * M + m) * N + n];
+  // the partials of four splits requested before their sums (in split order)
+  auto sum_splits = [&](const float* pp) {
+    float acc = 0.0f;
+    for (int sp = 0; sp < splits; sp += 4) {
+      float x[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) x[u] = pp[((size_t)min(sp + u, splits - 1) * M + m) * N + n];
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        if (sp + u < splits) acc += x[u];
+    }
+    return acc;
+  };
+  const float v = sum_splits(part);
   if (EPI == GEMM_SWIGLU) {
-    float u = 0.0f;
-    for (int sp = 0; sp < splits; sp++) u += part2[((size_t)sp * M + m) * N + n];
+    const float u = sum_splits(part2);
     store_split(p.c_hi, p.c_lo, (size_t)m * p.ldc + n, silu_mul(v, u), p.c_lo != nullptr);
   } else if (n < p.q_dim) {
     p.q[(size_t)m * p.q_dim + n] = v;
