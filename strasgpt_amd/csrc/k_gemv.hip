@@ -344,6 +344,22 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Sum over y < ny (at most YMAX) of part[y * stride], in y order, with
+// every partial requested (agent-coherently) before the first is added.
+template <int YMAX>
+__device__ __forceinline__ float sum_parts(const float* part, size_t stride, int ny) {
+  float v[YMAX];
+#pragma unroll
+  for (int y = 0; y < YMAX; y++) v[y] = y < ny ? cload(part + (size_t)y * stride) : 0.0f;
+  float sum = v[0];
+#pragma unroll
+  for (int y = 1; y < YMAX; y++)
+    if (y < ny) sum += v[y];
+  return sum;
+}
+constexpr int kSplitRangesMax = 8;   // K ranges of the split-K third form
+constexpr int kRowsRangesMax = 16;   // K ranges of the split-K rows form
+
 // SPLIT (residual epilogue, no RMSNorm): block (x, y) takes the rows of x
 // over K range y of gridDim.y ranges of whole steps: its row sums are
 // partial sums, stored agent-coherently to p.part[y][n]; the last of the
@@ -500,9 +516,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   compiler_fence();
   const int n_end = min(N, min(groups, g0 + per) * WV);
   for (int n = g0 * WV + (int)threadIdx.x; n < n_end; n += NT) {
-    float sum = cload(p.part + n);
-    for (int y = 1; y < (int)gridDim.y; y++) sum += cload(p.part + (size_t)y * N + n);
-    p.y[n] += sum;
+    p.y[n] += sum_parts<kSplitRangesMax>(p.part + n, N, gridDim.y);
   }
   if (threadIdx.x == 0) __hip_atomic_store(p.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -815,9 +829,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
   const int n0 = g0 * WV * R, n_end = min(N, min(groups, g0 + per) * WV * R);
   for (int i = (int)threadIdx.x; i < (n_end - n0) * M; i += NT) {
     const int m = i / (n_end - n0), n = n0 + i % (n_end - n0);
-    float sum = cload(p.part + (size_t)m * N + n);
-    for (int y = 1; y < (int)gridDim.y; y++) sum += cload(p.part + ((size_t)y * MM + m) * N + n);
-    p.y[(size_t)m * N + n] += sum;
+    p.y[(size_t)m * N + n] += sum_parts<kRowsRangesMax>(p.part + (size_t)m * N + n, (size_t)MM * N, gridDim.y);
   }
   if (threadIdx.x == 0) __hip_atomic_store(p.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -913,7 +925,7 @@ bool launch_v3(const GemvParams& p, hipStream_t s, int cap) {
 // row blocks per range, 4-16 steps in flight and ranges of 8 or 32 steps
 // measured the same.
 constexpr int kSplitSteps = 16;
-constexpr int kSplitMax = 8;  // ranges: K <= 65536
+constexpr int kSplitMax = kSplitRangesMax;  // ranges: K <= 65536
 template <int PD>
 bool launch_v3_split(const GemvParams& p, hipStream_t s, int cap) {
   const int S = (p.K + kStep - 1) / kStep;
@@ -936,7 +948,7 @@ bool launch_v3_split(const GemvParams& p, hipStream_t s, int cap) {
 // of eight wavefronts per CU); rows with RMSNorm must fit whole, residual
 // rows longer than that split over K (p.part / p.counters given).
 constexpr int kRowsLds = 128 * 1024;
-constexpr int kRowsSplitMax = 16;
+constexpr int kRowsSplitMax = kRowsRangesMax;
 
 template <int MM, int EPI, bool NORM, bool EXACT, bool SPLIT, int R>
 void rows_go_r(const GemvParams& p, dim3 grid, size_t shm, hipStream_t s) {
