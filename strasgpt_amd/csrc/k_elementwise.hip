@@ -17,6 +17,18 @@ __global__ __launch_bounds__(256) void embed_kernel(const int* tok, const uint16
   for (int e = threadIdx.x; e < d; e += blockDim.x) x[(size_t)t * d + e] = bf16_to_f32(row[e]);
 }
 
+// The same with one 16-byte load (8 values) per thread, grid (T, d / 2048
+// rounded up): one memory latency per row, where the loop above waits one
+// per 256 values of a row (a decode step's single row: 10.9 us at d = 5120).
+__global__ __launch_bounds__(256) void embed8_kernel(const int* tok, const uint16_t* table, int d, float* x) {
+  const int t = blockIdx.x, e = (blockIdx.y * 256 + threadIdx.x) * 8;
+  if (e >= d) return;
+  const uint4 w = *(const uint4*)(table + (size_t)tok[t] * d + e);
+  float* xr = x + (size_t)t * d + e;
+  *(float4*)xr = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+  *(float4*)(xr + 4) = make_float4(bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w));
+}
+
 // Reference rmsnorm (source/transformer.c:978-999) on one row per block.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const uint16_t* w,
                                                       float* y, int d, float eps) {
@@ -409,7 +421,10 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(ArgmaxParams p, int p
 
 void embed(const int* tok, int T, const uint16_t* table, int d, float* x, hipStream_t s) {
   if (T <= 0) ST_DIE("embed needs T > 0");
-  hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, s, tok, table, d, x);
+  if (d % 8 == 0 && (uintptr_t)table % 16 == 0 && (uintptr_t)x % 16 == 0)
+    hipLaunchKernelGGL(embed8_kernel, dim3(T, (d + 2047) / 2048), dim3(256), 0, s, tok, table, d, x);
+  else
+    hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, s, tok, table, d, x);
   HIP_CHECK(hipGetLastError());
 }
 
