@@ -115,6 +115,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
   int row0 = (v * per * kWaves + wave) * R;
   const int row_end = g_end * kWaves * R;
 
+  const int P = EPI == GEMV_QKV ? *p.pos : 0;  // (before any store: as gemv_store)
   Chunk<R, U, DUAL> cur, nxt;
   if (row0 < min(N, row_end)) load_chunk<R, U, DUAL>(p, row0, 0, lane, cur);
   if (LDS) stage_row<NORM>(p, xs, red);
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
           } else {
             const int j = n - p.q_dim - p.kv_dim;
             const int head = j / p.head_dim, h = j % p.head_dim;
-            const size_t at = ((size_t)head * p.ctx + *p.pos) * p.head_dim + h;
+            const size_t at = ((size_t)head * p.ctx + P) * p.head_dim + h;
             if (p.kv_bf16) ((uint16_t*)p.vcache)[at] = f32_to_bf16_any(acc[r]);
             else p.vcache[at] = acc[r];
           }
@@ -180,8 +181,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
 // kV2Lds bytes and XF float4 per thread.
 constexpr int kV2Lds = 64 * 1024;
 
+// P: the step's position (*p.pos), read by the kernel before its first
+// store: a read of it here, after the kernel's stores, would be a vector
+// load that waits for every weight load in flight.
 template <int EPI>
-__device__ __forceinline__ void gemv_store(const GemvParams& p, int n, float a, float a2) {
+__device__ __forceinline__ void gemv_store(const GemvParams& p, int n, float a, float a2, int P) {
   if (EPI == GEMV_STORE) {
     p.y[n] = a;
   } else if (EPI == GEMV_RESIDUAL) {
@@ -196,10 +200,36 @@ __device__ __forceinline__ void gemv_store(const GemvParams& p, int n, float a, 
     } else {
       const int j = n - p.q_dim - p.kv_dim;
       const int head = j / p.head_dim, h = j % p.head_dim;
-      const size_t at = ((size_t)head * p.ctx + *p.pos) * p.head_dim + h;
+      const size_t at = ((size_t)head * p.ctx + P) * p.head_dim + h;
       if (p.kv_bf16) ((uint16_t*)p.vcache)[at] = f32_to_bf16_any(a);
       else p.vcache[at] = a;
     }
+  }
+}
+
+// The residual epilogue's y values of a wavefront's rows r < WAVE (row
+// (g0 + r) * wv + wave in lane r), loaded before the weight stream. Read at
+// a row's end instead, each would wait for every weight load in flight (a
+// load completes in issue order), draining the ring once per row: with the
+// input row in registers and an 8-deep ring (Llama-3.2-1B O and down) that
+// cost 2.9% of the decode step; the LDS-staged third form, with more
+// wavefronts per SIMD to cover the drain, measured no better with it.
+template <int EPI>
+__device__ __forceinline__ float residual_ahead(const GemvParams& p, int g0, int wv, int wave, int nrows,
+                                                int lane) {
+  return EPI == GEMV_RESIDUAL && lane < nrows ? p.y[(size_t)(g0 + lane) * wv + wave] : 0.0f;
+}
+
+// Row n's result a (and a2): the residual epilogue adds y[n] as held in
+// lane rowi of yr by residual_ahead (rows past the first WAVE read it).
+template <int EPI>
+__device__ __forceinline__ void gemv_store_row(const GemvParams& p, int n, int rowi, float yr, float a, float a2,
+                                               int lane, int P) {
+  if (EPI == GEMV_RESIDUAL && rowi < WAVE) {
+    const float y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(yr), rowi));
+    if (lane == 0) p.y[n] = y + a;
+  } else if (lane == 0) {
+    gemv_store<EPI>(p, n, a, a2, P);
   }
 }
 
@@ -230,11 +260,16 @@ __global__ __launch_bounds__(kThreads) void gemv2_kernel(GemvParams p) {
     xv[i] = *(const float4*)(p.x + k);
     if (NORM) nv[i] = *(const uint2*)(p.norm_w + k);
   }
+  const float yr = residual_ahead<EPI>(p, g0, kWaves, wave, nrows, lane);
+  const int P = EPI == GEMV_QKV ? *p.pos : 0;
 
   // The ring. The refill cursor (rrow, rstep) walks the items in order.
   // Refills past the last item are issued all the same (so that every
   // consumption waits for an exact count of newer loads) but read the
-  // first 1 KiB of the input row, which is in cache, instead of weights.
+  // first 1 KiB of the input row, which is in cache, instead of weights;
+  // the up matrix's refills there read the neighbouring lane's 16 bytes
+  // (at the gate refill's own address the compiler reuses that load's
+  // value, a copy that waits for every load in flight at each refill).
   uint4 w[kPD], w2[DUAL ? kPD : 1];
   const int lk = lane * 8;
   int rrow = 0, rstep = 0;
@@ -244,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void gemv2_kernel(GemvParams p) {
     const int k = EXACT ? rstep * kStep + lk : min(rstep * kStep + lk, K - 8);
     const uint16_t* wa = past ? (const uint16_t*)p.x + lk : p.w + row * K + k;
     a = load_nt_u4(wa);
-    if (DUAL) b = load_nt_u4(past ? wa : p.w2 + row * K + k);
+    if (DUAL) b = load_nt_u4(past ? (const uint16_t*)p.x + (lk ^ 8) : p.w2 + row * K + k);
     if (++rstep == S) {
       rstep = 0;
       rrow++;
@@ -310,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void gemv2_kernel(GemvParams p) {
         if (DUAL) acc2 = dot8(b, xa, xb, acc2);
         if (++step == S) {
           const float r1 = wave_total(acc), r2 = DUAL ? wave_total(acc2) : 0.0f;
-          if (lane == 0) gemv_store<EPI>(p, (g0 + rowi) * kWaves + wave, r1, r2);
+          gemv_store_row<EPI>(p, (g0 + rowi) * kWaves + wave, rowi, yr, r1, r2, lane, P);
           acc = acc2 = 0.0f;
           step = 0;
           rowi++;
@@ -333,6 +368,29 @@ __global__ __launch_bounds__(kThreads) void gemv2_kernel(GemvParams p) {
 constexpr int kV3Nw = 8;  // uint2 of norm weights per thread: K <= 8192 with RMSNorm
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// global_load_lds_dwordx4 of 16 bytes per lane to LDS at l (wave-uniform)
+// + 16 * lane, written out in assembly (M0 saved and restored around it).
+// Issued through the compiler builtin, the DMA makes the compiler raise
+// the staging wait below (vmcnt(LOADS): the DMA done, the ring loads issued
+// after it still in flight) to vmcnt(0), draining the ring before the
+// first step. Hidden from the compiler, the DMA is ordered by that explicit
+// wait and the block barrier after it; the compiler's own waits for the
+// ring loads, which it counts without the older DMA, stay exact or wait
+// longer.
+__device__ __forceinline__ void dma_row16(const void* g, lds_ptr_t l) {
+  const int base = __builtin_amdgcn_readfirstlane((int)(uintptr_t)l);
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(base)
+      : "memory");
+}
 
 // Waits until at most N vector-memory operations of this wavefront are in
 // flight (N <= 63).
@@ -393,7 +451,8 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   const int nrows = max(0, min(min(groups, g0 + per), glast + 1) - g0);
   const int T = nrows * S;
 
-  // 1. this thread's RMSNorm weights (elements tid*4 + i*1024)
+  // 1. this thread's RMSNorm weights (elements tid*4 + i*1024), the position
+  const int P = EPI == GEMV_QKV ? *p.pos : 0;
   uint2 nv[NORM ? kV3Nw : 1];
   if (NORM) {
 #pragma unroll
@@ -407,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   for (int u0 = wave * WAVE; u0 < slots; u0 += NT) {
     const int u = u0 + lane;
     if (u < slots)  // inactive lanes write nothing
-      __builtin_amdgcn_global_load_lds((const void*)(x + u * 4), (lds_ptr_t)(xs + u0 * 4), 16, 0, 0);
+      dma_row16(x + u * 4, (lds_ptr_t)(xs + u0 * 4));
   }
   __builtin_amdgcn_sched_barrier(0);  // the row's DMA is issued before the ring loads
   // 3. the ring
@@ -420,7 +479,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
     const int k = EXACT ? rstep * kStep + lk : min(rstep * kStep + lk, K - 8);
     const uint16_t* wa = past ? (const uint16_t*)p.x + lk : wbase + row * KR + k;
     a = load_nt_u4(wa);
-    if (DUAL) b = load_nt_u4(past ? wa : p.w2 + row * KR + k);
+    if (DUAL) b = load_nt_u4(past ? (const uint16_t*)p.x + (lk ^ 8) : p.w2 + row * KR + k);  // (as gemv2)
     if (++rstep == S) {
       rstep = 0;
       rrow++;
@@ -488,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
           const int n = (g0 + rowi) * WV + wave;
           if (lane == 0) {
             if (SPLIT) cstore(p.part + (size_t)blockIdx.y * N + n, r1);
-            else gemv_store<EPI>(p, n, r1, r2);
+            else gemv_store<EPI>(p, n, r1, r2, P);
           }
           acc = acc2 = 0.0f;
           step = 0;
@@ -588,7 +647,7 @@ constexpr int log2_rows() {
 }
 
 template <int EPI, int MM, bool SPLIT>
-__device__ __forceinline__ void gemvm_store(const GemvParams& p, int m, int n, float a, float a2) {
+__device__ __forceinline__ void gemvm_store(const GemvParams& p, int m, int n, float a, float a2, int P) {
   const int N = p.N;
   if (SPLIT) {
     cstore(p.part + ((size_t)blockIdx.y * MM + m) * N + n, a);
@@ -599,7 +658,6 @@ __device__ __forceinline__ void gemvm_store(const GemvParams& p, int m, int n, f
   } else if (EPI == GEMV_SWIGLU) {
     p.y[(size_t)m * N + n] = silu_mul(a, a2);
   } else {  // GEMV_QKV: q, keys (cache or staging), values at position P + m
-    const int P = *p.pos;
     if (n < p.q_dim) {
       p.q[(size_t)m * p.q_dim + n] = a;
     } else if (n < p.q_dim + p.kv_dim) {
@@ -655,7 +713,9 @@ __global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
   const int nrows = max(0, min(min(groups, g0 + per), glast + 1) - g0);  // row sets of R
   const int T = nrows * S;
 
-  // 1. this thread's RMSNorm weights (elements tid*4 + i*NT*4)
+  // 1. this thread's RMSNorm weights (elements tid*4 + i*NT*4), the
+  // position (read here, before any store: as gemv_store)
+  const int P = EPI == GEMV_QKV ? *p.pos : 0;
   uint2 nv[NORM ? kV3Nw : 1];
   if (NORM) {
 #pragma unroll
@@ -672,7 +732,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
     for (int u0 = wave * WAVE; u0 < slots; u0 += NT) {
       const int u = u0 + lane;
       if (u < slots)  // inactive lanes write nothing
-        __builtin_amdgcn_global_load_lds((const void*)(xr + u * 4), (lds_ptr_t)(dst + u0 * 4), 16, 0, 0);
+        dma_row16(xr + u * 4, (lds_ptr_t)(dst + u0 * 4));
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // the rows' DMA is issued before the ring loads
@@ -803,7 +863,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
             float r2 = 0.0f;
             if constexpr (DUAL) r2 = multi_total<MM>(acc2[r], lane);
             const int n = ((g0 + rowi) * WV + wave) * R + r;
-            if (storer && n < N) gemvm_store<EPI, MM, SPLIT>(p, mrow, n, r1, r2);
+            if (storer && n < N) gemvm_store<EPI, MM, SPLIT>(p, mrow, n, r1, r2, P);
 #pragma unroll
             for (int m = 0; m < MM; m++) acc[r][m] = acc2[DUAL ? r : 0][m] = 0.0f;
           }
