@@ -73,6 +73,32 @@ __device__ __forceinline__ void gstore(float* p, float v) {
   *(__attribute__((address_space(1))) float*)p = v;
 }
 
+// global_load_lds_dwordx4: 16 bytes per lane from g to LDS at l
+// (wave-uniform) + 16 * lane, written out in assembly (M0 saved and
+// restored around it). Issued through the compiler builtin, an LDS DMA
+// makes the compiler turn every later wait on vector memory into
+// vmcnt(0) while it is pending (a staging wait meant to leave the loads
+// issued after the DMA in flight drains them; a wait for a value loaded
+// before the DMA waits for the DMA too). Hidden from the compiler, the DMA
+// is ordered by the caller's explicit s_waitcnt before a barrier; the
+// compiler's own waits for later loads, which it counts without the older
+// DMA, are then exact or longer. (In the MXFP4 expert GEMVs, selecting the
+// experts first and then issuing this DMA and the weights measured 0.6%
+// slower than the DMA first with the builtin.)
+__device__ __forceinline__ void dma16_hidden(const void* g, __attribute__((address_space(3))) void* l) {
+  const int base = __builtin_amdgcn_readfirstlane((int)(uintptr_t)l);
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(base)
+      : "memory");
+}
+
 // 128-bit non-temporal load from global memory (global, not flat,
 // instructions whatever the compiler knows of where `p` came from).
 __device__ __forceinline__ uint4 load_nt_u4(const void* p) {

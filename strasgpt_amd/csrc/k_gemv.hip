@@ -369,28 +369,6 @@ constexpr int kV3Nw = 8;  // uint2 of norm weights per thread: K <= 8192 with RM
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// global_load_lds_dwordx4 of 16 bytes per lane to LDS at l (wave-uniform)
-// + 16 * lane, written out in assembly (M0 saved and restored around it).
-// Issued through the compiler builtin, the DMA makes the compiler raise
-// the staging wait below (vmcnt(LOADS): the DMA done, the ring loads issued
-// after it still in flight) to vmcnt(0), draining the ring before the
-// first step. Hidden from the compiler, the DMA is ordered by that explicit
-// wait and the block barrier after it; the compiler's own waits for the
-// ring loads, which it counts without the older DMA, stay exact or wait
-// longer.
-__device__ __forceinline__ void dma_row16(const void* g, lds_ptr_t l) {
-  const int base = __builtin_amdgcn_readfirstlane((int)(uintptr_t)l);
-  int saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(g), "s"(base)
-      : "memory");
-}
 
 // Waits until at most N vector-memory operations of this wavefront are in
 // flight (N <= 63).
@@ -466,7 +444,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(GemvParams p) {
   for (int u0 = wave * WAVE; u0 < slots; u0 += NT) {
     const int u = u0 + lane;
     if (u < slots)  // inactive lanes write nothing
-      dma_row16(x + u * 4, (lds_ptr_t)(xs + u0 * 4));
+      dma16_hidden(x + u * 4, (lds_ptr_t)(xs + u0 * 4));
   }
   __builtin_amdgcn_sched_barrier(0);  // the row's DMA is issued before the ring loads
   // 3. the ring
@@ -732,7 +710,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemvm_kernel(GemvParams p) {
     for (int u0 = wave * WAVE; u0 < slots; u0 += NT) {
       const int u = u0 + lane;
       if (u < slots)  // inactive lanes write nothing
-        dma_row16(xr + u * 4, (lds_ptr_t)(dst + u0 * 4));
+        dma16_hidden(xr + u * 4, (lds_ptr_t)(dst + u0 * 4));
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // the rows' DMA is issued before the ring loads
