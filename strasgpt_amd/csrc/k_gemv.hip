@@ -1128,8 +1128,11 @@ void gemv(const GemvParams& p, int epi, hipStream_t s) {
           !launch_v2<GEMV_RESIDUAL, 8>(p, s, 256) && !launch_v3_split<8>(p, s, 256))
         launch<1, 4, GEMV_RESIDUAL>(p, s, 4096);
       break;
-    case GEMV_QKV:
-      if (!launch_v3<GEMV_QKV, 4>(p, s, 768) && !launch_v2<GEMV_QKV, 4>(p, s, 1024))
+    case GEMV_QKV:  // the register-row form first up to K = 3072 (Llama-3.2-1B
+      // 1563 -> 1578 tok/s, MXFP4 MoE 744 -> 751, Qwen3-4B 497 -> 498), the
+      // third form above it (Mistral-Small-24B 127.7 -> 126.7 the other way)
+      if (!(p.K <= 3072 && launch_v2<GEMV_QKV, 4>(p, s, 1024)) && !launch_v3<GEMV_QKV, 4>(p, s, 768) &&
+          !launch_v2<GEMV_QKV, 4>(p, s, 1024))
         launch<1, 2, GEMV_QKV>(p, s, 2048);
       break;
     case GEMV_SWIGLU:  // gate/up: the third form pays from K > 4096, with 4
