@@ -99,6 +99,20 @@ __device__ __forceinline__ void dma16_hidden(const void* g, __attribute__((addre
       : "memory");
 }
 
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+
+// (a, b) -> packed bf16 hi pair and lo pair: hi = bf16(x) (round to nearest
+// even, v_cvt_pk_bf16_f32), lo = bf16(x - hi) with x - hi exact in fp32.
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const bf16x2v h = __builtin_convertvector((f32x2v){a, b}, bf16x2v);
+  const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+  const float ra = a - __builtin_bit_cast(float, hb << 16);
+  const float rb = b - __builtin_bit_cast(float, hb & 0xffff0000u);
+  hi = hb;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){ra, rb}, bf16x2v));
+}
+
 // 128-bit non-temporal load from global memory (global, not flat,
 // instructions whatever the compiler knows of where `p` came from).
 __device__ __forceinline__ uint4 load_nt_u4(const void* p) {

@@ -245,19 +245,6 @@ __device__ __forceinline__ float dpp_ror8(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));  // row_ror:8
 }
 
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-typedef float f32x2v __attribute__((ext_vector_type(2)));
-
-// (a, b) -> packed bf16 hi pair and lo pair: hi = bf16(x) (round to nearest
-// even, v_cvt_pk_bf16_f32), lo = bf16(x - hi) with x - hi exact in fp32.
-__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const bf16x2v h = __builtin_convertvector((f32x2v){a, b}, bf16x2v);
-  const uint32_t hb = __builtin_bit_cast(uint32_t, h);
-  const float ra = a - __builtin_bit_cast(float, hb << 16);
-  const float rb = b - __builtin_bit_cast(float, hb & 0xffff0000u);
-  hi = hb;
-  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){ra, rb}, bf16x2v));
-}
 
 template <int HD>
 struct X3Lds {

@@ -260,12 +260,15 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
 // wavefront (the row, the norm weights, the lane's rotation) issued before
 // the first is used: the loop form waits a memory latency per step (row,
 // then weights, then rotation). Same arithmetic in the same order.
+// PLANES: a key head's wavefront also writes its finished key and the
+// value row of position P into the attention operand planes (hi/lo bf16
+// parts, as split_rows_kernel), for short prompts in place of that launch.
 constexpr int kQkrHeads = 4;
-template <int HD>
+template <int HD, bool PLANES>
 __global__ __launch_bounds__(kQkrHeads * WAVE) void qk_norm_rope_hd_kernel(
     float* q, int q_heads, int heads, float* kcache, int ctx, const int* pos, const uint16_t* qn,
     const uint16_t* kn, float eps, const float* rope, int pair_bound, int pair_offset, int pair_stride,
-    const float* kstage) {
+    const float* kstage, PlaneRows pl) {
 #pragma clang fp contract(off)
   constexpr int PER = (HD + WAVE - 1) / WAVE;
   __shared__ float vsh[kQkrHeads][HD];
@@ -288,12 +291,21 @@ __global__ __launch_bounds__(kQkrHeads * WAVE) void qk_norm_rope_hd_kernel(
     src = staged ? kstage + ((size_t)t * (heads - q_heads) + kh) * HD : row;
     nw = kn;
   }
-  float xv[PER], wv[PER];
+  float xv[PER], wv[PER], vv[PER];
 #pragma unroll
   for (int i = 0; i < PER; i++) {
     const int e = lane + i * WAVE;
     xv[i] = e < HD ? src[e] : 0.0f;
     wv[i] = nw && e < HD ? bf16_to_f32(nw[e]) : 1.0f;
+  }
+  const int kh = head - q_heads;
+  if (PLANES && head >= q_heads) {  // the value row of position P
+    const size_t at = ((size_t)kh * ctx + P) * HD;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int e = min(lane + i * WAVE, HD - 1);
+      vv[i] = pl.kv_bf16 ? bf16_to_f32(((const uint16_t*)pl.vcache)[at + e]) : ((const float*)pl.vcache)[at + e];
+    }
   }
   const int h = lane * pair_stride;
   const bool pair = h < pair_bound;
@@ -324,7 +336,7 @@ __global__ __launch_bounds__(kQkrHeads * WAVE) void qk_norm_rope_hd_kernel(
       row[h] = r0;
       row[h + pair_offset] = r1;
     }
-    return;
+    if (!PLANES || head < q_heads) return;
   }
   // staged key: rotate in LDS, then store every element rounded
   __builtin_amdgcn_wave_barrier();
@@ -335,10 +347,29 @@ __global__ __launch_bounds__(kQkrHeads * WAVE) void qk_norm_rope_hd_kernel(
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   uint16_t* row16 = (uint16_t*)kcache + ((size_t)(head - q_heads) * ctx + P) * HD;
+  const size_t kat = ((size_t)kh * ctx + P) * HD, vat = (size_t)kh * HD * pl.ctx_pad + P;
 #pragma unroll
   for (int i = 0; i < PER; i++) {
     const int e = lane + i * WAVE;
-    if (e < HD) row16[e] = f32_to_bf16_any(v[e]);
+    if (e < HD) {
+      // the key as the cache holds it (rounded to bf16 when staged), split
+      uint32_t hk, lk, hv, lv;
+      if (staged) {
+        const uint16_t b = f32_to_bf16_any(v[e]);
+        row16[e] = b;
+        hk = b;
+        lk = 0u;
+      } else {
+        split2(v[e], 0.0f, hk, lk);
+      }
+      if (PLANES) {
+        split2(vv[i], 0.0f, hv, lv);  // (exact hi, zero lo for a bf16 value)
+        pl.khi[kat + e] = (uint16_t)hk;
+        pl.klo[kat + e] = (uint16_t)lk;
+        pl.vthi[vat + (size_t)e * pl.ctx_pad] = (uint16_t)hv;
+        pl.vtlo[vat + (size_t)e * pl.ctx_pad] = (uint16_t)lv;
+      }
+    }
   }
 }
 
@@ -455,10 +486,14 @@ void residual_norm(const NormParams& p, hipStream_t s) {
   HIP_CHECK(hipGetLastError());
 }
 
-void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T, const int* pos,
+bool qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T, const int* pos,
                   int ctx, int hd, const uint16_t* qn, const uint16_t* kn, float eps,
                   const float* rope, int pair_bound, int pair_offset, int pair_stride,
-                  const float* kstage, hipStream_t s) {
+                  const float* kstage, const PlaneRows* planes, hipStream_t s) {
+  if (planes && (!planes->khi || !planes->klo || !planes->vthi || !planes->vtlo || !planes->vcache ||
+                 planes->ctx_pad < ctx || planes->kv_bf16 != (kstage != nullptr)))
+    ST_DIE("qk_norm_rope: inconsistent plane rows");
+  const PlaneRows pl = planes ? *planes : PlaneRows{};
   if (hd > 512 || hd % 2) ST_DIE("head_dim must be even and at most 512");
   if (pair_stride < 1 || pair_bound - pair_stride + pair_offset >= hd)
     ST_DIE("inconsistent RoPE pair geometry");
@@ -468,11 +503,16 @@ void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T, con
     switch (hd) {
 #define QKR_CASE(HD)                                                                                        \
   case HD:                                                                                                 \
-    hipLaunchKernelGGL(qk_norm_rope_hd_kernel<HD>, g4, dim3(kQkrHeads * WAVE), 0, s, q, q_heads,             \
-                       q_heads + kv_heads, kcache, ctx, pos, qn, kn, eps, rope, pair_bound, pair_offset,    \
-                       pair_stride, kstage);                                                              \
+    if (planes)                                                                                           \
+      hipLaunchKernelGGL((qk_norm_rope_hd_kernel<HD, true>), g4, dim3(kQkrHeads * WAVE), 0, s, q, q_heads, \
+                         q_heads + kv_heads, kcache, ctx, pos, qn, kn, eps, rope, pair_bound, pair_offset,  \
+                         pair_stride, kstage, pl);                                                        \
+    else                                                                                                  \
+      hipLaunchKernelGGL((qk_norm_rope_hd_kernel<HD, false>), g4, dim3(kQkrHeads * WAVE), 0, s, q, q_heads, \
+                         q_heads + kv_heads, kcache, ctx, pos, qn, kn, eps, rope, pair_bound, pair_offset,  \
+                         pair_stride, kstage, pl);                                                        \
     HIP_CHECK(hipGetLastError());                                                                         \
-    return;
+    return planes != nullptr;
       QKR_CASE(16)
       QKR_CASE(32)
       QKR_CASE(64)
@@ -484,6 +524,7 @@ void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T, con
   hipLaunchKernelGGL(qk_norm_rope_kernel, grid, dim3(64), 0, s, q, q_heads, kcache, ctx, hd, pos, qn, kn, eps,
                      rope, pair_bound, pair_offset, pair_stride, kstage);
   HIP_CHECK(hipGetLastError());
+  return false;
 }
 
 int argmax_blocks() { return kArgmaxBlocks; }

@@ -204,11 +204,23 @@ void residual_norm(const NormParams& p, hipStream_t s);
 // q ([T][heads*hd]) and on the T new key rows of one layer's k-cache. With
 // a bf16 cache (kstage given) the raw keys come from kstage [T][kv_heads*hd]
 // and the results are stored rounded into the bf16 cache.
-void qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T,
+// The bf16 planes of the attention kernels' key/value operands: K [kv][ctx]
+// [hd] hi/lo, V^T [kv][hd][ctx_pad] hi/lo, filled from the cache rows (the
+// values from vcache: fp32, or bf16 with kv_bf16).
+struct PlaneRows {
+  uint16_t *khi, *klo, *vthi, *vtlo;
+  const void* vcache;
+  int ctx_pad, kv_bf16;
+};
+
+// With planes: also writes rows P .. P + T - 1 of the planes (the finished
+// keys, the values) as attention_split_rows would; returns false where the
+// head size takes the loop form, which writes no planes.
+bool qk_norm_rope(float* q, int q_heads, float* kcache, int kv_heads, int T,
                   const int* pos, int ctx, int hd, const uint16_t* qn,
                   const uint16_t* kn, float eps, const float* rope,
                   int pair_bound, int pair_offset, int pair_stride, const float* kstage,
-                  hipStream_t s);
+                  const PlaneRows* planes, hipStream_t s);
 
 // ---------------------------------------------------------- attention --
 struct AttnParams {

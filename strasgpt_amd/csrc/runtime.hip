@@ -712,7 +712,7 @@ void layer_prefill(Dev* D, int l, int T, const uint16_t* next_norm) {
     sg::qk_norm_rope(D->q, D->qh, kc, D->kvh, T, D->pos, D->ctx, D->hd,
                      D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr,
                      D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
-                     D->po, D->pst, D->kv_bf16 ? D->kstage : nullptr, s);
+                     D->po, D->pst, D->kv_bf16 ? D->kstage : nullptr, nullptr, s);
   }
   // this chunk's cache rows into the bf16 planes (from a multiple of 32;
   // decode steps write their rows into the planes themselves)
@@ -836,16 +836,22 @@ void layer_prefill_rows(Dev* D, int l, int T) {
     Prof pr(D, K_QKV_GEMM, (double)D->qkv_rows * d * 2, 2.0 * M * D->qkv_rows * d);
     need(sg::gemv_rows(g, sg::GEMV_QKV, s));
   }
-  {
-    Prof pr(D, K_ELEM, 2.0 * M * (D->qd + D->kvd) * 4, 0);
-    sg::qk_norm_rope(D->q, D->qh, kc, D->kvh, T, D->pos, D->ctx, D->hd,
-                     D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr,
-                     D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
-                     D->po, D->pst, D->kv_bf16 ? D->kstage : nullptr, s);
-  }
+  // the prompt's cache rows go into the bf16 planes with the keys' norm and
+  // rotation (rows before P0 are there already: earlier chunks and decode
+  // steps write theirs), else, where that kernel cannot, by split_rows
   const size_t P0 = D->host_pos;
   const size_t vt_layer = (size_t)D->kvh * D->hd * D->ctx_pad;
+  bool planes_done;
   {
+    Prof pr(D, K_ELEM, 2.0 * M * (D->qd + D->kvd) * 4, 0);
+    const sg::PlaneRows pl{D->kp_hi + l * cache_layer, D->kp_lo + l * cache_layer, D->vt_hi + l * vt_layer,
+                           D->vt_lo + l * vt_layer, vc, D->ctx_pad, D->kv_bf16};
+    planes_done = sg::qk_norm_rope(D->q, D->qh, kc, D->kvh, T, D->pos, D->ctx, D->hd,
+                                   D->qk_norm ? W16(D, W_Q_NORM, l) : nullptr,
+                                   D->qk_norm ? W16(D, W_K_NORM, l) : nullptr, D->eps, D->rope, D->pb,
+                                   D->po, D->pst, D->kv_bf16 ? D->kstage : nullptr, &pl, s);
+  }
+  if (!planes_done) {
     const int r0 = (int)(P0 / 32 * 32), r1 = (int)(P0 + T);
     Prof pr(D, K_ELEM, 2.0 * (r1 - r0) * D->kvd * 4 * 2, 0);
     sg::attention_split_rows(kc, vc, D->kp_hi + l * cache_layer, D->kp_lo + l * cache_layer,
