@@ -3,7 +3,8 @@
  *
  * A CPU (C + OpenMP) restatement of the StrasGPT reference forward pass,
  * used only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
- * leg, as the checker of the HIP library and as the timed CPU baseline.
+ * leg, as the reference the HIP library's results are compared against and
+ * as the timed CPU baseline.
  * The product (strasgpt_amd/) never links, loads or calls it.
  *
  * Every function restates one piece of the reference and cites it; the
