@@ -189,6 +189,48 @@ def test_prefill_rows_form(name, kv, model_dir, monkeypatch):
         assert float(np.abs(got["1"] - got["0"]).max()) <= 2e-3
 
 
+_LONG_CUTS = [0, 7, 8, 16, 21, 29, 30, 36, 40]
+
+
+@pytest.mark.parametrize("name,kv,cuts", [("tiny-chunk", "fp32", _LONG_CUTS), ("small-m", "bf16", _LONG_CUTS),
+                                          ("tiny-rope-il128", "fp32", _LONG_CUTS),
+                                          ("tiny-qwen", "bf16", [0, 5, 6, 11, 19])])
+def test_prefill_rows_continued(name, kv, cuts, model_dir, monkeypatch):
+    """A prompt fed in pieces of 1 to 8 tokens across calls, over position
+    32 where the context allows: pieces of 2 to 8 tokens take the multi-row
+    GEMVs, whose QK-norm / RoPE kernel writes the new key and value rows
+    into the attention operand planes (rows before the piece come from
+    earlier calls; single tokens take the decode step, which writes its own
+    row). Logits after every call against the oracle fed the same pieces
+    (head_dim 32 and 128, interleaved RoPE, QK-norm with the staged bf16
+    keys on tiny-qwen, fp32 and bf16 caches), and the last logits against
+    the same pieces through the GEMM path (STRASGPT_PREFILL_ROWS=0, planes
+    by split_rows)."""
+    from oracle import oracle as orc
+    rt = runtime()
+    d = model_dir(name)
+    shp = synth.shape(name)
+    prompt = synth.prompt_tokens(shp.vocab, cuts[-1], 77)
+    pieces = [prompt[a:b] for a, b in zip(cuts[:-1], cuts[1:])]
+    om = orc.OracleModel(d, threads=16, kv_format=orc.KV_BF16 if kv == "bf16" else orc.KV_F32)
+    last = {}
+    for form in ("1", "0"):
+        monkeypatch.setenv("STRASGPT_PREFILL_ROWS", form)
+        om.reset()
+        with rt.Transformer(d) as t:
+            if kv == "bf16":
+                t.set_kv_cache_format(rt.KV_BF16)
+            for i, piece in enumerate(pieces):
+                gl = t.predict(piece)
+                ol = om.predict(piece)
+                err = float(np.abs(gl - ol).max())
+                log(f"{name} kv {kv} form {form} piece {i} ({len(piece)} tokens at {cuts[i]}): "
+                    f"max |logit error| {err:.3g}")
+                np.testing.assert_allclose(gl, ol, rtol=RTOL, atol=ATOL)
+            last[form] = gl
+    assert float(np.abs(last["1"] - last["0"]).max()) <= 2e-3
+
+
 @pytest.mark.parametrize("kernel", ["x3", "x3-16", "x3-32", "fp32"])
 @pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen", "tiny-chunk"])
 def test_prefill_attention_kernels(name, kernel, model_dir, monkeypatch):
