@@ -9,17 +9,10 @@ namespace sg {
 namespace {
 
 // Reference source/transformer.c:1247-1255: x[t][e] = bf16 -> f32 of the
-// token's embedding row (exact).
-__global__ __launch_bounds__(256) void embed_kernel(const int* tok, const uint16_t* table,
-                                                    int d, float* x) {
-  const int t = blockIdx.x;
-  const uint16_t* row = table + (size_t)tok[t] * d;
-  for (int e = threadIdx.x; e < d; e += blockDim.x) x[(size_t)t * d + e] = bf16_to_f32(row[e]);
-}
-
-// The same with one 16-byte load (8 values) per thread, grid (T, d / 2048
-// rounded up): one memory latency per row, where the loop above waits one
-// per 256 values of a row (a decode step's single row: 10.9 us at d = 5120).
+// token's embedding row (exact). One 16-byte load (8 values) per thread,
+// grid (T, d / 2048 rounded up): one memory latency per row (a block-strided
+// loop over the row waited one per 256 values: 10.9 against 2.9 us for a
+// decode step's row at d = 5120).
 __global__ __launch_bounds__(256) void embed8_kernel(const int* tok, const uint16_t* table, int d, float* x) {
   const int t = blockIdx.x, e = (blockIdx.y * 256 + threadIdx.x) * 8;
   if (e >= d) return;
@@ -452,10 +445,9 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(ArgmaxParams p, int p
 
 void embed(const int* tok, int T, const uint16_t* table, int d, float* x, hipStream_t s) {
   if (T <= 0) ST_DIE("embed needs T > 0");
-  if (d % 8 == 0 && (uintptr_t)table % 16 == 0 && (uintptr_t)x % 16 == 0)
-    hipLaunchKernelGGL(embed8_kernel, dim3(T, (d + 2047) / 2048), dim3(256), 0, s, tok, table, d, x);
-  else
-    hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, s, tok, table, d, x);
+  if (d % 8 || (uintptr_t)table % 16 || (uintptr_t)x % 16)
+    ST_DIE("embed needs d % 8 == 0 and 16-byte aligned rows (as every GEMV does)");
+  hipLaunchKernelGGL(embed8_kernel, dim3(T, (d + 2047) / 2048), dim3(256), 0, s, tok, table, d, x);
   HIP_CHECK(hipGetLastError());
 }
 
