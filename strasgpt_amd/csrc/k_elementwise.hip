@@ -331,7 +331,8 @@ __global__ __launch_bounds__(kQkrHeads * WAVE) void qk_norm_rope_hd_kernel(
     }
     if (!PLANES || head < q_heads) return;
   }
-  // staged key: rotate in LDS, then store every element rounded
+  // a staged key (stored rounded) or a key with plane rows: the rotated row
+  // in LDS, then every element
   __builtin_amdgcn_wave_barrier();
   if (pair) {
     v[h] = r0;
